@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MoE block (BASELINE.json metric).
+
+One step = forward + backward of the MoE feed-forward block on the c3
+workload: T=32768 tokens, d=1024, E=16 experts, top-4, expert hidden h=4096,
+bf16 with fp32 accumulation, router logits skewed by a Zipf(1.1) per-expert
+bias (max expert load ~4x the mean), loss = <dY, Y> + 0.1*aux + 1e-3*z.
+Inputs are synthetic (seed 1234) and resident in HBM before timing starts.
+
+Prints one JSON line: tokens/s, ms/step, the fraction of bf16 MFMA peak of
+the whole step, a per-kernel breakdown timed live with HIP events on the
+launch stream, the roofline of the dominant kernel, decode latency at
+T = 1/8/64 on the same weights, and the CPU oracle timed on this host's cores
+on a bounded token slice of the same workload.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "test-model-thing-cuda_amd"))
+
+METRIC = "MoE fwd+bwd tokens/s (E16 top4 d1024 bf16), % MFMA peak; decode µs/step"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def kernel_work(phase, T, d, E, K, h):
+    """Algorithmic work per launch: ('mfma', flops) or ('hbm', bytes)."""
+    TK = T * K
+    hn = h if h > 0 else d
+    w = {
+        "gemm_up": ("mfma", 2 * TK * d * hn),
+        "gemm_down": ("mfma", 2 * TK * h * d),
+        "gemm_dact": ("mfma", 2 * TK * d * h),
+        "gemm_dw_down": ("mfma", 2 * TK * d * h),
+        "gemm_dw_up": ("mfma", 2 * TK * hn * d),
+        "gemm_dx": ("mfma", 2 * TK * hn * d),
+        # X, Wr read; logits + probs, idx + gate, lse written
+        "router": ("hbm", 2 * T * d + 2 * E * d + 8 * T * E + 8 * TK + 4 * T),
+        # idx read; perm + slot_of written (plus block bases, negligible)
+        "permute": ("hbm", 4 * TK + 8 * TK),
+        "scan": ("hbm", 0),
+        # expert outputs gathered, residual read + written, gates and slots
+        "combine": ("hbm", 2 * TK * d + 4 * T * d + 8 * TK),
+        # dY, outputs read, dO written, probs/logit statistics, dlogits
+        "combine_bwd": ("hbm", 2 * T * d + 4 * TK * d + 8 * TK + 8 * T * E),
+        "router_dw": ("hbm", 2 * T * d + 4 * T * E + 4 * E * d),
+        "scatter": ("hbm", 2 * TK * d + 2 * T * d + 4 * T * E + 4 * TK),
+    }
+    return w.get(phase, ("hbm", 0))
+
+
+def step_flops(T, d, E, K, h):
+    fwd = 2 * T * d * E + (4 * T * K * d * h if h > 0 else 2 * T * K * d * d)
+    bwd = 2 * (4 * T * K * d * h) + 4 * T * d * E if h > 0 else 2 * (2 * T * K * d * d) + 4 * T * d * E
+    return fwd, bwd
+
+
+def cpu_baseline(case, cfg, target_s=15.0, max_threads=16):
+    """CPU oracle (test infrastructure) on a bounded token slice of the same
+    workload, timed on this host. Returns the cpu_baseline object."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import moe_oracle  # cpu_baseline leg only
+    threads = max(1, min(max_threads, os.cpu_count() or 1))
+    K, h = cfg["K"], cfg["h"]
+
+    def run(ts):
+        t0 = time.perf_counter()
+        moe_oracle.backward(case["X"][:ts], case["Wr"], case["W_up"], case["W_down"], case["dY"][:ts],
+                            K, h, bias=case.get("bias"), aux_coef=cfg.get("aux", 0.0),
+                            z_coef=cfg.get("z", 0.0), threads=threads)
+        return time.perf_counter() - t0
+
+    t_small = run(64)
+    ts = int(max(64, min(8192, 64 * target_s / max(t_small, 1e-3))))
+    ts -= ts % 64
+    dt = run(ts)
+    return {"value": round(ts / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle fwd+bwd (recomputes the forward) on the first {ts} tokens of the c3 "
+                      f"workload with all 16 experts, {dt:.1f} s wall, fp32 C++ on {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c3")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-profile", action="store_true",
+                    help="time the step without per-kernel events")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import tmt_moe
+    from synthetic import CONFIGS, make_case
+
+    cfg = CONFIGS[args.config]
+    T, d, E, K, h = (cfg[k] for k in ("T", "d", "E", "K", "h"))
+    hn = h if h > 0 else d
+    torch.cuda.set_device(0)
+    case = make_case(**cfg)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+    X, Wr, Wu, dY = (dev(case[k]) for k in ("X", "Wr", "W_up", "dY"))
+    Wd = dev(case["W_down"]) if h > 0 else None
+    bias = torch.from_numpy(case["bias"]).cuda() if case.get("bias") is not None else None
+    Y = torch.zeros(T, d, dtype=torch.bfloat16, device="cuda")
+    dX = torch.empty_like(X)
+    dWr = torch.empty(E, d, dtype=torch.float32, device="cuda")
+    dWu = torch.empty(E, hn, d, dtype=torch.float32, device="cuda")
+    dWd = torch.empty(E, d, h, dtype=torch.float32, device="cuda") if h > 0 else None
+    aux_c, z_c = cfg.get("aux", 0.0), cfg.get("z", 0.0)
+    m = tmt_moe.MoE(T, d, E, K, h)
+
+    def step():
+        m.forward(X, Wr, Wu, Wd, Y, beta=1.0, bias=bias)
+        m.backward(dY, X, Wr, Wu, Wd, dX, dWr, dWu, dWd, aux_c, z_c)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    m.set_profiling(not args.no_profile)
+    m.profile(reset=True)
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    prof = m.profile(reset=True)
+    m.set_profiling(False)
+    aux, z, counts = m.stats()
+
+    fwd_f, bwd_f = step_flops(T, d, E, K, h)
+    kernels = {}
+    for ph, (tot_ms, n) in prof.items():
+        if n == 0:
+            continue
+        avg = tot_ms / n
+        kind, work = kernel_work(ph, T, d, E, K, h)
+        k = {"avg_ms": round(avg, 4), "launches_per_step": n / args.steps,
+             "share": round(tot_ms / args.steps / ms_step, 4)}
+        if kind == "mfma":
+            k["tflops"] = round(work / avg / 1e9, 1)
+            k["mfma_frac"] = round(work / avg / 1e9 / PEAK_BF16_TFLOPS, 4)
+        elif work:
+            k["gbs"] = round(work / avg / 1e6, 1)
+            k["hbm_frac"] = round(work / avg / 1e6 / PEAK_HBM_GBS, 4)
+        kernels[ph] = k
+    roofline = None
+    if kernels:
+        dom = max(kernels, key=lambda p: kernels[p]["avg_ms"] * kernels[p]["launches_per_step"])
+        kind, work = kernel_work(dom, T, d, E, K, h)
+        avg = kernels[dom]["avg_ms"]
+        if kind == "mfma":
+            ach = work / avg / 1e9
+            roofline = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1),
+                        "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                        "work_per_launch": f"{work / 1e9:.1f} GFLOP = 2*T*K*d*h"}
+        else:
+            ach = work / avg / 1e6
+            roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1),
+                        "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                        "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None}
+
+    decode = None
+    if not args.no_decode and args.config == "c3":
+        decode = {}
+        md = tmt_moe.MoE(64, d, E, K, h)
+        for td in (1, 8, 64):
+            Xd = X[:td].contiguous()
+            Yd = torch.zeros(td, d, dtype=torch.bfloat16, device="cuda")
+            for _ in range(10):
+                md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 100
+            e0.record(stream)
+            for _ in range(reps):
+                md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / reps * 1000
+            routed = md.routing()
+            distinct = int(np.unique(routed["idx"]).size)
+            wbytes = distinct * 2 * d * h * 2 + E * d * 2
+            decode[f"T{td}"] = {"us_per_step": round(us, 2), "distinct_experts": distinct,
+                                "weight_bytes": wbytes,
+                                "hbm_gbs": round(wbytes / (us * 1e-6) / 1e9, 1)}
+        md.close()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(case, cfg)
+
+    tokens_s = T / (ms_step / 1e3)
+    out = {
+        "metric": METRIC,
+        "value": round(tokens_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seed 1234, N(0,1) activations, N(0,1/sqrt(fan_in)) weights, Zipf(1.1) router bias)",
+        "config": {"workload": f"{args.config}: MoE fwd+bwd T={T} d={d} E={E} top-{K} h={h}"
+                               + (f" Zipf(1.1) skew {counts.max() / counts.mean():.2f}x" if E > 1 else ""),
+                   "T": T, "d": d, "E": E, "K": K, "h": h, "aux": aux_c, "z": z_c,
+                   "parallelism": "single GPU"},
+        "mfma_frac_step": round((fwd_f + bwd_f) / (ms_step / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "step_tflop": round((fwd_f + bwd_f) / 1e12, 3),
+        "wall_s_timed": round(wall, 3),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": kernels,
+        "decode": decode,
+        "aux": round(aux, 6),
+        "z": round(z, 6),
+    }
+    m.close()
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

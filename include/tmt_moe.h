@@ -1,0 +1,168 @@
+/*
+ * tmt_moe.h -- C ABI of the MI355X (gfx950) Mixture-of-Experts block.
+ *
+ * Drop-in for the MoE layer of TMT (reference tree, tmt-cuda/src/moe.cu):
+ *   softmax router + top-k (ties -> lower expert index) + renormalised gates,
+ *   Switch load-balancing aux loss and router z-loss with analytic gradients,
+ *   SiLU experts, residual add (Y = beta*Y + MoE(X)).
+ *
+ * Two expert shapes:
+ *   hidden == 0  reference experts: one linear W_e [d][d] per expert and
+ *                SiLU applied in combine (moe.cu:142-158, 431-436).
+ *   hidden  > 0  up/down experts: O = silu(X W_up^T) W_down^T with
+ *                W_up [h][d] and W_down [d][h].
+ * experts == 1 is the reference's dense path without a router
+ * (moe.cu:397-403): Y = beta*Y + silu(X W_0^T) (hidden == 0).
+ *
+ * Layout: all matrices row-major, weights [out][in] like nn.Linear
+ * (linalg.cu:1-8). bf16 values are raw uint16 bit patterns. Per-expert
+ * weights are passed as host arrays of E device pointers, the reference's
+ * `bf16** Wexp` convention (moe.cu:374). All device pointers must be 16-byte
+ * aligned. d and hidden must be multiples of 128.
+ *
+ * Every function returns TMT_MOE_OK (0) or a negative error code and never
+ * exits the process; tmt_moe_last_error() gives a thread-local message.
+ * Forward and backward enqueue work on the given stream (hipStream_t passed
+ * as void*; NULL = default stream) and never synchronise with the host.
+ * A handle is single-layer state (the reference's MoeKeep + MoeWs,
+ * moe.cu:294-328): forward saves routing for the following backward.
+ * Calls on one handle must be ordered by the caller; different handles are
+ * independent.
+ */
+#ifndef TMT_MOE_H
+#define TMT_MOE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    TMT_MOE_OK = 0,
+    TMT_MOE_EINVAL = -1,   /* bad argument, shape or alignment */
+    TMT_MOE_ENOMEM = -2,   /* device allocation failed */
+    TMT_MOE_EDEVICE = -3,  /* HIP runtime or launch error */
+    TMT_MOE_ESTATE = -4    /* backward without a matching forward */
+};
+
+enum { TMT_MOE_WEIGHTS_BF16 = 0, TMT_MOE_WEIGHTS_MXFP4 = 1 };
+
+typedef struct tmt_moe_desc {
+    int32_t max_tokens;     /* T_max: largest T a call may pass */
+    int32_t d;              /* model width (multiple of 128) */
+    int32_t experts;        /* E, 1..64 */
+    int32_t topk;           /* K, 1..min(E, 8) */
+    int32_t hidden;         /* h (multiple of 128), or 0 for reference experts */
+    int32_t weight_format;  /* TMT_MOE_WEIGHTS_* */
+} tmt_moe_desc;
+
+typedef struct tmt_moe tmt_moe;
+
+/* Replaces moe_keep_alloc + moe_ws_alloc (moe.cu:330-362): one device arena
+ * sized from the descriptor; no allocation happens after this call. */
+int tmt_moe_create(const tmt_moe_desc* desc, tmt_moe** out);
+/* Replaces moe_keep_free + moe_ws_free (moe.cu:342-348, 363-370). */
+int tmt_moe_destroy(tmt_moe* moe);
+/* Arena bytes tmt_moe_create would allocate for this descriptor. */
+int tmt_moe_workspace_size(const tmt_moe_desc* desc, size_t* bytes);
+
+/*
+ * Replaces moe_forward (moe.cu:374-466).
+ *   X [T][d] bf16, Wr [E][d] bf16 (ignored when E == 1),
+ *   logit_bias [E] fp32 device pointer or NULL (added to the router logits;
+ *   NULL gives the reference's bias-free router, moe.cu:10-38),
+ *   W_up[E]  -> [h][d] bf16   (hidden > 0)  or W_e [d][d] (hidden == 0),
+ *   W_down[E]-> [d][h] bf16   (hidden > 0; NULL allowed when hidden == 0),
+ *   Y [T][d] bf16 is read-modify-write: Y = beta*Y + MoE(X).
+ * Unlike the reference there is no host synchronisation: counts, offsets
+ * and the expert tile table stay on the device. The reference's returned
+ * aux value and k.zloss are read with tmt_moe_read_stats.
+ */
+int tmt_moe_forward(tmt_moe* moe, void* stream, int32_t T, const uint16_t* X,
+                    const uint16_t* Wr, const float* logit_bias,
+                    const uint16_t* const* W_up, const uint16_t* const* W_down,
+                    uint16_t* Y, float beta);
+
+/*
+ * MXFP4 variant of tmt_moe_forward for weight_format == TMT_MOE_WEIGHTS_MXFP4
+ * (no reference counterpart: the reference has no FP4 path).
+ * W_up[e]: packed e2m1 [h][d/2] bytes (low nibble = even column) with
+ * W_up_scale[e]: e8m0 [h][d/32]; W_down[e]: [d][h/2] with scales [d][h/32].
+ */
+int tmt_moe_forward_mxfp4(tmt_moe* moe, void* stream, int32_t T,
+                          const uint16_t* X, const uint16_t* Wr,
+                          const float* logit_bias,
+                          const uint8_t* const* W_up, const uint8_t* const* W_up_scale,
+                          const uint8_t* const* W_down, const uint8_t* const* W_down_scale,
+                          uint16_t* Y, float beta);
+
+/*
+ * Replaces moe_backward (moe.cu:479-545) for the loss
+ *   L = <dY, Y> + aux_coef * aux + z_coef * z
+ * (aux_coef / z_coef already divided by the layer count, model.cu:677).
+ * X is the forward input (the reference keeps a copy in MoeKeep::H,
+ * moe.cu:396; here the caller passes it again). Outputs are overwritten:
+ *   dX [T][d] bf16, dWr [E][d] fp32 (may be NULL when E == 1),
+ *   dW_up[E] -> [h][d] fp32 (or [d][d] when hidden == 0),
+ *   dW_down[E] -> [d][h] fp32 (hidden > 0).
+ * Experts that received no tokens get all-zero gradients (the reference
+ * leaves them untouched, moe.cu:534-535).
+ */
+int tmt_moe_backward(tmt_moe* moe, void* stream, const uint16_t* dY,
+                     const uint16_t* X, const uint16_t* Wr,
+                     const uint16_t* const* W_up, const uint16_t* const* W_down,
+                     float aux_coef, float z_coef, uint16_t* dX, float* dWr,
+                     float* const* dW_up, float* const* dW_down);
+
+/*
+ * Replaces the host read of the router statistics (moe.cu:448-465 and
+ * moe_aux_from, moe.cu:470-475). Waits for `stream`, then writes the Switch
+ * aux loss E*sum_e(mean_p_e*frac_e), the z-loss mean(lse^2) and the
+ * per-expert token counts [E] (the reference's hcnt, capi.cu:131-136) of the
+ * last forward. Any output pointer may be NULL.
+ */
+int tmt_moe_read_stats(tmt_moe* moe, void* stream, float* aux, float* z,
+                       int32_t* counts);
+
+/* Device address of the last forward's statistics: float {aux, z} followed
+ * by E int32 counts. Lets a caller batch the read of many layers, like the
+ * reference's deferred k.stat slot (moe.cu:311-314, model.cu:542-549). */
+int tmt_moe_stats_device_ptr(tmt_moe* moe, const void** ptr);
+
+/*
+ * Parity/debug: waits for `stream` and copies the last forward's routing to
+ * host memory. Any pointer may be NULL. Shapes: logits, probs [T][E] fp32;
+ * idx [T][K] int32; gate [T][K] fp32 (renormalised weights);
+ * offsets [E+1] int32 (expert segment starts); perm [T*K] int32 (token of
+ * each slot, stable: ascending token inside a segment); slot_of [T][K].
+ */
+int tmt_moe_read_routing(tmt_moe* moe, void* stream, float* logits,
+                         float* probs, int32_t* idx, float* gate,
+                         int32_t* offsets, int32_t* perm, int32_t* slot_of);
+
+/*
+ * Per-kernel timing, the counterpart of the reference's TMT_PROFILE phase
+ * timers (moe.cu:380-394, 459-464), but with HIP events on the call's stream
+ * instead of device-wide synchronisation. While enabled, every kernel launch
+ * of forward/backward is bracketed by two events. tmt_moe_read_profile waits
+ * for the recorded events and returns, per phase, the summed milliseconds and
+ * the number of launches since the last reset (arrays of TMT_MOE_NPHASES).
+ */
+enum {
+    TMT_MOE_PH_ROUTER = 0, TMT_MOE_PH_SCAN, TMT_MOE_PH_PERMUTE, TMT_MOE_PH_GEMM_UP,
+    TMT_MOE_PH_GEMM_DOWN, TMT_MOE_PH_COMBINE, TMT_MOE_PH_COMBINE_BWD, TMT_MOE_PH_GEMM_DACT,
+    TMT_MOE_PH_GEMM_DW_DOWN, TMT_MOE_PH_GEMM_DW_UP, TMT_MOE_PH_GEMM_DX, TMT_MOE_PH_ROUTER_DW,
+    TMT_MOE_PH_SCATTER, TMT_MOE_NPHASES
+};
+int tmt_moe_set_profiling(tmt_moe* moe, int enable);
+int tmt_moe_read_profile(tmt_moe* moe, float* ms, int32_t* launches, int reset);
+const char* tmt_moe_phase_name(int phase);
+
+/* Thread-local message of the last failing call on this thread. */
+const char* tmt_moe_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,64 @@
+// device_util.hpp -- small gfx950 device helpers shared by the kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tmt {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// bf16 bit patterns packed two per dword: element 2i in the low half.
+__device__ __forceinline__ float bf_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+__device__ __forceinline__ float bf1(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (the conversion instruction of gfx950).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+
+// Unpack 8 bf16 held in a uint4 into fp32.
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+    f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
+    f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+    f[4] = bf_lo(v.z); f[5] = bf_hi(v.z);
+    f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
+}
+__device__ __forceinline__ uint4 pack8(const float* f) {
+    uint4 v;
+    v.x = pack_bf2(f[0], f[1]);
+    v.y = pack_bf2(f[2], f[3]);
+    v.z = pack_bf2(f[4], f[5]);
+    v.w = pack_bf2(f[6], f[7]);
+    return v;
+}
+
+// SiLU and its derivative (reference tmt-cuda/src/common.h:15-24) with the
+// hardware exp2 / reciprocal: x * sigmoid(x), g*s*(1 + x(1 - s)).
+__device__ __forceinline__ float sigmoid_fast(float x) {
+    return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
+}
+__device__ __forceinline__ float silu_fast(float x) { return x * sigmoid_fast(x); }
+__device__ __forceinline__ float dsilu_fast(float x) {
+    float s = sigmoid_fast(x);
+    return s * (1.0f + x * (1.0f - s));
+}
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
+
+__device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+__device__ __forceinline__ int shfl_xor(int v, int m) { return __shfl_xor(v, m, 64); }
+
+// Full-wave xor butterfly sum with offsets 32,16,...,1: every lane ends with
+// the same value (each step adds two equal-shaped partial trees).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + shfl_xor(v, off);
+    return v;
+}
+
+}  // namespace tmt

@@ -1,0 +1,533 @@
+// moe_api.cpp -- C ABI and host orchestration of the MI355X MoE block.
+//
+// Replaces moe_keep_alloc / moe_ws_alloc / moe_forward / moe_backward /
+// moe_aux_from of the reference (tmt-cuda/src/moe.cu:294-545). One handle
+// owns one device arena sized at creation; forward and backward only enqueue
+// kernels on the caller's stream (no allocation, no host synchronisation).
+// Errors are returned as codes with a thread-local message instead of the
+// reference's print-and-exit (tmt-cuda/src/common.h:26-33).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/tmt_moe.h"
+#include "moe_internal.hpp"
+
+using namespace tmt;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+#define HIP_TRY(call)                                                              \
+    do {                                                                           \
+        hipError_t err__ = (call);                                                 \
+        if (err__ != hipSuccess)                                                   \
+            return fail(TMT_MOE_EDEVICE, "%s failed: %s", #call, hipGetErrorString(err__)); \
+    } while (0)
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+struct Layout {
+    size_t total = 0;
+    size_t add(size_t bytes) {
+        size_t off = total;
+        total += (bytes + 255) & ~size_t(255);
+        return off;
+    }
+};
+
+}  // namespace
+
+struct tmt_moe {
+    tmt_moe_desc desc;
+    int hn = 0;        // width of the first expert GEMM (h, or d for h == 0)
+    int nblk_max = 0;  // router blocks at the largest T
+    int device = 0;
+    char* arena = nullptr;
+    size_t arena_bytes = 0;
+    // routing state (kept from forward for backward; the reference's MoeKeep)
+    float *logits, *probs, *lse, *gate, *blkstat, *stats;
+    int32_t *idx, *blkcnt, *blkbase, *counts, *offsets, *order, *perm, *slot_of;
+    // activations
+    uint16_t *U, *Aact, *O, *dO, *dU, *dXg;
+    float *dlogits, *dwr_partial;
+    int last_T = -1;
+    // per-kernel event timing (tmt_moe_set_profiling)
+    bool prof_on = false;
+    std::vector<hipEvent_t> prof_events;  // pairs: start, stop
+    std::vector<int> prof_phase;          // phase of each recorded pair
+    double prof_ms[TMT_MOE_NPHASES] = {};
+    int32_t prof_cnt[TMT_MOE_NPHASES] = {};
+};
+
+namespace {
+
+int validate_desc(const tmt_moe_desc* d) {
+    if (!d) return fail(TMT_MOE_EINVAL, "descriptor is NULL");
+    if (d->max_tokens < 1) return fail(TMT_MOE_EINVAL, "max_tokens must be >= 1");
+    if (d->d < 128 || d->d % 128 != 0) return fail(TMT_MOE_EINVAL, "d=%d must be a positive multiple of 128", d->d);
+    if (d->experts < 1 || d->experts > kMaxExperts)
+        return fail(TMT_MOE_EINVAL, "experts=%d must be in [1, %d]", d->experts, kMaxExperts);
+    if (d->topk < 1 || d->topk > d->experts || d->topk > kMaxTopK)
+        return fail(TMT_MOE_EINVAL, "require 1 <= topk <= min(experts, %d) (topk=%d)", kMaxTopK, d->topk);
+    if (d->hidden < 0 || d->hidden % 128 != 0)
+        return fail(TMT_MOE_EINVAL, "hidden=%d must be 0 or a multiple of 128", d->hidden);
+    if ((int64_t)d->experts * d->d > 32768)
+        return fail(TMT_MOE_EINVAL, "experts*d=%lld exceeds 32768 (router weights are staged in 64 KiB of LDS)",
+                    (long long)d->experts * d->d);
+    if ((int64_t)d->max_tokens * d->topk >= (1ll << 31))
+        return fail(TMT_MOE_EINVAL, "max_tokens*topk must fit in int32");
+    if (d->weight_format != TMT_MOE_WEIGHTS_BF16 && d->weight_format != TMT_MOE_WEIGHTS_MXFP4)
+        return fail(TMT_MOE_EINVAL, "unknown weight_format %d", d->weight_format);
+    if (d->weight_format == TMT_MOE_WEIGHTS_MXFP4 && d->hidden == 0)
+        return fail(TMT_MOE_EINVAL, "MXFP4 weights need hidden > 0");
+    return TMT_MOE_OK;
+}
+
+// Router rows per workgroup: 4 waves x R rows x iterations, aiming at a few
+// hundred workgroups and staying within the permutation kernel's group limit.
+int router_rows_per_block(int T, int E, int K) {
+    const int R = router_rows_per_wave(E);
+    const int base = 4 * R;
+    int iter = T / (base * 512);
+    const int rg = 64 / K;
+    int iter_max = (64 * rg) / base;
+    if (iter_max > 16) iter_max = 16;
+    if (iter > iter_max) iter = iter_max;
+    if (iter < 1) iter = 1;
+    return base * iter;
+}
+
+size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
+    const int64_t T = d->max_tokens, E = d->experts, K = d->topk, D = d->d, h = d->hidden;
+    const int64_t hn = h > 0 ? h : D;
+    const int64_t TK = T * K;
+    const int rpb_min = 4 * router_rows_per_wave((int)E);
+    const int64_t nblk = (T + rpb_min - 1) / rpb_min;
+    Layout L;
+    size_t o_logits = L.add(T * E * 4), o_probs = L.add(T * E * 4), o_lse = L.add(T * 4);
+    size_t o_gate = L.add(TK * 4), o_idx = L.add(TK * 4);
+    size_t o_blkcnt = L.add(nblk * E * 4), o_blkbase = L.add(nblk * E * 4);
+    size_t o_blkstat = L.add(nblk * (E + 1) * 4);
+    size_t o_counts = L.add(E * 4), o_offsets = L.add((E + 1) * 4), o_order = L.add(E * 4);
+    size_t o_stats = L.add((2 + E) * 4);
+    size_t o_perm = L.add(TK * 4), o_slot = L.add(TK * 4);
+    size_t o_U = L.add(TK * hn * 2);
+    size_t o_A = h > 0 ? L.add(TK * h * 2) : 0;
+    size_t o_O = h > 0 ? L.add(TK * D * 2) : 0;
+    size_t o_dO = L.add(TK * D * 2);
+    size_t o_dU = h > 0 ? L.add(TK * h * 2) : 0;
+    size_t o_dXg = L.add(TK * D * 2);
+    size_t o_dl = L.add(T * E * 4);
+    size_t o_dwr = L.add((size_t)router_dw_chunks((int)T) * E * D * 4);
+    if (m) {
+        char* a = m->arena;
+        m->logits = (float*)(a + o_logits);
+        m->probs = (float*)(a + o_probs);
+        m->lse = (float*)(a + o_lse);
+        m->gate = (float*)(a + o_gate);
+        m->idx = (int32_t*)(a + o_idx);
+        m->blkcnt = (int32_t*)(a + o_blkcnt);
+        m->blkbase = (int32_t*)(a + o_blkbase);
+        m->blkstat = (float*)(a + o_blkstat);
+        m->counts = (int32_t*)(a + o_counts);
+        m->offsets = (int32_t*)(a + o_offsets);
+        m->order = (int32_t*)(a + o_order);
+        m->stats = (float*)(a + o_stats);
+        m->perm = (int32_t*)(a + o_perm);
+        m->slot_of = (int32_t*)(a + o_slot);
+        m->U = (uint16_t*)(a + o_U);
+        m->Aact = h > 0 ? (uint16_t*)(a + o_A) : nullptr;
+        m->O = h > 0 ? (uint16_t*)(a + o_O) : nullptr;
+        m->dO = (uint16_t*)(a + o_dO);
+        m->dU = h > 0 ? (uint16_t*)(a + o_dU) : m->dO;  // h == 0: combine_bwd writes dU
+        m->dXg = (uint16_t*)(a + o_dXg);
+        m->dlogits = (float*)(a + o_dl);
+        m->dwr_partial = (float*)(a + o_dwr);
+        m->nblk_max = (int)nblk;
+    }
+    return L.total;
+}
+
+int check_device(const tmt_moe* m) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev != m->device)
+        return fail(TMT_MOE_EINVAL, "handle was created on device %d but device %d is current", m->device, dev);
+    return TMT_MOE_OK;
+}
+
+constexpr int kProfPairs = 2048;
+
+// Waits for every recorded pair and folds it into the per-phase totals.
+int prof_flush(tmt_moe* m) {
+    for (size_t i = 0; i < m->prof_phase.size(); ++i) {
+        HIP_TRY(hipEventSynchronize(m->prof_events[2 * i + 1]));
+        float ms = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&ms, m->prof_events[2 * i], m->prof_events[2 * i + 1]));
+        m->prof_ms[m->prof_phase[i]] += ms;
+        m->prof_cnt[m->prof_phase[i]] += 1;
+    }
+    m->prof_phase.clear();
+    return TMT_MOE_OK;
+}
+
+int prof_begin(tmt_moe* m, int phase, hipStream_t s, int* slot) {
+    *slot = -1;
+    if (!m->prof_on) return TMT_MOE_OK;
+    if ((int)m->prof_phase.size() == kProfPairs) {
+        int rc = prof_flush(m);
+        if (rc) return rc;
+    }
+    *slot = (int)m->prof_phase.size();
+    m->prof_phase.push_back(phase);
+    HIP_TRY(hipEventRecord(m->prof_events[2 * *slot], s));
+    return TMT_MOE_OK;
+}
+
+int prof_end(tmt_moe* m, int slot, hipStream_t s) {
+    if (slot < 0) return TMT_MOE_OK;
+    HIP_TRY(hipEventRecord(m->prof_events[2 * slot + 1], s));
+    return TMT_MOE_OK;
+}
+
+// Launch `call` (returning hipError_t) as phase `ph`, timed when profiling.
+#define LAUNCH(ph, call)                                  \
+    do {                                                  \
+        int slot__ = -1;                                  \
+        int rc__ = prof_begin(m, (ph), s, &slot__);       \
+        if (rc__) return rc__;                            \
+        HIP_TRY(call);                                    \
+        rc__ = prof_end(m, slot__, s);                    \
+        if (rc__) return rc__;                            \
+    } while (0)
+
+// Routing + dispatch: router / scan / permute (E > 1) or identity (E == 1).
+int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* Wr, const float* bias) {
+    const int E = m->desc.experts, K = m->desc.topk, d = m->desc.d;
+    if (E == 1) {
+        LAUNCH(TMT_MOE_PH_PERMUTE, launch_dense_dispatch(T, m->perm, m->slot_of, m->gate, m->counts,
+                                                        m->offsets, m->order, m->stats, s));
+        return TMT_MOE_OK;
+    }
+    const int rpb = router_rows_per_block(T, E, K);
+    const int nblk = T > 0 ? (T + rpb - 1) / rpb : 0;
+    if (nblk > m->nblk_max) return fail(TMT_MOE_EINVAL, "internal: router block count %d > %d", nblk, m->nblk_max);
+    if (nblk > 0) {
+        RouterParams rp{};
+        rp.X = X; rp.Wr = Wr; rp.bias = bias;
+        rp.T = T; rp.d = d; rp.E = E; rp.K = K; rp.rows_per_block = rpb;
+        rp.logits = m->logits; rp.probs = m->probs; rp.idx = m->idx; rp.gate = m->gate;
+        rp.lse = m->lse; rp.blkcnt = m->blkcnt; rp.blkstat = m->blkstat;
+        LAUNCH(TMT_MOE_PH_ROUTER, launch_router(rp, nblk, s));
+    }
+    ScanParams sp{};
+    sp.blkcnt = m->blkcnt; sp.blkstat = m->blkstat; sp.nblk = nblk; sp.T = T; sp.E = E; sp.K = K;
+    sp.counts = m->counts; sp.offsets = m->offsets; sp.blkbase = m->blkbase; sp.order = m->order;
+    sp.stats = m->stats;
+    LAUNCH(TMT_MOE_PH_SCAN, launch_scan(sp, s));
+    if (nblk > 0) {
+        PermuteParams pp{};
+        pp.idx = m->idx; pp.blkbase = m->blkbase; pp.T = T; pp.E = E; pp.K = K;
+        pp.rows_per_block = rpb; pp.perm = m->perm; pp.slot_of = m->slot_of;
+        LAUNCH(TMT_MOE_PH_PERMUTE, launch_permute(pp, nblk, s));
+    }
+    return TMT_MOE_OK;
+}
+
+int check_ptrs(const void* const* tab, int n, const char* what) {
+    if (!tab) return fail(TMT_MOE_EINVAL, "%s table is NULL", what);
+    for (int e = 0; e < n; ++e) {
+        if (!tab[e]) return fail(TMT_MOE_EINVAL, "%s[%d] is NULL", what, e);
+        if (!aligned16(tab[e])) return fail(TMT_MOE_EINVAL, "%s[%d] is not 16-byte aligned", what, e);
+    }
+    return TMT_MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tmt_moe_last_error(void) { return g_last_error.c_str(); }
+
+int tmt_moe_workspace_size(const tmt_moe_desc* desc, size_t* bytes) {
+    int rc = validate_desc(desc);
+    if (rc) return rc;
+    if (!bytes) return fail(TMT_MOE_EINVAL, "bytes is NULL");
+    *bytes = plan(desc, nullptr);
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_create(const tmt_moe_desc* desc, tmt_moe** out) {
+    if (!out) return fail(TMT_MOE_EINVAL, "out is NULL");
+    *out = nullptr;
+    int rc = validate_desc(desc);
+    if (rc) return rc;
+    tmt_moe* m = new (std::nothrow) tmt_moe();
+    if (!m) return fail(TMT_MOE_ENOMEM, "host allocation failed");
+    m->desc = *desc;
+    m->hn = desc->hidden > 0 ? desc->hidden : desc->d;
+    hipError_t err = hipGetDevice(&m->device);
+    if (err != hipSuccess) {
+        delete m;
+        return fail(TMT_MOE_EDEVICE, "hipGetDevice failed: %s", hipGetErrorString(err));
+    }
+    m->arena_bytes = plan(desc, nullptr);
+    err = hipMalloc(&m->arena, m->arena_bytes);
+    if (err != hipSuccess) {
+        delete m;
+        (void)hipGetLastError();
+        return fail(TMT_MOE_ENOMEM, "hipMalloc(%zu) failed: %s", m->arena_bytes, hipGetErrorString(err));
+    }
+    plan(desc, m);
+    *out = m;
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_destroy(tmt_moe* m) {
+    if (!m) return TMT_MOE_OK;
+    hipError_t err = hipSuccess;
+    for (hipEvent_t ev : m->prof_events) (void)hipEventDestroy(ev);
+    if (m->arena) err = hipFree(m->arena);
+    delete m;
+    if (err != hipSuccess) return fail(TMT_MOE_EDEVICE, "hipFree failed: %s", hipGetErrorString(err));
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_forward(tmt_moe* m, void* stream, int32_t T, const uint16_t* X,
+                    const uint16_t* Wr, const float* logit_bias,
+                    const uint16_t* const* W_up, const uint16_t* const* W_down,
+                    uint16_t* Y, float beta) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    const tmt_moe_desc& ds = m->desc;
+    if (ds.weight_format != TMT_MOE_WEIGHTS_BF16)
+        return fail(TMT_MOE_EINVAL, "handle expects MXFP4 weights: use tmt_moe_forward_mxfp4");
+    if (T < 0 || T > ds.max_tokens) return fail(TMT_MOE_EINVAL, "T=%d outside [0, %d]", T, ds.max_tokens);
+    const int E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden, hn = m->hn;
+    if (T > 0 && (!X || !Y)) return fail(TMT_MOE_EINVAL, "X and Y must be non-NULL");
+    if (!aligned16(X) || !aligned16(Y)) return fail(TMT_MOE_EINVAL, "X and Y must be 16-byte aligned");
+    if (E > 1 && (!Wr || !aligned16(Wr))) return fail(TMT_MOE_EINVAL, "Wr must be a 16-byte aligned pointer when experts > 1");
+    int rc = check_ptrs((const void* const*)W_up, E, "W_up");
+    if (rc) return rc;
+    if (h > 0 && (rc = check_ptrs((const void* const*)W_down, E, "W_down"))) return rc;
+    if ((rc = check_device(m))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    m->last_T = -1;
+
+    if ((rc = route(m, s, T, X, Wr, logit_bias))) return rc;
+    if (T > 0) {
+        GemmParams up{};
+        up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
+        up.N = hn; up.K = d; up.slots = T * K;
+        up.a = X; up.lda = d; up.c = m->U; up.ldc = hn; up.c2 = m->Aact;
+        for (int e = 0; e < E; ++e) up.w[e] = W_up[e];
+        up.ldb = d;
+        LAUNCH(TMT_MOE_PH_GEMM_UP, launch_gemm(GEMM_UP, h > 0, up, s));
+        if (h > 0) {
+            GemmParams dn{};
+            dn.offsets = m->offsets; dn.order = m->order; dn.perm = m->perm; dn.E = E;
+            dn.N = d; dn.K = h; dn.slots = T * K;
+            dn.a = m->Aact; dn.lda = h; dn.c = m->O; dn.ldc = d;
+            for (int e = 0; e < E; ++e) dn.w[e] = W_down[e];
+            dn.ldb = h;
+            LAUNCH(TMT_MOE_PH_GEMM_DOWN, launch_gemm(GEMM_DOWN, false, dn, s));
+        }
+        CombineParams cp{};
+        cp.O = h > 0 ? m->O : m->U; cp.slot_of = m->slot_of; cp.gate = m->gate;
+        cp.Y = Y; cp.beta = beta; cp.T = T; cp.d = d; cp.K = K; cp.silu = h == 0;
+        LAUNCH(TMT_MOE_PH_COMBINE, launch_combine(cp, s));
+    }
+    m->last_T = T;
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X,
+                          const uint16_t* Wr, const float* logit_bias,
+                          const uint8_t* const* W_up, const uint8_t* const* W_up_scale,
+                          const uint8_t* const* W_down, const uint8_t* const* W_down_scale,
+                          uint16_t* Y, float beta) {
+    (void)stream; (void)T; (void)X; (void)Wr; (void)logit_bias; (void)W_up; (void)W_up_scale;
+    (void)W_down; (void)W_down_scale; (void)Y; (void)beta;
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    return fail(TMT_MOE_EINVAL, "MXFP4 expert path is not available in this build");
+}
+
+int tmt_moe_backward(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_t* X,
+                     const uint16_t* Wr, const uint16_t* const* W_up,
+                     const uint16_t* const* W_down, float aux_coef, float z_coef,
+                     uint16_t* dX, float* dWr, float* const* dW_up, float* const* dW_down) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    const tmt_moe_desc& ds = m->desc;
+    if (ds.weight_format != TMT_MOE_WEIGHTS_BF16)
+        return fail(TMT_MOE_EINVAL, "backward needs bf16 weights");
+    if (m->last_T < 0) return fail(TMT_MOE_ESTATE, "backward called without a successful forward");
+    const int T = m->last_T, E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden, hn = m->hn;
+    if (T > 0 && (!dY || !X || !dX)) return fail(TMT_MOE_EINVAL, "dY, X and dX must be non-NULL");
+    if (!aligned16(dY) || !aligned16(X) || !aligned16(dX))
+        return fail(TMT_MOE_EINVAL, "dY, X and dX must be 16-byte aligned");
+    if (E > 1 && (!Wr || !dWr || !aligned16(Wr) || !aligned16(dWr)))
+        return fail(TMT_MOE_EINVAL, "Wr and dWr must be 16-byte aligned pointers when experts > 1");
+    int rc = check_ptrs((const void* const*)W_up, E, "W_up");
+    if (rc) return rc;
+    if ((rc = check_ptrs((const void* const*)dW_up, E, "dW_up"))) return rc;
+    if (h > 0) {
+        if ((rc = check_ptrs((const void* const*)W_down, E, "W_down"))) return rc;
+        if ((rc = check_ptrs((const void* const*)dW_down, E, "dW_down"))) return rc;
+    }
+    if ((rc = check_device(m))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+
+    if (T > 0) {
+        CombineBwdParams cb{};
+        cb.dY = dY; cb.O = h > 0 ? m->O : m->U; cb.slot_of = m->slot_of; cb.idx = m->idx;
+        cb.gate = m->gate; cb.probs = m->probs; cb.lse = m->lse; cb.counts = m->counts;
+        cb.T = T; cb.d = d; cb.E = E; cb.K = K; cb.silu = h == 0;
+        cb.aux_coef = aux_coef; cb.z_coef = z_coef; cb.dO = m->dO; cb.dlogits = m->dlogits;
+        LAUNCH(TMT_MOE_PH_COMBINE_BWD, launch_combine_bwd(cb, s));
+    }
+    if (h > 0) {
+        if (T > 0) {
+            GemmParams da{};
+            da.offsets = m->offsets; da.order = m->order; da.perm = m->perm; da.E = E;
+            da.N = h; da.K = d; da.slots = T * K;
+            da.a = m->dO; da.lda = d; da.c = m->dU; da.ldc = h; da.u = m->U;
+            for (int e = 0; e < E; ++e) da.w[e] = W_down[e];
+            da.ldb = h;
+            LAUNCH(TMT_MOE_PH_GEMM_DACT, launch_gemm(GEMM_DACT, false, da, s));
+        }
+        GemmParams dwd{};
+        dwd.offsets = m->offsets; dwd.order = m->order; dwd.perm = m->perm; dwd.E = E;
+        dwd.M = d; dwd.N = h;
+        dwd.a = m->dO; dwd.lda = d; dwd.b = m->Aact; dwd.ldb = h; dwd.ldc = h;
+        for (int e = 0; e < E; ++e) dwd.dw[e] = dW_down[e];
+        LAUNCH(TMT_MOE_PH_GEMM_DW_DOWN, launch_gemm(GEMM_DW_DOWN, false, dwd, s));
+    }
+    GemmParams dwu{};
+    dwu.offsets = m->offsets; dwu.order = m->order; dwu.perm = m->perm; dwu.E = E;
+    dwu.M = hn; dwu.N = d;
+    dwu.a = m->dU; dwu.lda = hn; dwu.b = X; dwu.ldb = d; dwu.ldc = d;
+    for (int e = 0; e < E; ++e) dwu.dw[e] = dW_up[e];
+    LAUNCH(TMT_MOE_PH_GEMM_DW_UP, launch_gemm(GEMM_DW_UP, false, dwu, s));
+    if (T > 0) {
+        GemmParams dx{};
+        dx.offsets = m->offsets; dx.order = m->order; dx.perm = m->perm; dx.E = E;
+        dx.N = d; dx.K = hn; dx.slots = T * K;
+        dx.a = m->dU; dx.lda = hn; dx.c = m->dXg; dx.ldc = d;
+        for (int e = 0; e < E; ++e) dx.w[e] = W_up[e];
+        dx.ldb = d;
+        LAUNCH(TMT_MOE_PH_GEMM_DX, launch_gemm(GEMM_DX, false, dx, s));
+    }
+    if (E > 1) {
+        // With T == 0 the partial pass sums no rows and writes zeros.
+        RouterDwParams rw{};
+        rw.dlogits = m->dlogits; rw.X = X; rw.T = T; rw.d = d; rw.E = E;
+        rw.nchunks = router_dw_chunks(T); rw.partial = m->dwr_partial; rw.dWr = dWr;
+        LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_router_dw(rw, s));
+    }
+    if (T > 0) {
+        ScatterParams sc{};
+        sc.dXg = m->dXg; sc.slot_of = m->slot_of; sc.dlogits = E > 1 ? m->dlogits : nullptr;
+        sc.Wr = Wr; sc.T = T; sc.d = d; sc.E = E; sc.K = K; sc.dX = dX;
+        LAUNCH(TMT_MOE_PH_SCATTER, launch_scatter(sc, s));
+    }
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_read_stats(tmt_moe* m, void* stream, float* aux, float* z, int32_t* counts) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    if (m->last_T < 0) return fail(TMT_MOE_ESTATE, "no forward has run on this handle");
+    int rc = check_device(m);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    const int E = m->desc.experts;
+    float st[2 + kMaxExperts];
+    HIP_TRY(hipMemcpy(st, m->stats, (size_t)(2 + E) * 4, hipMemcpyDeviceToHost));
+    if (aux) *aux = st[0];
+    if (z) *z = st[1];
+    if (counts) std::memcpy(counts, st + 2, (size_t)E * 4);
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_set_profiling(tmt_moe* m, int enable) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    if (enable && m->prof_events.empty()) {
+        m->prof_events.resize(2 * kProfPairs);
+        for (auto& ev : m->prof_events) HIP_TRY(hipEventCreate(&ev));
+    }
+    if (!enable && m->prof_on) {
+        int rc = prof_flush(m);
+        if (rc) return rc;
+    }
+    m->prof_on = enable != 0;
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_read_profile(tmt_moe* m, float* ms, int32_t* launches, int reset) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    int rc = prof_flush(m);
+    if (rc) return rc;
+    for (int i = 0; i < TMT_MOE_NPHASES; ++i) {
+        if (ms) ms[i] = (float)m->prof_ms[i];
+        if (launches) launches[i] = m->prof_cnt[i];
+        if (reset) {
+            m->prof_ms[i] = 0.0;
+            m->prof_cnt[i] = 0;
+        }
+    }
+    return TMT_MOE_OK;
+}
+
+const char* tmt_moe_phase_name(int phase) {
+    static const char* names[TMT_MOE_NPHASES] = {
+        "router", "scan", "permute", "gemm_up", "gemm_down", "combine", "combine_bwd",
+        "gemm_dact", "gemm_dw_down", "gemm_dw_up", "gemm_dx", "router_dw", "scatter"};
+    return (phase >= 0 && phase < TMT_MOE_NPHASES) ? names[phase] : "unknown";
+}
+
+int tmt_moe_stats_device_ptr(tmt_moe* m, const void** ptr) {
+    if (!m || !ptr) return fail(TMT_MOE_EINVAL, "handle or ptr is NULL");
+    *ptr = m->stats;
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_read_routing(tmt_moe* m, void* stream, float* logits, float* probs,
+                         int32_t* idx, float* gate, int32_t* offsets, int32_t* perm,
+                         int32_t* slot_of) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    if (m->last_T < 0) return fail(TMT_MOE_ESTATE, "no forward has run on this handle");
+    int rc = check_device(m);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    const int64_t T = m->last_T, E = m->desc.experts, K = m->desc.topk;
+    if (E > 1) {
+        if (logits && T) HIP_TRY(hipMemcpy(logits, m->logits, T * E * 4, hipMemcpyDeviceToHost));
+        if (probs && T) HIP_TRY(hipMemcpy(probs, m->probs, T * E * 4, hipMemcpyDeviceToHost));
+        if (idx && T) HIP_TRY(hipMemcpy(idx, m->idx, T * K * 4, hipMemcpyDeviceToHost));
+    } else {
+        if (logits) std::memset(logits, 0, T * E * 4);
+        if (probs) for (int64_t i = 0; i < T; ++i) probs[i] = 1.0f;
+        if (idx) std::memset(idx, 0, T * K * 4);
+    }
+    if (gate && T) HIP_TRY(hipMemcpy(gate, m->gate, T * K * 4, hipMemcpyDeviceToHost));
+    if (offsets) HIP_TRY(hipMemcpy(offsets, m->offsets, (E + 1) * 4, hipMemcpyDeviceToHost));
+    if (perm && T) HIP_TRY(hipMemcpy(perm, m->perm, T * K * 4, hipMemcpyDeviceToHost));
+    if (slot_of && T) HIP_TRY(hipMemcpy(slot_of, m->slot_of, T * K * 4, hipMemcpyDeviceToHost));
+    return TMT_MOE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,144 @@
+// moe_internal.hpp -- shared declarations of the gfx950 MoE kernels.
+//
+// Kernel families (one .hip file each):
+//   router.hip    router logits + softmax + top-k, block histograms, expert
+//                 offset scan, stable token permutation
+//   gemm.hip      grouped bf16 MFMA GEMMs over expert segments
+//   pointwise.hip combine, combine/router backward, router dW, dX scatter
+// The host orchestration lives in moe_api.cpp.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tmt {
+
+constexpr int kMaxExperts = 64;
+constexpr int kMaxTopK = 8;
+constexpr int kThreads = 256;  // every kernel runs 4 waves of 64
+
+// ---------------------------------------------------------------- router --
+struct RouterParams {
+    const uint16_t* X;     // [T][d] bf16
+    const uint16_t* Wr;    // [E][d] bf16
+    const float* bias;     // [E] or nullptr
+    int T, d, E, K;
+    int rows_per_block;    // multiple of 4 * (64 / EP)
+    float* logits;         // [T][E]
+    float* probs;          // [T][E]
+    int32_t* idx;          // [T][K]
+    float* gate;           // [T][K]
+    float* lse;            // [T]
+    int32_t* blkcnt;       // [nblk][E] picks per expert in each block
+    float* blkstat;        // [nblk][E+1] sum of probs per expert, sum of lse^2
+};
+int router_ep(int E);  // padded expert count used by the router (power of 2)
+int router_rows_per_wave(int E);
+hipError_t launch_router(const RouterParams& p, int nblk, hipStream_t s);
+
+struct ScanParams {
+    const int32_t* blkcnt;   // [nblk][E]
+    const float* blkstat;    // [nblk][E+1]
+    int nblk, T, E, K;
+    int32_t* counts;         // [E]
+    int32_t* offsets;        // [E+1]
+    int32_t* blkbase;        // [nblk][E]
+    int32_t* order;          // [E] experts by descending count (stable)
+    float* stats;            // {aux, z} followed by E int32 counts
+};
+hipError_t launch_scan(const ScanParams& p, hipStream_t s);
+
+struct PermuteParams {
+    const int32_t* idx;      // [T][K]
+    const int32_t* blkbase;  // [nblk][E]
+    int T, E, K, rows_per_block;
+    int32_t* perm;           // [T*K] slot -> token
+    int32_t* slot_of;        // [T][K] (token, j) -> slot
+};
+hipError_t launch_permute(const PermuteParams& p, int nblk, hipStream_t s);
+
+// E == 1: identity dispatch, gates of 1, offsets {0, T}.
+hipError_t launch_dense_dispatch(int T, int32_t* perm, int32_t* slot_of,
+                                 float* gate, int32_t* counts, int32_t* offsets,
+                                 int32_t* order, float* stats, hipStream_t s);
+
+// ------------------------------------------------------------------ gemm --
+enum GemmKind {
+    GEMM_UP = 0,       // C = gather(X) W_up^T        (+ SiLU copy when dual)
+    GEMM_DOWN = 1,     // C = A W_down^T
+    GEMM_DACT = 2,     // C = (dO W_down) * silu'(U)
+    GEMM_DX = 3,       // C = dU W_up
+    GEMM_DW_DOWN = 4,  // dW_down[e] = dO^T A            (reduction over slots)
+    GEMM_DW_UP = 5     // dW_up[e]   = dU^T gather(X)    (reduction over slots)
+};
+
+struct GemmParams {
+    const int32_t* offsets;  // [E+1] expert segment starts (slot space)
+    const int32_t* order;    // [E] processing order for weight-gradient GEMMs
+    const int32_t* perm;     // [TK] slot -> token (gather table)
+    int E;
+    int M;                   // weight-gradient GEMMs: rows of C
+    int N;                   // columns of C
+    int K;                   // activation GEMMs: reduction length
+    int slots;               // activation GEMMs: T*K routed rows (bounds the row tiles)
+    const uint16_t* a; int64_t lda;   // activation operand
+    const uint16_t* b; int64_t ldb;   // second activation operand (dW GEMMs)
+    void* c; int64_t ldc;             // output (activation GEMMs)
+    uint16_t* c2;                     // SiLU copy (GEMM_UP with hidden > 0)
+    const uint16_t* u;                // pre-activation for GEMM_DACT
+    const uint16_t* w[kMaxExperts];   // per-expert weights (activation GEMMs)
+    float* dw[kMaxExperts];           // per-expert fp32 outputs (dW GEMMs)
+};
+// Grid size the launcher will use (for tests of the tile bound).
+hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s);
+
+// ------------------------------------------------------------- pointwise --
+struct CombineParams {
+    const uint16_t* O;       // [TK][d] expert outputs (hidden > 0) or U (hidden == 0)
+    const int32_t* slot_of;  // [T][K]
+    const float* gate;       // [T][K]
+    uint16_t* Y;             // [T][d]
+    float beta;
+    int T, d, K;
+    int silu;                // 1: apply SiLU to O (hidden == 0)
+};
+hipError_t launch_combine(const CombineParams& p, hipStream_t s);
+
+struct CombineBwdParams {
+    const uint16_t* dY;      // [T][d]
+    const uint16_t* O;       // [TK][d] (hidden > 0) or U (hidden == 0)
+    const int32_t* slot_of;  // [T][K]
+    const int32_t* idx;      // [T][K]
+    const float* gate;       // [T][K]
+    const float* probs;      // [T][E]
+    const float* lse;        // [T]
+    const int32_t* counts;   // [E]
+    int T, d, E, K;
+    int silu;                // 1: hidden == 0 (SiLU applied in combine)
+    float aux_coef, z_coef;
+    uint16_t* dO;            // [TK][d] gradient at the expert output
+    float* dlogits;          // [T][E] (E > 1)
+};
+hipError_t launch_combine_bwd(const CombineBwdParams& p, hipStream_t s);
+
+struct RouterDwParams {
+    const float* dlogits;    // [T][E]
+    const uint16_t* X;       // [T][d]
+    int T, d, E;
+    int nchunks;
+    float* partial;          // [nchunks][E][d]
+    float* dWr;              // [E][d]
+};
+int router_dw_chunks(int T);
+hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s);
+
+struct ScatterParams {
+    const uint16_t* dXg;     // [TK][d]
+    const int32_t* slot_of;  // [T][K]
+    const float* dlogits;    // [T][E] or nullptr
+    const uint16_t* Wr;      // [E][d]
+    int T, d, E, K;
+    uint16_t* dX;            // [T][d]
+};
+hipError_t launch_scatter(const ScatterParams& p, hipStream_t s);
+
+}  // namespace tmt

@@ -1,0 +1,103 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/tmt_moe.h declares, validates descriptors with clear errors, and the
+product path has no route to the oracle or any CPU implementation."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import tmt_moe
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tmt_moe.h")
+PKG = os.path.join(ROOT, "test-model-thing-cuda_amd")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tmt_moe_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = tmt_moe.load_library()
+    names = declared_functions()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(tmt_moe.EXPORTED)
+
+
+def test_workspace_size_matches_layout():
+    c3 = tmt_moe.workspace_size(32768, 1024, 16, 4, 4096)
+    TK = 32768 * 4
+    # U, A, dU (TK x h) + O, dO, dXg (TK x d) in bf16 dominate
+    big = 3 * TK * 4096 * 2 + 3 * TK * 1024 * 2
+    assert big <= c3 <= big + (64 << 20)
+    ref_mode = tmt_moe.workspace_size(2048, 256, 4, 2, 0)
+    assert ref_mode < tmt_moe.workspace_size(2048, 256, 4, 2, 1024)
+
+
+@pytest.mark.parametrize("desc,msg", [
+    ((16, 100, 4, 2, 0), "multiple of 128"),
+    ((16, 128, 0, 1, 0), "experts"),
+    ((16, 128, 65, 1, 0), "experts"),
+    ((16, 128, 4, 5, 0), "topk"),
+    ((16, 128, 16, 9, 0), "topk"),
+    ((16, 128, 4, 2, 100), "hidden"),
+    ((0, 128, 4, 2, 0), "max_tokens"),
+    ((16, 4096, 16, 2, 0), "LDS"),
+])
+def test_invalid_descriptors_are_rejected(desc, msg):
+    with pytest.raises(tmt_moe.MoeError) as ei:
+        tmt_moe.workspace_size(*desc)
+    assert ei.value.code == -1
+    assert msg in str(ei.value)
+
+
+def test_mxfp4_requires_hidden():
+    with pytest.raises(tmt_moe.MoeError, match="hidden"):
+        tmt_moe.workspace_size(16, 128, 4, 2, 0, tmt_moe.WEIGHTS_MXFP4)
+
+
+def test_null_handle_is_an_error_not_a_crash():
+    lib = tmt_moe.load_library()
+    assert lib.tmt_moe_forward(None, None, 0, None, None, None, None, None, None,
+                               ctypes.c_float(1.0)) == -1
+    assert "NULL" in tmt_moe.last_error()
+    assert lib.tmt_moe_destroy(None) == 0
+    assert lib.tmt_moe_phase_name(0) == b"router"
+    assert lib.tmt_moe_phase_name(99) == b"unknown"
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    monkeypatch.setattr(tmt_moe, "_lib", None)
+    with pytest.raises(FileNotFoundError, match="no non-HIP implementation"):
+        tmt_moe.load_library(str(tmp_path / "absent.so"))
+
+
+def test_product_path_never_touches_the_oracle():
+    for root in (PKG,):
+        for dirpath, _, files in os.walk(root):
+            for f in files:
+                if f.endswith((".py", ".cpp", ".hip", ".hpp", ".h")):
+                    text = open(os.path.join(dirpath, f)).read()
+                    assert "moe_oracle" not in text and "liboracle" not in text, f
+    # bench.py may use the oracle only inside its cpu_baseline leg
+    import ast
+    src = open(os.path.join(ROOT, "bench.py")).read()
+    tree = ast.parse(src)
+    allowed = [(n.lineno, n.end_lineno) for n in ast.walk(tree)
+               if isinstance(n, ast.FunctionDef) and n.name == "cpu_baseline"]
+    assert allowed, "bench.py must keep its oracle use inside cpu_baseline()"
+    for node in ast.walk(tree):
+        name = getattr(node, "id", None) or getattr(node, "name", None)
+        if isinstance(node, ast.alias):
+            name = node.name
+        if name == "moe_oracle":
+            line = getattr(node, "lineno", None)
+            if line is None:  # alias nodes: find the import statement
+                line = next(n.lineno for n in ast.walk(tree)
+                            if isinstance(n, (ast.Import, ast.ImportFrom)) and node in n.names)
+            assert any(a <= line <= b for a, b in allowed), f"bench.py:{line} uses the oracle"

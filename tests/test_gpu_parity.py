@@ -1,0 +1,267 @@
+"""GPU parity: the HIP path, called through the C ABI, against the oracle.
+
+Bars (from the build's contract):
+  * routing -- router logits, top-k indices, expert offsets, permutation and
+    slot table -- bit-exact against the CPU oracle;
+  * floating-point outputs and gradients within 1e-2 relative L2 of the
+    oracle's fp32 results (bf16 inputs, fp32 accumulation); at the full c2/c3
+    sizes the fp32 reference is torch autograd on the GPU, fed with the
+    routing that was just matched bit for bit.
+Every test prints its case before touching the GPU.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import tmt_moe
+from synthetic import CONFIGS, bf16_bits, bf16_to_f32, make_case
+from torch_ref import moe_reference
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-2  # north-star tolerance for floating outputs and gradients
+
+
+def say(msg):
+    print(f"[gpu-case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(u16):
+    return torch.from_numpy(np.ascontiguousarray(u16).view(np.int16)).cuda().view(torch.bfloat16)
+
+
+def host_f32(t):
+    return bf16_to_f32(t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
+
+
+def near(got, ref, atol, rtol, what):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    bad = ~(np.abs(got - ref) <= atol + rtol * np.abs(ref))
+    assert not bad.any(), f"{what}: {bad.sum()} mismatches, e.g. {got[bad][:4]} vs {ref[bad][:4]}"
+
+
+def run_gpu(case, K, h, beta=0.0, Y0=None, backward=False, aux=0.0, z=0.0, max_tokens=None,
+            keep=False):
+    T, d = case["X"].shape
+    E = case["W_up"].shape[0]
+    hn = h if h > 0 else d
+    m = tmt_moe.MoE(max_tokens or max(T, 1), d, E, K, h)
+    X = dev(case["X"])
+    Wr = dev(case["Wr"])
+    Wu = dev(case["W_up"])
+    Wd = dev(case["W_down"]) if h > 0 else None
+    bias = torch.from_numpy(case["bias"]).cuda() if case.get("bias") is not None else None
+    Y = dev(Y0) if Y0 is not None else torch.zeros(T, d, dtype=torch.bfloat16, device="cuda")
+    m.forward(X, Wr, Wu, Wd, Y, beta=beta, bias=bias)
+    out = {"Y": host_f32(Y)}
+    out.update(m.routing())
+    out["aux"], out["z"], out["counts"] = m.stats()
+    if backward:
+        dY = dev(case["dY"])
+        nan = float("nan")
+        dX = torch.full((T, d), nan, dtype=torch.bfloat16, device="cuda")
+        dWr = torch.full((E, d), nan, dtype=torch.float32, device="cuda")
+        dWu = torch.full((E, hn, d), nan, dtype=torch.float32, device="cuda")
+        dWd = torch.full((E, d, h), nan, dtype=torch.float32, device="cuda") if h > 0 else None
+        m.backward(dY, X, Wr, Wu, Wd, dX, dWr if E > 1 else None, dWu, dWd, aux, z)
+        torch.cuda.synchronize()
+        out.update(dX=host_f32(dX), dW_up=dWu.cpu().numpy())
+        out["dWr"] = dWr.cpu().numpy() if E > 1 else None
+        out["dW_down"] = dWd.cpu().numpy() if h > 0 else None
+    if keep:
+        out["_moe"] = m
+    else:
+        m.close()
+    return out
+
+
+def check_routing(g, r, E):
+    assert np.array_equal(g["idx"], r["idx"]), "top-k indices differ"
+    if E > 1:
+        assert np.array_equal(g["logits"].view(np.uint32), r["logits"].view(np.uint32)), \
+            "router logits are not bit-identical to the canonical order"
+        near(g["probs"], r["probs"], 1e-6, 1e-5, "probs")
+    near(g["gate"], r["gate"], 1e-6, 1e-5, "gates")
+    assert np.array_equal(g["offsets"], r["offsets"]), "expert offsets differ"
+    assert np.array_equal(g["perm"], r["perm"]), "permutation differs"
+    assert np.array_equal(g["slot_of"], r["slot_of"]), "slot table differs"
+
+
+def check_grads(g, r, h, E):
+    names = ["dX", "dW_up"] + (["dW_down"] if h > 0 else []) + (["dWr"] if E > 1 else [])
+    for n in names:
+        assert np.isfinite(g[n]).all(), f"{n} has unwritten/non-finite entries"
+        err = rel_l2(g[n], r[n])
+        say(f"  {n}: rel-L2 {err:.2e}")
+        assert err <= REL_L2, f"{n} rel-L2 {err:.3e} > {REL_L2}"
+
+
+def oracle_case(orc, case, K, h, Y0=None, beta=0.0, backward=False, aux=0.0, z=0.0):
+    f = orc.forward(case["X"], case["Wr"], case["W_up"], case["W_down"], K, h,
+                    bias=case.get("bias"), Y_in=Y0, beta=beta)
+    if backward:
+        f.update(orc.backward(case["X"], case["Wr"], case["W_up"], case["W_down"], case["dY"], K, h,
+                              bias=case.get("bias"), aux_coef=aux, z_coef=z))
+    return f
+
+
+# ------------------------------------------------------------------ c1 ----
+
+def test_c1_forward_against_oracle(orc):
+    cfg = CONFIGS["c1"]
+    say("c1 forward T=2048 d=256 E=4 K=2 h=1024 beta=1")
+    case = make_case(**cfg)
+    Y0 = bf16_bits(np.random.default_rng(1).standard_normal((cfg["T"], cfg["d"])).astype(np.float32))
+    g = run_gpu(case, cfg["K"], cfg["h"], beta=1.0, Y0=Y0)
+    r = oracle_case(orc, case, cfg["K"], cfg["h"], Y0=Y0, beta=1.0)
+    check_routing(g, r, cfg["E"])
+    err = rel_l2(g["Y"], r["Y"])
+    say(f"  Y rel-L2 {err:.2e}")
+    assert err <= REL_L2
+    near(g["aux"], r["aux"], 1e-6, 1e-4, "aux")
+    near(g["z"], r["z"], 1e-6, 1e-4, "z")
+    assert np.array_equal(g["counts"], r["counts"])
+
+
+def test_c1_backward_against_oracle(orc):
+    cfg = CONFIGS["c1"]
+    say("c1 forward+backward aux=0.1 z=1e-3")
+    case = make_case(**cfg)
+    g = run_gpu(case, cfg["K"], cfg["h"], backward=True, aux=0.1, z=1e-3)
+    r = oracle_case(orc, case, cfg["K"], cfg["h"], backward=True, aux=0.1, z=1e-3)
+    check_routing(g, r, cfg["E"])
+    assert rel_l2(g["Y"], r["Y"]) <= REL_L2
+    check_grads(g, r, cfg["h"], cfg["E"])
+
+
+@pytest.mark.parametrize("T,d,E,K,h", [
+    (1000, 256, 4, 2, 0),      # reference single-linear experts, SiLU in combine
+    (777, 256, 1, 1, 0),       # reference dense path (experts=1, no router)
+    (1237, 384, 8, 2, 256),    # ragged T, d not a multiple of 512
+    (300, 512, 64, 8, 128),    # widest router (64 experts), top-8
+    (500, 1024, 32, 4, 256),   # the c5 router shape
+    (129, 128, 3, 3, 128),     # E == K, odd expert count
+])
+def test_shapes_against_oracle(orc, T, d, E, K, h):
+    say(f"shape T={T} d={d} E={E} K={K} h={h} fwd+bwd")
+    case = make_case(T, d, E, K, h, seed=T + d)
+    aux, z = (0.1, 1e-3) if E > 1 else (0.0, 0.0)
+    Y0 = bf16_bits(np.random.default_rng(T).standard_normal((T, d)).astype(np.float32))
+    g = run_gpu(case, K, h, beta=1.0, Y0=Y0, backward=True, aux=aux, z=z)
+    r = oracle_case(orc, case, K, h, Y0=Y0, beta=1.0, backward=True, aux=aux, z=z)
+    check_routing(g, r, E)
+    err = rel_l2(g["Y"], r["Y"])
+    say(f"  Y rel-L2 {err:.2e}")
+    assert err <= REL_L2
+    check_grads(g, r, h, E)
+
+
+def test_empty_batch():
+    say("T=0 forward+backward")
+    T, d, E, K, h = 0, 256, 4, 2, 256
+    case = make_case(T, d, E, K, h)
+    g = run_gpu(case, K, h, backward=True, aux=0.1, z=1e-3, max_tokens=16)
+    assert g["aux"] == 0.0 and g["z"] == 0.0
+    assert np.all(g["counts"] == 0) and np.all(g["offsets"] == 0)
+    for n in ("dWr", "dW_up", "dW_down"):
+        assert np.all(g[n] == 0.0), n
+
+
+def test_dead_experts_get_zero_gradients(orc):
+    say("dead experts: bias routes every token to experts 0 and 1")
+    T, d, E, K, h = 640, 256, 8, 2, 256
+    case = make_case(T, d, E, K, h, seed=5)
+    case["bias"] = np.array([40, 40, -40, -40, -40, -40, -40, -40], np.float32)
+    g = run_gpu(case, K, h, backward=True, aux=0.1, z=1e-3)
+    r = oracle_case(orc, case, K, h, backward=True, aux=0.1, z=1e-3)
+    check_routing(g, r, E)
+    assert list(g["counts"]) == [T, T, 0, 0, 0, 0, 0, 0]
+    assert np.all(g["dW_up"][2:] == 0.0) and np.all(g["dW_down"][2:] == 0.0)
+    check_grads(g, r, h, E)
+
+
+def test_router_ties_go_to_lower_index(orc):
+    say("router ties: experts 2 and 4 have identical rows")
+    T, d, E, K, h = 256, 256, 6, 2, 128
+    case = make_case(T, d, E, K, h, seed=6)
+    case["Wr"][2] = case["Wr"][4]
+    case["bias"] = np.array([-30, -30, 20, -30, 20, -30], np.float32)
+    g = run_gpu(case, K, h)
+    assert np.all(g["idx"] == np.array([2, 4]))
+    assert np.array_equal(g["logits"][:, 2].view(np.uint32), g["logits"][:, 4].view(np.uint32))
+    r = oracle_case(orc, case, K, h)
+    check_routing(g, r, E)
+
+
+def test_runs_are_bitwise_deterministic():
+    say("determinism: two identical fwd+bwd runs")
+    T, d, E, K, h = 2000, 512, 8, 2, 512
+    case = make_case(T, d, E, K, h, seed=8)
+    a = run_gpu(case, K, h, backward=True, aux=0.1, z=1e-3)
+    b = run_gpu(case, K, h, backward=True, aux=0.1, z=1e-3)
+    for n in ("Y", "dX", "dWr", "dW_up", "dW_down", "perm", "logits"):
+        assert np.array_equal(np.asarray(a[n]).view(np.uint32), np.asarray(b[n]).view(np.uint32)), n
+
+
+# ------------------------------------------------------- c2 / c3 full size --
+
+def _full_size(orc, name):
+    cfg = CONFIGS[name]
+    T, d, E, K, h = (cfg[k] for k in ("T", "d", "E", "K", "h"))
+    say(f"{name} full size T={T} d={d} E={E} K={K} h={h} fwd+bwd")
+    case = make_case(**cfg)
+    g = run_gpu(case, K, h, backward=True, aux=cfg["aux"], z=cfg["z"])
+    # routing against the oracle router + dispatch at full size
+    rr = orc.router(case["X"], case["Wr"], K, bias=case.get("bias"))
+    rd = orc.dispatch(rr["idx"], E)
+    rr.update(rd)
+    check_routing(g, rr, E)
+    aux, z = orc.aux_z(rr["probs"], rd["counts"], rr["lse"], K)
+    near(g["aux"], aux, 1e-6, 1e-4, "aux")
+    near(g["z"], z, 1e-6, 1e-4, "z")
+    # floating outputs against fp32 torch autograd on the matched routing
+    t = lambda a: torch.from_numpy(bf16_to_f32(a)).cuda()
+    ref = moe_reference(t(case["X"]), t(case["Wr"]), t(case["W_up"]),
+                        t(case["W_down"]), torch.from_numpy(rr["idx"].astype(np.int64)).cuda(),
+                        t(case["dY"]), h,
+                        bias=None if case.get("bias") is None else torch.from_numpy(case["bias"]).cuda(),
+                        aux_coef=cfg["aux"], z_coef=cfg["z"])
+    err = rel_l2(g["Y"], ref["Y"].cpu().numpy())
+    say(f"  Y rel-L2 {err:.2e}")
+    assert err <= REL_L2
+    refn = {k: (v.cpu().numpy() if torch.is_tensor(v) else v) for k, v in ref.items()}
+    check_grads(g, refn, h, E)
+    return g, case
+
+
+def test_c2_full_size(orc):
+    _full_size(orc, "c2")
+
+
+def test_c3_full_size_zipf(orc):
+    g, case = _full_size(orc, "c3")
+    cnt = g["counts"]
+    skew = cnt.max() / cnt.mean()
+    say(f"  c3 load skew max/mean = {skew:.2f} (alpha {case['alpha']:.3f})")
+    assert 3.0 < skew < 5.0
+
+
+@pytest.mark.parametrize("T", [1, 8, 64])
+def test_decode_steps_against_oracle(orc, T):
+    cfg = CONFIGS["c3"]
+    say(f"decode T={T} on c3 weights")
+    case = make_case(T, cfg["d"], cfg["E"], cfg["K"], cfg["h"], seed=1234 + T)
+    Y0 = bf16_bits(np.random.default_rng(T).standard_normal((T, cfg["d"])).astype(np.float32))
+    g = run_gpu(case, cfg["K"], cfg["h"], beta=1.0, Y0=Y0, max_tokens=64)
+    r = oracle_case(orc, case, cfg["K"], cfg["h"], Y0=Y0, beta=1.0)
+    check_routing(g, r, cfg["E"])
+    assert rel_l2(g["Y"], r["Y"]) <= REL_L2
