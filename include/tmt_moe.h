@@ -18,7 +18,7 @@
  * (linalg.cu:1-8). bf16 values are raw uint16 bit patterns. Per-expert
  * weights are passed as host arrays of E device pointers, the reference's
  * `bf16** Wexp` convention (moe.cu:374). All device pointers must be 16-byte
- * aligned. d and hidden must be multiples of 128.
+ * aligned. d and hidden must be multiples of 64.
  *
  * Every function returns TMT_MOE_OK (0) or a negative error code and never
  * exits the process; tmt_moe_last_error() gives a thread-local message.
@@ -50,10 +50,10 @@ enum { TMT_MOE_WEIGHTS_BF16 = 0, TMT_MOE_WEIGHTS_MXFP4 = 1 };
 
 typedef struct tmt_moe_desc {
     int32_t max_tokens;     /* T_max: largest T a call may pass */
-    int32_t d;              /* model width (multiple of 128) */
+    int32_t d;              /* model width (multiple of 64) */
     int32_t experts;        /* E, 1..64 */
     int32_t topk;           /* K, 1..min(E, 8) */
-    int32_t hidden;         /* h (multiple of 128), or 0 for reference experts */
+    int32_t hidden;         /* h (multiple of 64), or 0 for reference experts */
     int32_t weight_format;  /* TMT_MOE_WEIGHTS_* */
 } tmt_moe_desc;
 

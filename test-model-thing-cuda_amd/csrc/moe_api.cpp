@@ -80,13 +80,13 @@ namespace {
 int validate_desc(const tmt_moe_desc* d) {
     if (!d) return fail(TMT_MOE_EINVAL, "descriptor is NULL");
     if (d->max_tokens < 1) return fail(TMT_MOE_EINVAL, "max_tokens must be >= 1");
-    if (d->d < 128 || d->d % 128 != 0) return fail(TMT_MOE_EINVAL, "d=%d must be a positive multiple of 128", d->d);
+    if (d->d < 64 || d->d % 64 != 0) return fail(TMT_MOE_EINVAL, "d=%d must be a positive multiple of 64", d->d);
     if (d->experts < 1 || d->experts > kMaxExperts)
         return fail(TMT_MOE_EINVAL, "experts=%d must be in [1, %d]", d->experts, kMaxExperts);
     if (d->topk < 1 || d->topk > d->experts || d->topk > kMaxTopK)
         return fail(TMT_MOE_EINVAL, "require 1 <= topk <= min(experts, %d) (topk=%d)", kMaxTopK, d->topk);
-    if (d->hidden < 0 || d->hidden % 128 != 0)
-        return fail(TMT_MOE_EINVAL, "hidden=%d must be 0 or a multiple of 128", d->hidden);
+    if (d->hidden < 0 || d->hidden % 64 != 0)
+        return fail(TMT_MOE_EINVAL, "hidden=%d must be 0 or a multiple of 64", d->hidden);
     if ((int64_t)d->experts * d->d > 32768)
         return fail(TMT_MOE_EINVAL, "experts*d=%lld exceeds 32768 (router weights are staged in 64 KiB of LDS)",
                     (long long)d->experts * d->d);

@@ -40,7 +40,7 @@ def test_workspace_size_matches_layout():
 
 
 @pytest.mark.parametrize("desc,msg", [
-    ((16, 100, 4, 2, 0), "multiple of 128"),
+    ((16, 100, 4, 2, 0), "multiple of 64"),
     ((16, 128, 0, 1, 0), "experts"),
     ((16, 128, 65, 1, 0), "experts"),
     ((16, 128, 4, 5, 0), "topk"),

@@ -150,6 +150,7 @@ def test_c1_backward_against_oracle(orc):
     (300, 512, 64, 8, 128),    # widest router (64 experts), top-8
     (500, 1024, 32, 4, 256),   # the c5 router shape
     (129, 128, 3, 3, 128),     # E == K, odd expert count
+    (333, 192, 5, 2, 320),     # d and h not multiples of the 256-wide GEMM tile
 ])
 def test_shapes_against_oracle(orc, T, d, E, K, h):
     say(f"shape T={T} d={d} E={E} K={K} h={h} fwd+bwd")
