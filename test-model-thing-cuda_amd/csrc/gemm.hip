@@ -4,21 +4,29 @@
 // forward, :533-539 backward; wrappers tmt-cuda/src/linalg.cu:9-41) and the
 // gather kernel (moe.cu:127-140): one launch covers all experts, tiles are
 // found from the device-side offset table (no host sync, no 128-row padding),
-// and the token gather is folded into the operand loads.
+// and the forward token gather is folded into the operand addressing.
 //
 // Tile: 256 x 256 outputs per 256-thread workgroup (one workgroup per CU),
 // 4 waves in 2 x 2, each wave 128 x 128 = 4 x 4 v_mfma_f32_32x32x16_bf16
-// tiles (256 fp32 accumulators per lane). K step 64 with two 64 KiB LDS
-// stages. Per K step a wave reads 32 KiB of fragments for 2 MFLOP, half the
-// LDS traffic per flop of a 64 x 64 wave tile.
+// tiles (256 fp32 accumulators per lane, held in AGPRs).
 //
-// Operands are staged in LDS as [rows][64] bf16, K contiguous, 16-byte chunks
-// XOR-swizzled by (row ^ row>>3) & 7: fragment reads and both kinds of stores
-// are bank-conflict free. Operands whose memory layout has the row index
-// contiguous (weights read as [K][N] in backward, token-major activations in
-// the weight-gradient GEMMs) are transposed in registers: a thread loads an
-// 8 x 8 block with eight 16-byte loads and stores eight K-contiguous rows.
-// Global loads for step k+2 are in flight while step k computes.
+// Operand staging: direct global -> LDS loads (global_load_lds_dwordx4, the
+// data never passes through VGPRs) into a ring of 4 LDS stages of K = 32
+// (32 KiB each), issued three tiles ahead of the MFMAs that use them.
+//   * K-contiguous operands (activations in every GEMM, weights in the
+//     forward) land as [256 rows][32] bf16, 16-byte chunks XOR-swizzled by
+//     (row >> 1) & 3, and are read with ds_read_b128.
+//   * Row-contiguous operands (weights read as [K][N] in the backward, and
+//     the token-major operands of the weight-gradient GEMMs) land as
+//     [32 k][256] bf16, chunks swizzled by 2 * (k & 3), and are read with the
+//     gfx950 transposing ds_read_b64_tr_b16: inside each 16-lane group, lane
+//     r points at row k0 + r/4, columns c0 + 4(r%4) .. +3, and lane i receives
+//     column c0 + i of rows k0 .. k0+3 -- a K-contiguous MFMA fragment.
+// The loads are issued from inline asm with explicit vmcnt accounting: the
+// compiler would otherwise wait for every outstanding LDS-DMA load before
+// each LDS read. Masked rows/columns are clamped to valid addresses (they
+// only feed outputs that are not stored), except the reduction tail of the
+// weight-gradient GEMMs, which is zeroed in LDS.
 //
 // Epilogue: accumulators go through LDS (fp32, 16-byte chunks swizzled by
 // row) so every global store is a 16-byte vector and each output row is
@@ -29,17 +37,23 @@
 namespace tmt {
 namespace {
 
-constexpr int BK = 64;
+constexpr int BK = 32;
 constexpr int BM = 256;
 constexpr int BN = 256;
+constexpr int NSTAGE = 4;
 constexpr int WTM = 128, WTN = 128;       // wave tile
 constexpr int MI = WTM / 32, NJ = WTN / 32;
-constexpr int STAGE = (BM + BN) * BK;     // bf16 elements per LDS stage
+constexpr int OPND = 256 * BK;            // bf16 elements of one operand tile
+constexpr int STAGE = 2 * OPND;           // A then B
+constexpr int DMA_PER_OPND = 4;           // 1 KiB wave loads per operand tile per wave
+constexpr int DMA_PER_TILE = 2 * DMA_PER_OPND;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 template <int KIND> struct Traits;
-// C[slot][n] = X[perm[slot]] . W_up[e][n]         A: K-contig gather, B: K-contig
+// C[slot][n] = X[perm[slot]] . W_up[e][n]              A: K-contig (gathered), B: K-contig
 template <> struct Traits<GEMM_UP> {
     static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = true;
 };
@@ -47,11 +61,11 @@ template <> struct Traits<GEMM_UP> {
 template <> struct Traits<GEMM_DOWN> {
     static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = false;
 };
-// C[slot][n] = (dO[slot] . W_down[e][:, n]) * silu'(U)   B is [K][N]
+// C[slot][n] = (dO[slot] . W_down[e][:, n]) * silu'(U)  B: [K][N]
 template <> struct Traits<GEMM_DACT> {
     static constexpr bool group_k = false, a_kc = true, b_kc = false, gather = false;
 };
-// C[slot][n] = dU[slot] . W_up[e][:, n]            B is [K][N]
+// C[slot][n] = dU[slot] . W_up[e][:, n]                 B: [K][N]
 template <> struct Traits<GEMM_DX> {
     static constexpr bool group_k = false, a_kc = true, b_kc = false, gather = false;
 };
@@ -59,37 +73,39 @@ template <> struct Traits<GEMM_DX> {
 template <> struct Traits<GEMM_DW_DOWN> {
     static constexpr bool group_k = true, a_kc = false, b_kc = false, gather = false;
 };
-// dW_up[e][m][n] = sum_slot dU[slot][m] * X[perm[slot]][n]
+// dW_up[e][m][n] = sum_slot dU[slot][m] * Xg[slot][n]   (Xg: X gathered to slot order)
 template <> struct Traits<GEMM_DW_UP> {
-    static constexpr bool group_k = true, a_kc = false, b_kc = false, gather = true;
+    static constexpr bool group_k = true, a_kc = false, b_kc = false, gather = false;
 };
 
-__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
-
-__device__ __forceinline__ uint32_t comp(const uint4& v, int i) {
-    return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
-}
-
-// Element i (0..7) of eight 8-element rows st[0..7] -> one 8-element column.
-__device__ __forceinline__ uint4 column8(const uint4* st, int i) {
-    uint32_t d[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const uint32_t a = comp(st[2 * q], i >> 1), b = comp(st[2 * q + 1], i >> 1);
-        d[q] = (i & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
-    }
-    return make_uint4(d[0], d[1], d[2], d[3]);
-}
-
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
+// One wave-wide 16-byte-per-lane load from global memory into LDS at
+// lds_base + 16 * lane (lds_base must be wave-uniform).
+// M0 is written here and declared clobbered (clang warns that it is reserved).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const uint16_t* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
+}
 
 template <int KIND, bool DUAL>
 __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p) {
     using Tr = Traits<KIND>;
-    __shared__ uint4 lds_raw[2 * STAGE / 8];
+    __shared__ uint4 lds_raw[NSTAGE * STAGE / 8];
     uint16_t* lds = reinterpret_cast<uint16_t*>(lds_raw);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int wm = wave >> 1, wn = wave & 1;
     const int ntn = (p.N + BN - 1) / BN;
 
@@ -146,110 +162,118 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
     const int nlim = min(BN, p.N - nt * BN);  // valid output columns in this tile
     const int nk = (kend - kbeg + BK - 1) / BK;
 
-    // ---- loaders: every thread stages 8 vectors of each operand ------------
-    // K-contiguous: rows kc_r + 32i, 16-byte chunk kc_ch.
-    // Row-contiguous: columns 8*mc_c8 .. +7, k rows 8*mc_kg .. +7.
-    const int kc_ch = tid & 7, kc_r = tid >> 3;
-    const int mc_c8 = tid & 31, mc_kg = tid >> 5;
-
-    // Row/column indices past the valid range are clamped to a valid address
-    // instead of masked: they only feed output rows or columns that the
-    // epilogue does not store. Only the reduction tail of the weight-gradient
-    // GEMMs (slots past the expert segment) must read as zero; it is masked
-    // with an all-ones/zero word that the compiler cannot turn into a branch.
-    const uint16_t* a_rp[8];
-    const uint16_t* b_rp[8];
-    const uint16_t* a_mc = nullptr;
-    const uint16_t* b_mc = nullptr;
-    int b_src[8];  // gathered source rows of the next B tile (dW_up)
-
-    if constexpr (Tr::a_kc) {
+    // ---- DMA addressing -----------------------------------------------------
+    // K-contiguous tile: wave load q = 4*wave + i covers rows 16q .. 16q+15;
+    // lane -> row 16q + lane/4, physical chunk lane%4, logical chunk
+    // (lane%4) ^ ((row >> 1) & 3). Row-contiguous tile: wave load q covers k
+    // rows 2q, 2q+1; lane -> k = 2q + lane/32, physical chunk lane%32, logical
+    // chunk (lane%32) ^ (2 * (k & 3)).
+    // K-contiguous operands keep one source pointer per wave load; row-
+    // contiguous ones keep a column pointer and the lane's k row, clamped to
+    // the last valid reduction index when issued (the tail is zeroed in LDS).
+    const uint16_t* a_ptr[DMA_PER_OPND];
+    const uint16_t* b_ptr[DMA_PER_OPND];
+    int a_k[DMA_PER_OPND], b_k[DMA_PER_OPND];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int slot = min(row0 + kc_r + 32 * i, p.slots - 1);
-            const int src = Tr::gather ? p.perm[slot] : slot;
-            a_rp[i] = p.a + (int64_t)src * p.lda + kc_ch * 8;
-        }
-    } else {
-        a_mc = p.a + min(mt * BM + mc_c8 * 8, p.M - 8);
-    }
-    if constexpr (Tr::b_kc) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int n = min(nt * BN + kc_r + 32 * i, p.N - 1);
-            b_rp[i] = p.w[e] + (int64_t)n * p.ldb + kc_ch * 8;
-        }
-    } else if constexpr (!Tr::group_k) {
-        b_mc = p.w[e] + min(nt * BN + mc_c8 * 8, p.N - 8);  // weight read as [K][N]
-    } else {
-        b_mc = p.b + min(nt * BN + mc_c8 * 8, p.N - 8);
-    }
-
-    auto fetch_src = [&](int k0) {
-        if constexpr (Tr::group_k && Tr::gather) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) b_src[t] = p.perm[min(k0 + mc_kg * 8 + t, kend - 1)];
-        }
-    };
-    auto tail_mask = [&](int k) {
-        uint32_t m = k < kend ? 0xffffffffu : 0u;
-        asm("" : "+v"(m));
-        return m;
-    };
-    auto and4 = [](uint4 v, uint32_t m) { return make_uint4(v.x & m, v.y & m, v.z & m, v.w & m); };
-
-    uint4 sa[8], sb[8];
-    auto gload = [&](int k0) {
+    for (int i = 0; i < DMA_PER_OPND; ++i) {
+        const int q = wave * DMA_PER_OPND + i;
         if constexpr (Tr::a_kc) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) sa[i] = ld16(a_rp[i] + k0);
+            const int r = 16 * q + (lane >> 2);
+            const int c = (lane & 3) ^ ((r >> 1) & 3);
+            const int slot = min(row0 + r, p.slots - 1);
+            const int src = Tr::gather ? p.perm[slot] : slot;
+            a_ptr[i] = p.a + (int64_t)src * p.lda + c * 8;
+            a_k[i] = 0;
         } else {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const int k = k0 + mc_kg * 8 + t;
-                sa[t] = and4(ld16(a_mc + (int64_t)min(k, kend - 1) * p.lda), tail_mask(k));
-            }
+            const int k = 2 * q + (lane >> 5);
+            const int c = (lane & 31) ^ (2 * (k & 3));
+            a_ptr[i] = p.a + min(mt * BM + c * 8, p.M - 8);
+            a_k[i] = k;
         }
         if constexpr (Tr::b_kc) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) sb[i] = ld16(b_rp[i] + k0);
-        } else if constexpr (Tr::group_k && Tr::gather) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t)
-                sb[t] = and4(ld16(b_mc + (int64_t)b_src[t] * p.ldb), tail_mask(k0 + mc_kg * 8 + t));
-            fetch_src(k0 + BK);  // source rows of the next tile, off the critical path
-        } else if constexpr (Tr::group_k) {
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const int k = k0 + mc_kg * 8 + t;
-                sb[t] = and4(ld16(b_mc + (int64_t)min(k, kend - 1) * p.ldb), tail_mask(k));
-            }
+            const int r = 16 * q + (lane >> 2);
+            const int c = (lane & 3) ^ ((r >> 1) & 3);
+            const int n = min(nt * BN + r, p.N - 1);
+            b_ptr[i] = p.w[e] + (int64_t)n * p.ldb + c * 8;
+            b_k[i] = 0;
         } else {
+            const int k = 2 * q + (lane >> 5);
+            const int c = (lane & 31) ^ (2 * (k & 3));
+            const uint16_t* base = Tr::group_k ? p.b : p.w[e];
+            b_ptr[i] = base + min(nt * BN + c * 8, p.N - 8);
+            b_k[i] = k;
+        }
+    }
+    const uint32_t lds0 = lds_addr(lds);
+    // Issue the 8 wave loads of K tile t (clamped to the last real tile so the
+    // per-tile load count stays constant) into stage t % NSTAGE.
+    auto dma_tile = [&](int t) {
+        const int k0 = kbeg + min(t, nk - 1) * BK;  // first reduction index of the tile
+        const uint32_t sbase = lds0 + (uint32_t)((t % NSTAGE) * STAGE) * 2u;
 #pragma unroll
-            for (int t = 0; t < 8; ++t) sb[t] = ld16(b_mc + (int64_t)(k0 + mc_kg * 8 + t) * p.ldb);
+        for (int i = 0; i < DMA_PER_OPND; ++i) {
+            const uint32_t qoff = (uint32_t)(wave * DMA_PER_OPND + i) * 1024u;
+            const uint16_t* ga = Tr::a_kc ? a_ptr[i] + k0
+                                          : a_ptr[i] + (int64_t)min(k0 + a_k[i], kend - 1) * p.lda;
+            const uint16_t* gb = Tr::b_kc ? b_ptr[i] + k0
+                                          : b_ptr[i] + (int64_t)min(k0 + b_k[i], kend - 1) * p.ldb;
+            dma16(ga, sbase + qoff);
+            dma16(gb, sbase + OPND * 2u + qoff);
         }
     };
-    // Store half `hf` (vectors 4hf..4hf+3) of the staged tile into LDS stage.
-    auto lstore_half = [&](int stage, int hf) {
-        uint16_t* ta = lds + stage * STAGE;
-        uint16_t* tb = ta + BM * BK;
-#pragma unroll
-        for (int i = 4 * hf; i < 4 * hf + 4; ++i) {
-            if constexpr (Tr::a_kc) {
-                const int r = kc_r + 32 * i;
-                *reinterpret_cast<uint4*>(ta + r * BK + swz(r, kc_ch) * 8) = sa[i];
-            } else {
-                const int r = mc_c8 * 8 + i;
-                *reinterpret_cast<uint4*>(ta + r * BK + swz(r, mc_kg) * 8) = column8(sa, i);
-            }
-            if constexpr (Tr::b_kc) {
-                const int r = kc_r + 32 * i;
-                *reinterpret_cast<uint4*>(tb + r * BK + swz(r, kc_ch) * 8) = sb[i];
-            } else {
-                const int r = mc_c8 * 8 + i;
-                *reinterpret_cast<uint4*>(tb + r * BK + swz(r, mc_kg) * 8) = column8(sb, i);
+    // Reduction tail of the weight-gradient GEMMs: zero k rows >= kvalid of
+    // the last tile in both operand tiles (rows of 512 bytes).
+    auto zero_tail = [&](int t) {
+        if constexpr (Tr::group_k) {
+            const int kvalid = kend - (kbeg + t * BK);
+            if (kvalid < BK) {
+                uint16_t* st = lds + (t % NSTAGE) * STAGE;
+                const int nvec = (BK - kvalid) * 32;  // 16-byte vectors per operand
+                for (int v = tid; v < 2 * nvec; v += kThreads) {
+                    const int opnd = v >= nvec, w = v - opnd * nvec;
+                    *reinterpret_cast<uint4*>(st + opnd * OPND + kvalid * 256 + w * 8) = make_uint4(0, 0, 0, 0);
+                }
             }
         }
+    };
+
+    // ---- fragments ----------------------------------------------------------
+    struct Frag {
+        uint4 a[MI], b[NJ];
+    };
+    // K-contiguous: lane reads row base + lane%32, chunk 2s + lane/32.
+    auto read_kc = [&](const uint16_t* t, int rbase, int s) {
+        const int r = rbase + (lane & 31);
+        const int c = (2 * s + (lane >> 5)) ^ ((r >> 1) & 3);
+        return *reinterpret_cast<const uint4*>(t + r * BK + c * 8);
+    };
+    // Row-contiguous: two transposing reads give k = 16s + 8(lane/32) + 0..7
+    // for column cbase + lane%32.
+    auto read_mc = [&](const uint16_t* t, int cbase, int s) {
+        const int g = lane >> 4, r = lane & 15;
+        const int col = cbase + 16 * (g & 1) + 4 * (r & 3);
+        const int kb = 16 * s + 8 * (g >> 1) + (r >> 2);
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = kb + 4 * h;
+            const int c = (col >> 3) ^ (2 * (k & 3));
+            const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (lds_s16x4*)(t + k * 256 + c * 8 + (col & 7)));
+            w[2 * h] = (uint32_t)(uint16_t)v[0] | ((uint32_t)(uint16_t)v[1] << 16);
+            w[2 * h + 1] = (uint32_t)(uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16);
+        }
+        return make_uint4(w[0], w[1], w[2], w[3]);
+    };
+    auto load_frag = [&](Frag& f, int t, int s) {
+        const uint16_t* tA = lds + (t % NSTAGE) * STAGE;
+        const uint16_t* tB = tA + OPND;
+#pragma unroll
+        for (int i = 0; i < MI; ++i)
+            f.a[i] = Tr::a_kc ? read_kc(tA, wm * WTM + 32 * i, s) : read_mc(tA, wm * WTM + 32 * i, s);
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            f.b[j] = Tr::b_kc ? read_kc(tB, wn * WTN + 32 * j, s) : read_mc(tB, wn * WTN + 32 * j, s);
     };
 
     f32x16 acc[MI][NJ];
@@ -259,26 +283,6 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
         for (int j = 0; j < NJ; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
-    // Fragments of one k16 step: A rows wm*128 + 32i + lane%32, B rows
-    // wn*128 + 32j + lane%32, 16-byte chunk 2s + lane/32.
-    struct Frag {
-        uint4 a[MI], b[NJ];
-    };
-    auto load_frag = [&](Frag& f, const uint16_t* tA, int s) {
-        const uint16_t* tB = tA + BM * BK;
-        const int chunk = s * 2 + (lane >> 5);
-#pragma unroll
-        for (int i = 0; i < MI; ++i) {
-            const int r = wm * WTM + i * 32 + (lane & 31);
-            f.a[i] = *reinterpret_cast<const uint4*>(tA + r * BK + swz(r, chunk) * 8);
-        }
-#pragma unroll
-        for (int j = 0; j < NJ; ++j) {
-            const int r = wn * WTN + j * 32 + (lane & 31);
-            f.b[j] = *reinterpret_cast<const uint4*>(tB + r * BK + swz(r, chunk) * 8);
-        }
-    };
     auto mma = [&](const Frag& f) {
 #pragma unroll
         for (int i = 0; i < MI; ++i)
@@ -289,68 +293,54 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
                     acc[i][j], 0, 0, 0);
     };
 
+    // ---- main loop ----------------------------------------------------------
+    // Iteration kt: phase A reads step-1 fragments of tile kt, issues the loads
+    // of tile kt+3 and runs step 0; phase B waits for this wave's loads of
+    // tile kt+1, synchronises the workgroup (all loads of tile kt+1 visible;
+    // every wave is done reading the stage phase A of kt+1 refills), reads
+    // step-0 fragments of tile kt+1 and runs step 1 of tile kt.
+    constexpr int VM_AHEAD = (NSTAGE - 2) * DMA_PER_TILE;
     if (nk > 0) {
-        fetch_src(kbeg);
-        gload(kbeg);
-        lstore_half(0, 0);
-        lstore_half(0, 1);
-        const int last_k0 = kbeg + (nk - 1) * BK;  // prefetches past the end re-read it
-        gload(min(kbeg + BK, last_k0));
+#pragma unroll
+        for (int t = 0; t < NSTAGE - 1; ++t) dma_tile(t);
+        wait_vm<VM_AHEAD>();
         __syncthreads();
+        if (nk == 1) {
+            zero_tail(0);
+            __syncthreads();
+        }
         Frag f0, f1;
+        load_frag(f0, 0, 0);
         for (int kt = 0; kt < nk; ++kt) {
-            const uint16_t* tA = lds + (kt & 1) * STAGE;
-            const int nxt = (kt + 1) & 1;
-            // The loop body is one basic block; the scheduling groups below pin
-            // the order: fragments for step s+1 are read while step s's 16
-            // MFMAs run, the next tile's LDS stores and the global loads of the
-            // tile after it are interleaved one per MFMA. Stores into the idle
-            // stage after the last tile are harmless.
-            load_frag(f0, tA, 0);
-            load_frag(f1, tA, 1);
-            __builtin_amdgcn_sched_barrier(0);
+            load_frag(f1, kt, 1);
+            dma_tile(kt + NSTAGE - 1);
             mma(f0);
-            lstore_half(nxt, 0);
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
             }
             __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
             __builtin_amdgcn_sched_barrier(0);
-            load_frag(f0, tA, 2);
-            mma(f1);
-            lstore_half(nxt, 1);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);  // DS read
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
-            }
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x200, 1, 1);  // DS write
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            load_frag(f1, tA, 3);
-            mma(f0);
-            gload(min(kbeg + (kt + 2) * BK, last_k0));
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 2);  // DS read
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);  // MFMA
-            }
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x020, 2, 2);  // VMEM read
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 2);  // MFMA
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            mma(f1);
-            __builtin_amdgcn_sched_barrier(0);
+            wait_vm<VM_AHEAD>();
             __syncthreads();
+            if (kt + 1 == nk - 1) {
+                zero_tail(kt + 1);
+                __syncthreads();
+            }
+            load_frag(f0, min(kt + 1, nk - 1), 0);
+            mma(f1);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+    wait_vm<0>();
+    __syncthreads();
 
     // ---- epilogue ---------------------------------------------------------
     // acc[i][j][r] = C[m][n] with m = wm*128 + 32i + (lane&31) and

@@ -64,7 +64,7 @@ struct tmt_moe {
     float *logits, *probs, *lse, *gate, *blkstat, *stats;
     int32_t *idx, *blkcnt, *blkbase, *counts, *offsets, *order, *perm, *slot_of;
     // activations
-    uint16_t *U, *Aact, *O, *dO, *dU, *dXg;
+    uint16_t *U, *Aact, *O, *dO, *dU, *dXg, *Xg;
     float *dlogits, *dwr_partial;
     int last_T = -1;
     // per-kernel event timing (tmt_moe_set_profiling)
@@ -133,6 +133,7 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
     size_t o_dO = L.add(TK * D * 2);
     size_t o_dU = h > 0 ? L.add(TK * h * 2) : 0;
     size_t o_dXg = L.add(TK * D * 2);
+    size_t o_Xg = L.add(TK * D * 2);
     size_t o_dl = L.add(T * E * 4);
     size_t o_dwr = L.add((size_t)router_dw_chunks((int)T) * E * D * 4);
     if (m) {
@@ -157,6 +158,7 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->dO = (uint16_t*)(a + o_dO);
         m->dU = h > 0 ? (uint16_t*)(a + o_dU) : m->dO;  // h == 0: combine_bwd writes dU
         m->dXg = (uint16_t*)(a + o_dXg);
+        m->Xg = (uint16_t*)(a + o_Xg);
         m->dlogits = (float*)(a + o_dl);
         m->dwr_partial = (float*)(a + o_dwr);
         m->nblk_max = (int)nblk;
@@ -398,6 +400,7 @@ int tmt_moe_backward(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_
         cb.gate = m->gate; cb.probs = m->probs; cb.lse = m->lse; cb.counts = m->counts;
         cb.T = T; cb.d = d; cb.E = E; cb.K = K; cb.silu = h == 0;
         cb.aux_coef = aux_coef; cb.z_coef = z_coef; cb.dO = m->dO; cb.dlogits = m->dlogits;
+        cb.X = X; cb.Xg = m->Xg;
         LAUNCH(TMT_MOE_PH_COMBINE_BWD, launch_combine_bwd(cb, s));
     }
     if (h > 0) {
@@ -420,7 +423,7 @@ int tmt_moe_backward(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_
     GemmParams dwu{};
     dwu.offsets = m->offsets; dwu.order = m->order; dwu.perm = m->perm; dwu.E = E;
     dwu.M = hn; dwu.N = d;
-    dwu.a = m->dU; dwu.lda = hn; dwu.b = X; dwu.ldb = d; dwu.ldc = d;
+    dwu.a = m->dU; dwu.lda = hn; dwu.b = m->Xg; dwu.ldb = d; dwu.ldc = d;
     for (int e = 0; e < E; ++e) dwu.dw[e] = dW_up[e];
     LAUNCH(TMT_MOE_PH_GEMM_DW_UP, launch_gemm(GEMM_DW_UP, false, dwu, s));
     if (T > 0) {

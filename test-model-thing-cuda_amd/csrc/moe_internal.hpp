@@ -117,6 +117,8 @@ struct CombineBwdParams {
     float aux_coef, z_coef;
     uint16_t* dO;            // [TK][d] gradient at the expert output
     float* dlogits;          // [T][E] (E > 1)
+    const uint16_t* X;       // [T][d] layer input
+    uint16_t* Xg;            // [TK][d] X gathered to slot order (dW_up operand)
 };
 hipError_t launch_combine_bwd(const CombineBwdParams& p, hipStream_t s);
 

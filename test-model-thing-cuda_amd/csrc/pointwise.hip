@@ -4,7 +4,8 @@
 //                (reference combine_kernel, tmt-cuda/src/moe.cu:142-158)
 //   combine_bwd  s_rj = dY_r . O[slot], dO[slot] = gate_rj * dY_r, and the
 //                router gradient of row r through renorm + softmax + aux + z
-//                (moe.cu:160-234, fused; one wave per token row)
+//                (moe.cu:160-234, fused; one wave per token row); also copies
+//                X_r to Xg[slot] (the reference's gather recompute, moe.cu:497-502)
 //   router_dw    dWr = dlogits^T X with a fixed-order two-pass reduction
 //                (moe.cu:521; no atomics)
 //   scatter      dX_r = sum_j dXg[slot(r,j)] + dlogits_r . Wr  (moe.cu:236-249
@@ -86,6 +87,8 @@ __global__ __launch_bounds__(kThreads) void combine_bwd_kernel(CombineBwdParams 
                     }
                 }
                 *reinterpret_cast<uint4*>(p.dO + pos * d + c0) = pack8(out);
+                *reinterpret_cast<uint4*>(p.Xg + pos * d + c0) =
+                    *reinterpret_cast<const uint4*>(p.X + (int64_t)r * d + c0);
             }
             s[j] = wave_sum(part);
         }
