@@ -30,23 +30,40 @@
 //
 // Epilogue: accumulators go through LDS (fp32, 16-byte chunks swizzled by
 // row) so every global store is a 16-byte vector and each output row is
-// written as one contiguous 256-byte (bf16) or 512-byte (fp32) run.
+// written as one contiguous 256-byte (bf16) or 512-byte (fp32) run; the
+// stores (and GEMM_DACT's pre-activation reads) are non-temporal.
 #include "device_util.hpp"
 #include "moe_internal.hpp"
 
 namespace tmt {
 namespace {
 
-constexpr int BK = 32;
 constexpr int BM = 256;
 constexpr int BN = 256;
-constexpr int NSTAGE = 4;
 constexpr int WTM = 128, WTN = 128;       // wave tile
 constexpr int MI = WTM / 32, NJ = WTN / 32;
-constexpr int OPND = 256 * BK;            // bf16 elements of one operand tile
-constexpr int STAGE = 2 * OPND;           // A then B
-constexpr int DMA_PER_OPND = 4;           // 1 KiB wave loads per operand tile per wave
-constexpr int DMA_PER_TILE = 2 * DMA_PER_OPND;
+constexpr int LDS_BYTES = 128 * 1024;     // LDS ring (and epilogue staging) per workgroup
+
+// K-step geometry. BK_ is the K depth of one LDS stage (32 or 64), NST the
+// number of stages in the ring.
+template <int BK_, int NST>
+struct Geo {
+    static constexpr int BK = BK_;
+    static constexpr int NSTAGE = NST;
+    static constexpr int KCH = BK / 8;                 // 16-byte chunks per K-contiguous row
+    static constexpr int OPND = 256 * BK;              // bf16 elements of one operand tile
+    static constexpr int STAGE = 2 * OPND;             // A then B
+    static constexpr int DMA_PER_OPND = OPND * 2 / 1024 / 4;  // 1 KiB wave loads per operand per wave
+    static constexpr int DMA_PER_TILE = 2 * DMA_PER_OPND;
+    static constexpr int KC_ROWS = 1024 / (2 * BK);    // K-contiguous rows per wave load
+    static constexpr int STEPS = BK / 16;              // MFMA k16 steps per stage
+    static_assert(NST * STAGE * 2 <= 160 * 1024, "LDS ring too large");
+    // K-contiguous rows: 16-byte chunk swizzle making 8 consecutive rows hit
+    // distinct banks for ds_read_b128.
+    static __device__ __forceinline__ int kc_swz(int r) {
+        return KCH == 4 ? ((r >> 1) & 3) : ((r ^ (r >> 3)) & 7);
+    }
+};
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -80,6 +97,21 @@ template <> struct Traits<GEMM_DW_UP> {
 
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// Streaming (non-temporal) 16-byte accesses for the epilogue: outputs are
+// written once and read by a later kernel, so they should not displace the
+// operand tiles the other workgroups are reusing from L2.
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st16_nt(void* p, uint4 v) {
+    __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(p));
+}
+__device__ __forceinline__ void st16_nt(void* p, f32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+}
+__device__ __forceinline__ uint4 ld16_nt(const uint16_t* p) {
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
 }
@@ -98,10 +130,15 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
 }
 
-template <int KIND, bool DUAL>
+template <int KIND, bool DUAL, int BK_, int NST>
 __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p) {
     using Tr = Traits<KIND>;
-    __shared__ uint4 lds_raw[NSTAGE * STAGE / 8];
+    using Gm = Geo<BK_, NST>;
+    constexpr int BK = Gm::BK, NSTAGE = Gm::NSTAGE, OPND = Gm::OPND, STAGE = Gm::STAGE;
+    constexpr int DMA_PER_OPND = Gm::DMA_PER_OPND, DMA_PER_TILE = Gm::DMA_PER_TILE;
+    constexpr int KCH = Gm::KCH, KC_ROWS = Gm::KC_ROWS, STEPS = Gm::STEPS;
+    static_assert(NSTAGE * STAGE * 2 <= LDS_BYTES + 32 * 1024, "LDS ring too large");
+    __shared__ uint4 lds_raw[(NSTAGE * STAGE * 2 > LDS_BYTES ? NSTAGE * STAGE * 2 : LDS_BYTES) / 16];
     uint16_t* lds = reinterpret_cast<uint16_t*>(lds_raw);
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -178,8 +215,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
     for (int i = 0; i < DMA_PER_OPND; ++i) {
         const int q = wave * DMA_PER_OPND + i;
         if constexpr (Tr::a_kc) {
-            const int r = 16 * q + (lane >> 2);
-            const int c = (lane & 3) ^ ((r >> 1) & 3);
+            const int r = KC_ROWS * q + lane / KCH;
+            const int c = (lane % KCH) ^ Gm::kc_swz(r);
             const int slot = min(row0 + r, p.slots - 1);
             const int src = Tr::gather ? p.perm[slot] : slot;
             a_ptr[i] = p.a + (int64_t)src * p.lda + c * 8;
@@ -191,8 +228,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             a_k[i] = k;
         }
         if constexpr (Tr::b_kc) {
-            const int r = 16 * q + (lane >> 2);
-            const int c = (lane & 3) ^ ((r >> 1) & 3);
+            const int r = KC_ROWS * q + lane / KCH;
+            const int c = (lane % KCH) ^ Gm::kc_swz(r);
             const int n = min(nt * BN + r, p.N - 1);
             b_ptr[i] = p.w[e] + (int64_t)n * p.ldb + c * 8;
             b_k[i] = 0;
@@ -244,7 +281,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
     // K-contiguous: lane reads row base + lane%32, chunk 2s + lane/32.
     auto read_kc = [&](const uint16_t* t, int rbase, int s) {
         const int r = rbase + (lane & 31);
-        const int c = (2 * s + (lane >> 5)) ^ ((r >> 1) & 3);
+        const int c = (2 * s + (lane >> 5)) ^ Gm::kc_swz(r);
         return *reinterpret_cast<const uint4*>(t + r * BK + c * 8);
     };
     // Row-contiguous: two transposing reads give k = 16s + 8(lane/32) + 0..7
@@ -294,42 +331,50 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
     };
 
     // ---- main loop ----------------------------------------------------------
-    // Iteration kt: phase A reads step-1 fragments of tile kt, issues the loads
-    // of tile kt+3 and runs step 0; phase B waits for this wave's loads of
-    // tile kt+1, synchronises the workgroup (all loads of tile kt+1 visible;
-    // every wave is done reading the stage phase A of kt+1 refills), reads
-    // step-0 fragments of tile kt+1 and runs step 1 of tile kt.
+    // Iteration kt runs the STEPS k16 steps of tile kt. Every step first reads
+    // the next step's fragments; the first step also issues the loads of
+    // tile kt + NSTAGE - 1. Before the last step the wave waits for its loads
+    // of tile kt+1 and the workgroup synchronises (all loads of tile kt+1 are
+    // visible, and every wave is done reading the stage that the next
+    // iteration refills); the last step then prefetches step 0 of tile kt+1.
     constexpr int VM_AHEAD = (NSTAGE - 2) * DMA_PER_TILE;
     if (nk > 0) {
 #pragma unroll
         for (int t = 0; t < NSTAGE - 1; ++t) dma_tile(t);
-        wait_vm<VM_AHEAD>();
+        wait_vm<(NSTAGE >= 2 ? VM_AHEAD : 0)>();
         __syncthreads();
         if (nk == 1) {
             zero_tail(0);
             __syncthreads();
         }
-        Frag f0, f1;
-        load_frag(f0, 0, 0);
+        Frag f[2];
+        load_frag(f[0], 0, 0);
         for (int kt = 0; kt < nk; ++kt) {
-            load_frag(f1, kt, 1);
-            dma_tile(kt + NSTAGE - 1);
-            mma(f0);
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+            for (int s = 0; s < STEPS - 1; ++s) {
+                load_frag(f[(s + 1) & 1], kt, s + 1);
+                if (s == 0) dma_tile(kt + NSTAGE - 1);
+                mma(f[s & 1]);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            wait_vm<VM_AHEAD>();
+            if constexpr (NSTAGE == 2) {
+                wait_vm<0>();
+            } else {
+                wait_vm<VM_AHEAD>();
+            }
             __syncthreads();
             if (kt + 1 == nk - 1) {
                 zero_tail(kt + 1);
                 __syncthreads();
             }
-            load_frag(f0, min(kt + 1, nk - 1), 0);
-            mma(f1);
+            load_frag(f[0], min(kt + 1, nk - 1), 0);
+            mma(f[1]);
 #pragma unroll
             for (int q = 0; q < 8; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
@@ -370,10 +415,21 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             // 16 lanes per row (8 bf16 each), 4 rows per instruction
             uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
             const int cl = lane & 15;
-#pragma unroll 4
-            for (int rr = lane >> 4; rr < 64; rr += 4) {
+            const int n = nbase + cl * 8;
+            uint4 uin[16];  // GEMM_DACT: pre-activations, all loads issued first
+            if constexpr (KIND == GEMM_DACT) {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) {
+                    const int m = mbase + pass * 64 + (lane >> 4) + 4 * k;
+                    const bool ok = m < mlim && n < nlim;
+                    const int64_t off = (int64_t)(row0 + (ok ? m : 0)) * p.ldc + nt * BN + (ok ? n : 0);
+                    uin[k] = ld16_nt(p.u + off);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                const int rr = (lane >> 4) + 4 * k;
                 const int m = mbase + pass * 64 + rr;
-                const int n = nbase + cl * 8;
                 if (m >= mlim || n >= nlim) continue;
                 const float* src = stage_f + rr * 128;
                 const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + (((2 * cl) ^ (rr & 31)) * 4));
@@ -382,15 +438,15 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
                 const int64_t off = (int64_t)(row0 + m) * p.ldc + nt * BN + n;
                 if constexpr (KIND == GEMM_DACT) {
                     float u[8];
-                    unpack8(ld16(p.u + off), u);
+                    unpack8(uin[k], u);
 #pragma unroll
                     for (int t = 0; t < 8; ++t) v[t] *= dsilu_fast(u[t]);
                 }
-                *reinterpret_cast<uint4*>(C + off) = pack8(v);
+                st16_nt(C + off, pack8(v));
                 if constexpr (DUAL) {
 #pragma unroll
                     for (int t = 0; t < 8; ++t) v[t] = silu_fast(v[t]);
-                    *reinterpret_cast<uint4*>(p.c2 + off) = pack8(v);
+                    st16_nt(p.c2 + off, pack8(v));
                 }
             }
         } else {
@@ -403,7 +459,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
                 const int n = nbase + cl * 4;
                 if (m >= mlim || n >= nlim) continue;
                 const f32x4 v = *reinterpret_cast<const f32x4*>(stage_f + rr * 128 + ((cl ^ (rr & 31)) * 4));
-                *reinterpret_cast<f32x4*>(C + (int64_t)(mt * BM + m) * p.ldc + nt * BN + n) = v;
+                st16_nt(C + (int64_t)(mt * BM + m) * p.ldc + nt * BN + n, v);
             }
         }
         __syncthreads();
@@ -411,6 +467,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
 }
 
 }  // namespace
+
+constexpr int kBK = 32, kNST = 4;  // chosen by the K-step sweep (see the design notes)
 
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s) {
     if (p.N % 8 != 0 || p.N <= 0) return hipErrorInvalidValue;
@@ -425,7 +483,7 @@ hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_
         const int64_t ntm = (p.M + BM - 1) / BM;
         groups = (int64_t)p.E * ((ntm + gm - 1) / gm) * ngn;
     } else {
-        if (p.K % BK != 0) return hipErrorInvalidValue;
+        if (p.K % kBK != 0) return hipErrorInvalidValue;
         // sum_e ceil(cnt_e / BM) <= ceil(slots / BM) + E - 1
         const int64_t mtiles = (int64_t)(p.slots + BM - 1) / BM + p.E;
         groups = ((mtiles + gm - 1) / gm) * ngn;
@@ -437,14 +495,14 @@ hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_
     const unsigned g = (unsigned)grid;
     switch (kind) {
         case GEMM_UP:
-            if (dual) grouped_gemm_kernel<GEMM_UP, true><<<g, block, 0, s>>>(p);
-            else grouped_gemm_kernel<GEMM_UP, false><<<g, block, 0, s>>>(p);
+            if (dual) grouped_gemm_kernel<GEMM_UP, true, kBK, kNST><<<g, block, 0, s>>>(p);
+            else grouped_gemm_kernel<GEMM_UP, false, kBK, kNST><<<g, block, 0, s>>>(p);
             break;
-        case GEMM_DOWN: grouped_gemm_kernel<GEMM_DOWN, false><<<g, block, 0, s>>>(p); break;
-        case GEMM_DACT: grouped_gemm_kernel<GEMM_DACT, false><<<g, block, 0, s>>>(p); break;
-        case GEMM_DX: grouped_gemm_kernel<GEMM_DX, false><<<g, block, 0, s>>>(p); break;
-        case GEMM_DW_DOWN: grouped_gemm_kernel<GEMM_DW_DOWN, false><<<g, block, 0, s>>>(p); break;
-        case GEMM_DW_UP: grouped_gemm_kernel<GEMM_DW_UP, false><<<g, block, 0, s>>>(p); break;
+        case GEMM_DOWN: grouped_gemm_kernel<GEMM_DOWN, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
+        case GEMM_DACT: grouped_gemm_kernel<GEMM_DACT, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
+        case GEMM_DX: grouped_gemm_kernel<GEMM_DX, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
+        case GEMM_DW_DOWN: grouped_gemm_kernel<GEMM_DW_DOWN, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
+        case GEMM_DW_UP: grouped_gemm_kernel<GEMM_DW_UP, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
