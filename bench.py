@@ -83,6 +83,43 @@ def cpu_baseline(case, cfg, target_s=15.0, max_threads=16):
                       f"workload with all 16 experts, {dt:.1f} s wall, fp32 C++ on {threads} threads"}
 
 
+def bench_mxfp4(stream, reps=5):
+    """c5: MXFP4 experts forward (T=65536, d=1024, E=32, top-4, h=4096)."""
+    import numpy as np
+    import torch
+
+    import tmt_moe
+    from synthetic import CONFIGS, make_case, mxfp4_experts
+
+    cfg = CONFIGS["c5"]
+    T, d, E, K, h = (cfg[k] for k in ("T", "d", "E", "K", "h"))
+    case = make_case(T, d, E, K, h, with_dy=False)
+    qu, qd = mxfp4_experts(case["W_up"]), mxfp4_experts(case["W_down"])
+    dev16 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+    dev8 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    X, Wr = dev16(case["X"]), dev16(case["Wr"])
+    cu, su, cd, sd = dev8(qu["codes"]), dev8(qu["scales"]), dev8(qd["codes"]), dev8(qd["scales"])
+    Y = torch.zeros(T, d, dtype=torch.bfloat16, device="cuda")
+    m = tmt_moe.MoE(T, d, E, K, h, weight_format=tmt_moe.WEIGHTS_MXFP4)
+    for _ in range(2):
+        m.forward_mxfp4(X, Wr, cu, su, cd, sd, Y, beta=0.0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        m.forward_mxfp4(X, Wr, cu, su, cd, sd, Y, beta=0.0)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    m.close()
+    flops = 2 * T * d * E + 4 * T * K * d * h
+    return {"workload": f"c5: MXFP4 experts forward T={T} d={d} E={E} top-{K} h={h}",
+            "ms": round(ms, 4), "tokens_per_s": round(T / (ms / 1e3), 1),
+            "tflops": round(flops / (ms / 1e3) / 1e12, 1),
+            "mfma_frac_bf16_peak": round(flops / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "note": "weights streamed as e2m1+e8m0 and expanded to bf16 for bf16 MFMA"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,6 +128,7 @@ def main():
     ap.add_argument("--config", default="c3")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-fp4", action="store_true", help="skip the c5 MXFP4 forward measurement")
     ap.add_argument("--no-profile", action="store_true",
                     help="time the step without per-kernel events")
     args = ap.parse_args()
@@ -205,6 +243,10 @@ def main():
                                 "hbm_gbs": round(wbytes / (us * 1e-6) / 1e9, 1)}
         md.close()
 
+    fp4 = None
+    if not args.no_fp4 and args.config == "c3":
+        fp4 = bench_mxfp4(stream)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(case, cfg)
@@ -234,6 +276,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kernels,
         "decode": decode,
+        "mxfp4_forward": fp4,
         "aux": round(aux, 6),
         "z": round(z, 6),
     }

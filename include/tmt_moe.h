@@ -86,9 +86,16 @@ int tmt_moe_forward(tmt_moe* moe, void* stream, int32_t T, const uint16_t* X,
 
 /*
  * MXFP4 variant of tmt_moe_forward for weight_format == TMT_MOE_WEIGHTS_MXFP4
- * (no reference counterpart: the reference has no FP4 path).
- * W_up[e]: packed e2m1 [h][d/2] bytes (low nibble = even column) with
- * W_up_scale[e]: e8m0 [h][d/32]; W_down[e]: [d][h/2] with scales [d][h/32].
+ * (no reference counterpart: the reference has no FP4 path). OCP MX format:
+ * e2m1 values in blocks of 32 along the reduction dimension sharing one e8m0
+ * scale 2^(s-127). Per expert e:
+ *   W_up[e]        packed codes [h][d/2] bytes, low nibble = even column
+ *   W_up_scale[e]  scales [d/32][h] bytes (block-major: the scales of one
+ *                  K block are contiguous over the output rows)
+ *   W_down[e]      [d][h/2] bytes,  W_down_scale[e]  [h/32][d] bytes.
+ * Activations stay bf16; weights are expanded to bf16 (exactly) inside the
+ * GEMM, so the result matches the fp32 product with dequantised weights.
+ * Forward only: backward needs bf16 master weights.
  */
 int tmt_moe_forward_mxfp4(tmt_moe* moe, void* stream, int32_t T,
                           const uint16_t* X, const uint16_t* Wr,

@@ -72,28 +72,56 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 template <int KIND> struct Traits;
 // C[slot][n] = X[perm[slot]] . W_up[e][n]              A: K-contig (gathered), B: K-contig
 template <> struct Traits<GEMM_UP> {
-    static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = true;
+    static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = true, b_fp4 = false;
 };
 // C[slot][n] = A[slot] . W_down[e][n]
 template <> struct Traits<GEMM_DOWN> {
-    static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = false;
+    static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = false, b_fp4 = false;
 };
 // C[slot][n] = (dO[slot] . W_down[e][:, n]) * silu'(U)  B: [K][N]
 template <> struct Traits<GEMM_DACT> {
-    static constexpr bool group_k = false, a_kc = true, b_kc = false, gather = false;
+    static constexpr bool group_k = false, a_kc = true, b_kc = false, gather = false, b_fp4 = false;
 };
 // C[slot][n] = dU[slot] . W_up[e][:, n]                 B: [K][N]
 template <> struct Traits<GEMM_DX> {
-    static constexpr bool group_k = false, a_kc = true, b_kc = false, gather = false;
+    static constexpr bool group_k = false, a_kc = true, b_kc = false, gather = false, b_fp4 = false;
 };
 // dW_down[e][m][n] = sum_slot dO[slot][m] * A[slot][n]
 template <> struct Traits<GEMM_DW_DOWN> {
-    static constexpr bool group_k = true, a_kc = false, b_kc = false, gather = false;
+    static constexpr bool group_k = true, a_kc = false, b_kc = false, gather = false, b_fp4 = false;
 };
 // dW_up[e][m][n] = sum_slot dU[slot][m] * Xg[slot][n]   (Xg: X gathered to slot order)
 template <> struct Traits<GEMM_DW_UP> {
-    static constexpr bool group_k = true, a_kc = false, b_kc = false, gather = false;
+    static constexpr bool group_k = true, a_kc = false, b_kc = false, gather = false, b_fp4 = false;
 };
+
+// MXFP4 variants: same as GEMM_UP / GEMM_DOWN, B = e2m1 weights + e8m0 scales.
+template <> struct Traits<GEMM_UP_FP4> {
+    static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = true, b_fp4 = true;
+};
+template <> struct Traits<GEMM_DOWN_FP4> {
+    static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = false, b_fp4 = true;
+};
+
+// e2m1 code (bit 3 = sign) times 2^(scale - 127) as bf16 bits. The e2m1
+// magnitudes {0, .5, 1, 1.5, 2, 3, 4, 6} have at most two significant bits,
+// so the bf16 value is exact while the scaled exponent stays in range.
+__device__ __forceinline__ uint32_t e2m1_bf16(uint32_t c, int dexp) {
+    const uint32_t m = c & 7u;
+    const uint64_t lut = (m & 4u) ? 0x40C0408040404000ull : 0x3FC03F803F000000ull;
+    uint32_t bits = (uint32_t)(lut >> ((m & 3u) * 16)) & 0xffffu;
+    bits = bits ? (uint32_t)((int)bits + (dexp << 7)) : 0u;
+    return bits | ((c & 8u) << 12);
+}
+// 8 codes (low nibble first) with one shared scale -> 8 bf16.
+__device__ __forceinline__ uint4 dequant8(uint32_t w, uint32_t scale) {
+    const int dexp = (int)scale - 127;
+    uint32_t o[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        o[q] = e2m1_bf16((w >> (8 * q)) & 15u, dexp) | (e2m1_bf16((w >> (8 * q + 4)) & 15u, dexp) << 16);
+    return make_uint4(o[0], o[1], o[2], o[3]);
+}
 
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
@@ -121,7 +149,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // M0 is written here and declared clobbered (clang warns that it is reserved).
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const uint16_t* g, uint32_t lds_base) {
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "m0");
 }
 #pragma clang diagnostic pop
@@ -134,8 +162,14 @@ template <int KIND, bool DUAL, int BK_, int NST>
 __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p) {
     using Tr = Traits<KIND>;
     using Gm = Geo<BK_, NST>;
-    constexpr int BK = Gm::BK, NSTAGE = Gm::NSTAGE, OPND = Gm::OPND, STAGE = Gm::STAGE;
-    constexpr int DMA_PER_OPND = Gm::DMA_PER_OPND, DMA_PER_TILE = Gm::DMA_PER_TILE;
+    constexpr int BK = Gm::BK, NSTAGE = Gm::NSTAGE, OPND = Gm::OPND;
+    constexpr int DMA_PER_OPND = Gm::DMA_PER_OPND;
+    // MXFP4 B operand per stage: 256 rows x 16 bytes of codes (BK = 32 = one
+    // scale block), then one 1 KiB copy of the 256 row scales per wave.
+    static_assert(!Tr::b_fp4 || BK == 32, "MXFP4 tiles cover exactly one scale block");
+    constexpr int FP4_CODES = 256 * 16, FP4_SCALES = 4 * 1024;
+    constexpr int STAGE = Tr::b_fp4 ? OPND + (FP4_CODES + FP4_SCALES) / 2 : Gm::STAGE;  // bf16 elements
+    constexpr int DMA_PER_TILE = Tr::b_fp4 ? DMA_PER_OPND + 2 : Gm::DMA_PER_TILE;
     constexpr int KCH = Gm::KCH, KC_ROWS = Gm::KC_ROWS, STEPS = Gm::STEPS;
     static_assert(NSTAGE * STAGE * 2 <= LDS_BYTES + 32 * 1024, "LDS ring too large");
     __shared__ uint4 lds_raw[(NSTAGE * STAGE * 2 > LDS_BYTES ? NSTAGE * STAGE * 2 : LDS_BYTES) / 16];
@@ -227,7 +261,10 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             a_ptr[i] = p.a + min(mt * BM + c * 8, p.M - 8);
             a_k[i] = k;
         }
-        if constexpr (Tr::b_kc) {
+        if constexpr (Tr::b_fp4) {
+            b_ptr[i] = nullptr;
+            b_k[i] = 0;
+        } else if constexpr (Tr::b_kc) {
             const int r = KC_ROWS * q + lane / KCH;
             const int c = (lane % KCH) ^ Gm::kc_swz(r);
             const int n = min(nt * BN + r, p.N - 1);
@@ -240,6 +277,17 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             b_ptr[i] = base + min(nt * BN + c * 8, p.N - 8);
             b_k[i] = k;
         }
+    }
+    // MXFP4: wave w loads the codes of rows 64w + lane (16 bytes per tile) and
+    // its own copy of the tile's 256 row scales (lane l -> rows 16(l%16)..+15;
+    // row groups past N are clamped to the tile's first group).
+    const uint8_t* q_ptr = nullptr;
+    const uint8_t* sc_ptr = nullptr;
+    if constexpr (Tr::b_fp4) {
+        const int n = min(nt * BN + 64 * wave + lane, p.N - 1);
+        q_ptr = p.wq[e] + (int64_t)n * (p.K / 2);
+        const int g = nt * BN + 16 * (lane & 15);
+        sc_ptr = p.wsc[e] + (g < p.N ? g : nt * BN);
     }
     const uint32_t lds0 = lds_addr(lds);
     // Issue the 8 wave loads of K tile t (clamped to the last real tile so the
@@ -255,7 +303,12 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             const uint16_t* gb = Tr::b_kc ? b_ptr[i] + k0
                                           : b_ptr[i] + (int64_t)min(k0 + b_k[i], kend - 1) * p.ldb;
             dma16(ga, sbase + qoff);
-            dma16(gb, sbase + OPND * 2u + qoff);
+            if constexpr (!Tr::b_fp4) dma16(gb, sbase + OPND * 2u + qoff);
+        }
+        if constexpr (Tr::b_fp4) {
+            const int kb = k0 / 32;  // scale block of this tile
+            dma16(q_ptr + kb * 16, sbase + OPND * 2u + (uint32_t)wave * 1024u);
+            dma16(sc_ptr + (int64_t)kb * p.N, sbase + OPND * 2u + FP4_CODES + (uint32_t)wave * 1024u);
         }
     };
     // Reduction tail of the weight-gradient GEMMs: zero k rows >= kvalid of
@@ -302,6 +355,16 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
         }
         return make_uint4(w[0], w[1], w[2], w[3]);
     };
+    // MXFP4: lane reads 4 bytes (8 codes: k = 16s + 8(lane/32) .. +7) of row
+    // rbase + lane%32 and that row's scale from its wave's copy, and expands
+    // them to a bf16 fragment.
+    auto read_fp4 = [&](const uint16_t* tB, int rbase, int s) {
+        const uint8_t* codes = reinterpret_cast<const uint8_t*>(tB);
+        const uint8_t* scales = codes + FP4_CODES + wave * 1024;
+        const int r = rbase + (lane & 31);
+        const uint32_t w = *reinterpret_cast<const uint32_t*>(codes + r * 16 + (2 * s + (lane >> 5)) * 4);
+        return dequant8(w, scales[r]);
+    };
     auto load_frag = [&](Frag& f, int t, int s) {
         const uint16_t* tA = lds + (t % NSTAGE) * STAGE;
         const uint16_t* tB = tA + OPND;
@@ -310,7 +373,8 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             f.a[i] = Tr::a_kc ? read_kc(tA, wm * WTM + 32 * i, s) : read_mc(tA, wm * WTM + 32 * i, s);
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
-            f.b[j] = Tr::b_kc ? read_kc(tB, wn * WTN + 32 * j, s) : read_mc(tB, wn * WTN + 32 * j, s);
+            f.b[j] = Tr::b_fp4 ? read_fp4(tB, wn * WTN + 32 * j, s)
+                               : (Tr::b_kc ? read_kc(tB, wn * WTN + 32 * j, s) : read_mc(tB, wn * WTN + 32 * j, s));
     };
 
     f32x16 acc[MI][NJ];
@@ -474,6 +538,7 @@ hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_
     if (p.N % 8 != 0 || p.N <= 0) return hipErrorInvalidValue;
     dim3 block(kThreads);
     const bool group_k = kind == GEMM_DW_DOWN || kind == GEMM_DW_UP;
+    if ((kind == GEMM_UP_FP4 || kind == GEMM_DOWN_FP4) && p.K % 32 != 0) return hipErrorInvalidValue;
     const int64_t ntn = (p.N + BN - 1) / BN;
     const int64_t gn = ntn < 8 ? ntn : 8, gm = 32 / gn;
     const int64_t ngn = (ntn + gn - 1) / gn;
@@ -503,6 +568,11 @@ hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_
         case GEMM_DX: grouped_gemm_kernel<GEMM_DX, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
         case GEMM_DW_DOWN: grouped_gemm_kernel<GEMM_DW_DOWN, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
         case GEMM_DW_UP: grouped_gemm_kernel<GEMM_DW_UP, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
+        case GEMM_UP_FP4:
+            if (dual) grouped_gemm_kernel<GEMM_UP_FP4, true, 32, kNST><<<g, block, 0, s>>>(p);
+            else grouped_gemm_kernel<GEMM_UP_FP4, false, 32, kNST><<<g, block, 0, s>>>(p);
+            break;
+        case GEMM_DOWN_FP4: grouped_gemm_kernel<GEMM_DOWN_FP4, false, 32, kNST><<<g, block, 0, s>>>(p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -130,12 +130,14 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
     size_t o_U = L.add(TK * hn * 2);
     size_t o_A = h > 0 ? L.add(TK * h * 2) : 0;
     size_t o_O = h > 0 ? L.add(TK * D * 2) : 0;
-    size_t o_dO = L.add(TK * D * 2);
-    size_t o_dU = h > 0 ? L.add(TK * h * 2) : 0;
-    size_t o_dXg = L.add(TK * D * 2);
-    size_t o_Xg = L.add(TK * D * 2);
-    size_t o_dl = L.add(T * E * 4);
-    size_t o_dwr = L.add((size_t)router_dw_chunks((int)T) * E * D * 4);
+    // MXFP4 handles are forward-only: no backward buffers.
+    const bool bwd = d->weight_format == TMT_MOE_WEIGHTS_BF16;
+    size_t o_dO = bwd ? L.add(TK * D * 2) : 0;
+    size_t o_dU = bwd && h > 0 ? L.add(TK * h * 2) : 0;
+    size_t o_dXg = bwd ? L.add(TK * D * 2) : 0;
+    size_t o_Xg = bwd ? L.add(TK * D * 2) : 0;
+    size_t o_dl = bwd ? L.add(T * E * 4) : 0;
+    size_t o_dwr = bwd ? L.add((size_t)router_dw_chunks((int)T) * E * D * 4) : 0;
     if (m) {
         char* a = m->arena;
         m->logits = (float*)(a + o_logits);
@@ -155,12 +157,12 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->U = (uint16_t*)(a + o_U);
         m->Aact = h > 0 ? (uint16_t*)(a + o_A) : nullptr;
         m->O = h > 0 ? (uint16_t*)(a + o_O) : nullptr;
-        m->dO = (uint16_t*)(a + o_dO);
-        m->dU = h > 0 ? (uint16_t*)(a + o_dU) : m->dO;  // h == 0: combine_bwd writes dU
-        m->dXg = (uint16_t*)(a + o_dXg);
-        m->Xg = (uint16_t*)(a + o_Xg);
-        m->dlogits = (float*)(a + o_dl);
-        m->dwr_partial = (float*)(a + o_dwr);
+        m->dO = bwd ? (uint16_t*)(a + o_dO) : nullptr;
+        m->dU = bwd ? (h > 0 ? (uint16_t*)(a + o_dU) : m->dO) : nullptr;  // h == 0: combine_bwd writes dU
+        m->dXg = bwd ? (uint16_t*)(a + o_dXg) : nullptr;
+        m->Xg = bwd ? (uint16_t*)(a + o_Xg) : nullptr;
+        m->dlogits = bwd ? (float*)(a + o_dl) : nullptr;
+        m->dwr_partial = bwd ? (float*)(a + o_dwr) : nullptr;
         m->nblk_max = (int)nblk;
     }
     return L.total;
@@ -363,10 +365,44 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
                           const uint8_t* const* W_up, const uint8_t* const* W_up_scale,
                           const uint8_t* const* W_down, const uint8_t* const* W_down_scale,
                           uint16_t* Y, float beta) {
-    (void)stream; (void)T; (void)X; (void)Wr; (void)logit_bias; (void)W_up; (void)W_up_scale;
-    (void)W_down; (void)W_down_scale; (void)Y; (void)beta;
     if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
-    return fail(TMT_MOE_EINVAL, "MXFP4 expert path is not available in this build");
+    const tmt_moe_desc& ds = m->desc;
+    if (ds.weight_format != TMT_MOE_WEIGHTS_MXFP4)
+        return fail(TMT_MOE_EINVAL, "handle expects bf16 weights: use tmt_moe_forward");
+    if (T < 0 || T > ds.max_tokens) return fail(TMT_MOE_EINVAL, "T=%d outside [0, %d]", T, ds.max_tokens);
+    const int E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden;
+    if (T > 0 && (!X || !Y)) return fail(TMT_MOE_EINVAL, "X and Y must be non-NULL");
+    if (!aligned16(X) || !aligned16(Y)) return fail(TMT_MOE_EINVAL, "X and Y must be 16-byte aligned");
+    if (E > 1 && (!Wr || !aligned16(Wr))) return fail(TMT_MOE_EINVAL, "Wr must be a 16-byte aligned pointer when experts > 1");
+    int rc;
+    if ((rc = check_ptrs((const void* const*)W_up, E, "W_up"))) return rc;
+    if ((rc = check_ptrs((const void* const*)W_up_scale, E, "W_up_scale"))) return rc;
+    if ((rc = check_ptrs((const void* const*)W_down, E, "W_down"))) return rc;
+    if ((rc = check_ptrs((const void* const*)W_down_scale, E, "W_down_scale"))) return rc;
+    if ((rc = check_device(m))) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    m->last_T = -1;
+    if ((rc = route(m, s, T, X, Wr, logit_bias))) return rc;
+    if (T > 0) {
+        GemmParams up{};
+        up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
+        up.N = h; up.K = d; up.slots = T * K;
+        up.a = X; up.lda = d; up.c = m->U; up.ldc = h; up.c2 = m->Aact;
+        for (int e = 0; e < E; ++e) { up.wq[e] = W_up[e]; up.wsc[e] = W_up_scale[e]; }
+        LAUNCH(TMT_MOE_PH_GEMM_UP, launch_gemm(GEMM_UP_FP4, true, up, s));
+        GemmParams dn{};
+        dn.offsets = m->offsets; dn.order = m->order; dn.perm = m->perm; dn.E = E;
+        dn.N = d; dn.K = h; dn.slots = T * K;
+        dn.a = m->Aact; dn.lda = h; dn.c = m->O; dn.ldc = d;
+        for (int e = 0; e < E; ++e) { dn.wq[e] = W_down[e]; dn.wsc[e] = W_down_scale[e]; }
+        LAUNCH(TMT_MOE_PH_GEMM_DOWN, launch_gemm(GEMM_DOWN_FP4, false, dn, s));
+        CombineParams cp{};
+        cp.O = m->O; cp.slot_of = m->slot_of; cp.gate = m->gate;
+        cp.Y = Y; cp.beta = beta; cp.T = T; cp.d = d; cp.K = K; cp.silu = 0;
+        LAUNCH(TMT_MOE_PH_COMBINE, launch_combine(cp, s));
+    }
+    m->last_T = T;
+    return TMT_MOE_OK;
 }
 
 int tmt_moe_backward(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_t* X,

@@ -68,7 +68,9 @@ enum GemmKind {
     GEMM_DACT = 2,     // C = (dO W_down) * silu'(U)
     GEMM_DX = 3,       // C = dU W_up
     GEMM_DW_DOWN = 4,  // dW_down[e] = dO^T A            (reduction over slots)
-    GEMM_DW_UP = 5     // dW_up[e]   = dU^T gather(X)    (reduction over slots)
+    GEMM_DW_UP = 5,    // dW_up[e]   = dU^T Xg           (reduction over slots)
+    GEMM_UP_FP4 = 6,   // GEMM_UP with MXFP4 weights dequantised to bf16 in registers
+    GEMM_DOWN_FP4 = 7  // GEMM_DOWN with MXFP4 weights
 };
 
 struct GemmParams {
@@ -87,6 +89,8 @@ struct GemmParams {
     const uint16_t* u;                // pre-activation for GEMM_DACT
     const uint16_t* w[kMaxExperts];   // per-expert weights (activation GEMMs)
     float* dw[kMaxExperts];           // per-expert fp32 outputs (dW GEMMs)
+    const uint8_t* wq[kMaxExperts];   // MXFP4 weights: packed e2m1 [N][K/2] (low nibble = even k)
+    const uint8_t* wsc[kMaxExperts];  // MXFP4 scales: e8m0 [K/32][N]
 };
 // Grid size the launcher will use (for tests of the tile bound).
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s);

@@ -44,6 +44,46 @@ def bf16_to_f32(b: np.ndarray) -> np.ndarray:
     return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
+# e2m1 rounding boundaries between consecutive codes 0..7 (magnitudes
+# 0, .5, 1, 1.5, 2, 3, 4, 6); a value exactly on a boundary goes to the even code.
+_E2M1_BOUNDS = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], np.float32)
+
+
+def mxfp4_quantize(w: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """OCP MXFP4 quantisation of fp32 rows (length a multiple of 32).
+
+    Returns (codes [rows][n/2] uint8, low nibble = even element;
+             scales [rows][n/32] uint8, e8m0). Scale exponent
+    floor(log2(amax)) - 2 per block of 32, elements rounded to the nearest
+    e2m1 value (ties to the even code), saturating at 6."""
+    w = np.ascontiguousarray(w, np.float32)
+    rows, n = w.reshape(-1, w.shape[-1]).shape
+    blocks = w.reshape(rows, n // 32, 32)
+    amax = np.abs(blocks).max(axis=2)
+    _, ex = np.frexp(amax)                      # amax = f * 2^ex, f in [0.5, 1)
+    se = np.where(amax > 0, np.clip(ex.astype(np.int32) - 3, -127, 127), 0)
+    scaled = blocks * np.ldexp(np.float32(1.0), -se)[:, :, None].astype(np.float32)
+    a = np.abs(scaled)
+    code = np.zeros(a.shape, np.uint8)
+    for k, b in enumerate(_E2M1_BOUNDS):
+        code += ((a > b) if k % 2 == 0 else (a >= b)).astype(np.uint8)
+    code |= np.signbit(scaled).astype(np.uint8) << 3
+    code = code.reshape(rows, n)
+    packed = (code[:, 0::2] | (code[:, 1::2] << 4)).astype(np.uint8)
+    scales = (se + 127).astype(np.uint8)
+    return packed.reshape(*w.shape[:-1], n // 2), scales.reshape(*w.shape[:-1], n // 32)
+
+
+def mxfp4_dequantize(packed: np.ndarray, scales: np.ndarray) -> np.ndarray:
+    """Exact inverse of the code/scale encoding (fp32)."""
+    grid = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6], np.float32)
+    lo, hi = packed & 15, packed >> 4
+    codes = np.stack([lo, hi], axis=-1).reshape(*packed.shape[:-1], packed.shape[-1] * 2)
+    v = grid[codes]
+    sc = np.ldexp(np.float32(1.0), scales.astype(np.int32) - 127).astype(np.float32)
+    return v * np.repeat(sc, 32, axis=-1)
+
+
 def _normal(rng: np.random.Generator, shape, std: float) -> np.ndarray:
     return bf16_bits(rng.standard_normal(shape, dtype=np.float32) * np.float32(std))
 
@@ -72,6 +112,17 @@ def zipf_bias(X: np.ndarray, Wr: np.ndarray, K: int, s: float = 1.1,
             hi = mid
     alpha = 0.5 * (lo + hi)
     return (alpha * prof).astype(np.float32), alpha
+
+
+def mxfp4_experts(W: np.ndarray) -> dict:
+    """Quantise bf16 expert weights [E][N][K] to the library's MXFP4 layout:
+    codes [E][N][K/2] and block-major scales [E][K/32][N]; also returns the
+    exactly dequantised weights as bf16 bits (the reference operand)."""
+    packed, scales = mxfp4_quantize(bf16_to_f32(W))
+    deq = mxfp4_dequantize(packed, scales)
+    return {"codes": np.ascontiguousarray(packed),
+            "scales": np.ascontiguousarray(np.swapaxes(scales, -1, -2)),
+            "deq_bf16": bf16_bits(deq)}
 
 
 def make_case(T: int, d: int, E: int, K: int, h: int, seed: int = 1234,
