@@ -120,6 +120,38 @@ def bench_mxfp4(stream, reps=5):
             "note": "weights streamed as e2m1+e8m0 and expanded to bf16 for bf16 MFMA"}
 
 
+COPY_PROBE_BYTES = 1 << 30
+
+
+def copy_probe(reps=5):
+    """Copies COPY_PROBE_BYTES between two device buffers `reps` times: a kernel
+    whose HBM traffic is known (that many bytes read, that many written), so
+    that FETCH_SIZE / WRITE_SIZE counters can be scaled to bytes."""
+    import torch
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "reps": reps}))
+
+
+def measured_traffic(phase):
+    """HBM bytes per launch of `phase` on c3, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy-probe factor);
+    None when the summary does not list the kernel."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_c3.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) >= 4 and parts[0] == "traffic" and parts[1] == phase:
+                    return int(parts[2]) + int(parts[3])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -131,6 +163,8 @@ def main():
     ap.add_argument("--no-fp4", action="store_true", help="skip the c5 MXFP4 forward measurement")
     ap.add_argument("--no-profile", action="store_true",
                     help="time the step without per-kernel events")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only run a device copy of known size (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -139,6 +173,10 @@ def main():
 
     import numpy as np
     import torch
+
+    if args.copy_probe:
+        copy_probe()
+        return
 
     import tmt_moe
     from synthetic import CONFIGS, make_case
@@ -209,13 +247,15 @@ def main():
             ach = work / avg / 1e9
             roofline = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1),
                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                        "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+                        "traffic": measured_traffic(dom) if args.config == "c3" else None,
                         "work_per_launch": f"{work / 1e9:.1f} GFLOP = 2*T*K*d*h"}
         else:
             ach = work / avg / 1e6
             roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                        "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None}
+                        "frac": round(ach / PEAK_HBM_GBS, 4),
+                        "traffic": measured_traffic(dom) if args.config == "c3" else None}
 
     decode = None
     if not args.no_decode and args.config == "c3":
