@@ -1,0 +1,198 @@
+/*
+ * tmt_moe.hpp -- C++17 host interface with the reference's MoE operator
+ * signatures, layered on the C ABI of tmt_moe.h.
+ *
+ * The reference's MoE layer is a set of header-inline C++ functions compiled
+ * into each program (tmt-cuda/src/moe.cu:294-545). This header offers the
+ * same names with the same argument meaning, so a call site such as
+ * tmt-cuda/src/model.cu:512-514 or :676-677 compiles against it unchanged:
+ *
+ *   MoeKeep / MoeWs                     moe.cu:294-328
+ *   moe_keep_alloc / moe_keep_free      moe.cu:330-348
+ *   moe_ws_alloc / moe_ws_free          moe.cu:349-370
+ *   moe_forward                         moe.cu:372-466
+ *   moe_aux_from                        moe.cu:468-475
+ *   moe_backward                        moe.cu:477-545
+ *
+ * Behaviour kept from the reference:
+ *   - experts are single d x d linears with SiLU inside combine (hidden = 0);
+ *     moe_keep_alloc's extra `hidden` argument selects the up/SiLU/down
+ *     expert, whose forward/backward take a second weight table;
+ *   - moe_forward saves a copy of X in MoeKeep::H for the backward
+ *     (moe.cu:396), returns the Switch aux loss and sets MoeKeep::zloss, or,
+ *     when MoeKeep::stat is set, only copies the statistics there and returns
+ *     0 (moe.cu:448-452); moe_aux_from then yields aux and zloss;
+ *   - MoeKeep::hcnt holds the per-expert token counts after the statistics
+ *     were read (read by tmt_model_expert_counts, capi.cu:131-136);
+ *   - moe_backward overwrites dX, dWrouter and dWexp (linalg.cu:32-41 with
+ *     beta 0); experts without tokens get zero gradients;
+ *   - errors print a message and exit(1), as CUDA_CHECK does
+ *     (common.h:26-33); callers that want status codes use tmt_moe.h.
+ * Work goes to MoeKeep::stream (default: the null stream, the reference's
+ * default stream). Unlike the reference there is no host synchronisation
+ * inside moe_forward when MoeKeep::stat is set, and none in moe_backward.
+ * MoeWs exists for source compatibility: each MoeKeep's handle owns its
+ * workspace, so moe_ws_alloc / moe_ws_free do nothing.
+ */
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+
+#include "tmt_moe.h"
+
+struct MoeKeep {
+    float zloss = 0;
+    float* stat = nullptr;          // optional caller-owned device slot (>= 2 floats: aux, z)
+    const float* bias = nullptr;    // optional [E] fp32 logit bias (not in the reference)
+    hipStream_t stream = nullptr;
+    uint16_t* H = nullptr;          // [N][D] bf16 copy of the forward input
+    int32_t hcnt[64] = {0};         // tokens per expert (after the statistics were read)
+    int N = 0, E = 0, K = 0, D = 0, hidden = 0, max_N = 0;
+    tmt_moe* handle = nullptr;
+};
+struct MoeWs {};
+
+namespace tmt_moe_detail {
+[[noreturn]] inline void die(const char* where, const char* what) {
+    std::printf("%s: %s\n", where, what);
+    std::fflush(stdout);
+    std::exit(1);
+}
+inline void check(int rc, const char* where) {
+    if (rc != TMT_MOE_OK) die(where, tmt_moe_last_error());
+}
+inline void check_hip(hipError_t e, const char* where) {
+    if (e != hipSuccess) die(where, hipGetErrorString(e));
+}
+template <class B>
+inline const uint16_t* bits(const B* p) {
+    static_assert(sizeof(B) == 2, "bf16 element type expected");
+    return reinterpret_cast<const uint16_t*>(p);
+}
+template <class B>
+inline uint16_t* bits(B* p) {
+    static_assert(sizeof(B) == 2, "bf16 element type expected");
+    return reinterpret_cast<uint16_t*>(p);
+}
+template <class B>
+inline const uint16_t* const* table(B* const* p) {
+    static_assert(sizeof(B) == 2, "bf16 element type expected");
+    return reinterpret_cast<const uint16_t* const*>(p);
+}
+
+// Copy the input for the backward, run the forward, deliver the statistics.
+inline float forward(const uint16_t* X, const uint16_t* Wr, const uint16_t* const* Wup,
+                     const uint16_t* const* Wdown, uint16_t* Y, MoeKeep& k, int N, int E,
+                     int K, int D, float beta) {
+    const char* where = "moe_forward";
+    if (!k.handle) die(where, "moe_keep_alloc was not called");
+    if (E != k.E || K != k.K || D != k.D) die(where, "E, K or D differ from moe_keep_alloc");
+    if (N < 0 || N > k.max_N) die(where, "N exceeds the moe_keep_alloc size");
+    k.N = N;
+    if (N > 0) check_hip(hipMemcpyAsync(k.H, X, (size_t)N * D * 2, hipMemcpyDeviceToDevice, k.stream), where);
+    check(tmt_moe_forward(k.handle, k.stream, N, X, Wr, k.bias, Wup, Wdown, Y, beta), where);
+    if (E == 1) return 0.f;  // dense path: no router statistics (moe.cu:397-403)
+    if (k.stat) {            // deferred: the owner reads all layers at once
+        const void* st = nullptr;
+        check(tmt_moe_stats_device_ptr(k.handle, &st), where);
+        check_hip(hipMemcpyAsync(k.stat, st, 2 * sizeof(float), hipMemcpyDeviceToDevice, k.stream), where);
+        k.zloss = 0;
+        return 0.f;
+    }
+    float aux = 0, z = 0;
+    check(tmt_moe_read_stats(k.handle, k.stream, &aux, &z, k.hcnt), where);
+    k.zloss = z;
+    return aux;
+}
+
+inline void backward(const uint16_t* dY, const uint16_t* const* Wup, const uint16_t* const* Wdown,
+                     const uint16_t* Wr, float* dWr, float* const* dWup, float* const* dWdown,
+                     uint16_t* dX, MoeKeep& k, float aux, float zcoef) {
+    const char* where = "moe_backward";
+    if (!k.handle) die(where, "moe_keep_alloc was not called");
+    if (k.E == 1 && dWr)  // the reference zeroes the unused router gradient too (moe.cu:487)
+        check_hip(hipMemsetAsync(dWr, 0, (size_t)k.D * 4, k.stream), where);
+    check(tmt_moe_backward(k.handle, k.stream, dY, k.H, Wr, Wup, Wdown, aux, zcoef, dX,
+                           k.E > 1 ? dWr : nullptr, dWup, dWdown), where);
+}
+}  // namespace tmt_moe_detail
+
+/* moe.cu:330-341. N is the largest token count a forward will see. */
+inline void moe_keep_alloc(MoeKeep& k, int N, int E, int K, int D, int hidden = 0) {
+    tmt_moe_desc desc{};
+    desc.max_tokens = N;
+    desc.d = D;
+    desc.experts = E;
+    desc.topk = K;
+    desc.hidden = hidden;
+    desc.weight_format = TMT_MOE_WEIGHTS_BF16;
+    tmt_moe_detail::check(tmt_moe_create(&desc, &k.handle), "moe_keep_alloc");
+    if (N > 0)
+        tmt_moe_detail::check_hip(hipMalloc((void**)&k.H, (size_t)N * D * 2), "moe_keep_alloc");
+    k.E = E; k.K = K; k.D = D; k.hidden = hidden; k.max_N = N;
+}
+
+/* moe.cu:342-348 */
+inline void moe_keep_free(MoeKeep& k) {
+    if (k.handle) tmt_moe_destroy(k.handle);
+    if (k.H) (void)hipFree(k.H);
+    k = MoeKeep();
+}
+
+/* moe.cu:349-370: the workspace lives in each MoeKeep's handle. */
+inline void moe_ws_alloc(MoeWs&, int, int, int, int) {}
+inline void moe_ws_free(MoeWs&) {}
+
+/* moe.cu:372-466: Y = beta*Y + MoE(X) with the reference's single-linear
+ * experts Wexp[e] [D][D] (hidden == 0). Returns the Switch aux loss. */
+template <class B>
+inline float moe_forward(const B* X, const B* Wrouter, B** Wexp, B* Y, MoeKeep& k, MoeWs&,
+                         int N, int E, int K, int D, float beta = 0.0f) {
+    if (k.hidden != 0) tmt_moe_detail::die("moe_forward", "hidden > 0 needs the W_down table");
+    using namespace tmt_moe_detail;
+    return forward(bits(X), bits(Wrouter), table(Wexp), nullptr, bits(Y), k, N, E, K, D, beta);
+}
+
+/* Up/SiLU/down experts (hidden > 0): W_up[e] [hidden][D], W_down[e] [D][hidden]. */
+template <class B>
+inline float moe_forward(const B* X, const B* Wrouter, B** W_up, B** W_down, B* Y, MoeKeep& k,
+                         MoeWs&, int N, int E, int K, int D, float beta = 0.0f) {
+    if (k.hidden == 0) tmt_moe_detail::die("moe_forward", "hidden == 0 takes one weight table");
+    using namespace tmt_moe_detail;
+    return forward(bits(X), bits(Wrouter), table(W_up), table(W_down), bits(Y), k, N, E, K, D, beta);
+}
+
+/* moe.cu:468-475: aux from the statistics moe_forward copied to k.stat
+ * (hsum = the host copy of that slot); sets k.zloss and k.hcnt. */
+inline float moe_aux_from(MoeKeep& k, const float* hsum) {
+    k.zloss = hsum[1];
+    tmt_moe_detail::check(tmt_moe_read_stats(k.handle, k.stream, nullptr, nullptr, k.hcnt),
+                          "moe_aux_from");
+    return hsum[0];
+}
+
+/* moe.cu:477-545: dX [N][D] bf16, dWrouter [E][D] fp32, dWexp[e] [D][D] fp32,
+ * all overwritten; aux / zcoef are the loss coefficients (already / L). */
+template <class B>
+inline void moe_backward(const B* dY, B** Wexp, const B* Wrouter, float* dWrouter, float** dWexp,
+                         B* dX, MoeKeep& k, MoeWs&, float aux = 0.f, float zcoef = 0.f) {
+    if (k.hidden != 0) tmt_moe_detail::die("moe_backward", "hidden > 0 needs the W_down tables");
+    using namespace tmt_moe_detail;
+    backward(bits(dY), table(Wexp), nullptr, bits(Wrouter), dWrouter, dWexp, nullptr, bits(dX), k,
+             aux, zcoef);
+}
+
+/* Up/SiLU/down experts: dW_up[e] [hidden][D], dW_down[e] [D][hidden] fp32. */
+template <class B>
+inline void moe_backward(const B* dY, B** W_up, B** W_down, const B* Wrouter, float* dWrouter,
+                         float** dW_up, float** dW_down, B* dX, MoeKeep& k, MoeWs&,
+                         float aux = 0.f, float zcoef = 0.f) {
+    if (k.hidden == 0) tmt_moe_detail::die("moe_backward", "hidden == 0 takes one weight table");
+    using namespace tmt_moe_detail;
+    backward(bits(dY), table(W_up), table(W_down), bits(Wrouter), dWrouter, dW_up, dW_down,
+             bits(dX), k, aux, zcoef);
+}
