@@ -341,7 +341,10 @@ int tmt_moe_forward(tmt_moe* m, void* stream, int32_t T, const uint16_t* X,
         up.a = X; up.lda = d; up.c = m->U; up.ldc = hn; up.c2 = m->Aact;
         for (int e = 0; e < E; ++e) up.w[e] = W_up[e];
         up.ldb = d;
-        LAUNCH(TMT_MOE_PH_GEMM_UP, launch_gemm(GEMM_UP, h > 0, up, s));
+        // Decode-sized batches stream the weights with the skinny kernel.
+        const bool skinny = T <= kSkinnyMaxTokens;
+        LAUNCH(TMT_MOE_PH_GEMM_UP, skinny ? launch_skinny_gemm(GEMM_UP, h > 0, up, T, s)
+                                          : launch_gemm(GEMM_UP, h > 0, up, s));
         if (h > 0) {
             GemmParams dn{};
             dn.offsets = m->offsets; dn.order = m->order; dn.perm = m->perm; dn.E = E;
@@ -349,7 +352,8 @@ int tmt_moe_forward(tmt_moe* m, void* stream, int32_t T, const uint16_t* X,
             dn.a = m->Aact; dn.lda = h; dn.c = m->O; dn.ldc = d;
             for (int e = 0; e < E; ++e) dn.w[e] = W_down[e];
             dn.ldb = h;
-            LAUNCH(TMT_MOE_PH_GEMM_DOWN, launch_gemm(GEMM_DOWN, false, dn, s));
+            LAUNCH(TMT_MOE_PH_GEMM_DOWN, skinny ? launch_skinny_gemm(GEMM_DOWN, false, dn, T, s)
+                                                : launch_gemm(GEMM_DOWN, false, dn, s));
         }
         CombineParams cp{};
         cp.O = h > 0 ? m->O : m->U; cp.slot_of = m->slot_of; cp.gate = m->gate;

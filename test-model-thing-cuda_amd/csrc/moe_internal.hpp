@@ -4,6 +4,7 @@
 //   router.hip    router logits + softmax + top-k, block histograms, expert
 //                 offset scan, stable token permutation
 //   gemm.hip      grouped bf16 MFMA GEMMs over expert segments
+//   skinny.hip    weight-streaming expert GEMMs for decode-sized batches
 //   pointwise.hip combine, combine/router backward, router dW, dX scatter
 // The host orchestration lives in moe_api.cpp.
 #pragma once
@@ -92,8 +93,12 @@ struct GemmParams {
     const uint8_t* wq[kMaxExperts];   // MXFP4 weights: packed e2m1 [N][K/2] (low nibble = even k)
     const uint8_t* wsc[kMaxExperts];  // MXFP4 scales: e8m0 [K/32][N]
 };
-// Grid size the launcher will use (for tests of the tile bound).
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s);
+
+// Decode-sized forward GEMMs (GEMM_UP / GEMM_DOWN, bf16 weights) for
+// T <= kSkinnyMaxTokens tokens: every expert then owns at most T rows.
+constexpr int kSkinnyMaxTokens = 64;
+hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s);
 
 // ------------------------------------------------------------- pointwise --
 struct CombineParams {

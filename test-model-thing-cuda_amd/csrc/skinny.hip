@@ -1,0 +1,164 @@
+// skinny.hip -- grouped expert GEMMs for decode-sized batches (gfx950).
+//
+// With T <= 64 tokens every expert owns at most T rows, so the expert GEMMs
+// are weight-streaming problems (the reference runs them as padded 128-row
+// cuBLAS calls, tmt-cuda/src/moe.cu:414-436, tmt-cuda/src/generate.h:19-44).
+// The 256 x 256 tiles of gemm.hip would leave most CUs idle and read each
+// weight tile through a deep LDS pipeline for one useful row. Here a
+// workgroup owns 16 output columns of one expert and all of its rows:
+//   * the 4 waves split the reduction (K) into contiguous quarters;
+//   * each lane streams one weight row (output column) straight from HBM
+//     into registers, 128 contiguous bytes per 256-element chunk, and the
+//     matching activation row of each 16-row block (rows past the expert's
+//     count are zero and not loaded);
+//   * v_mfma_f32_16x16x32_bf16 multiplies them. A and B use the same
+//     lane/k assignment (lane group g holds k = base + 64g + 8i .. +7 for
+//     MFMA i), which is a permutation of the reduction, so the product is
+//     the plain dot product;
+//   * the wave partials are summed in LDS in a fixed order and written with
+//     the same epilogue semantics as gemm.hip (U, SiLU(U) from the fp32 sum).
+// Experts are visited in descending-count order (the scan's LPT order), so
+// the grid only spans min(E, T*K) expert ranks.
+#include "device_util.hpp"
+#include "moe_internal.hpp"
+
+namespace tmt {
+namespace {
+
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+__device__ __forceinline__ f32x4 mfma16(const uint4& w, const uint4& a, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w),
+                                                   __builtin_bit_cast(bf16x8, a), c, 0, 0, 0);
+}
+
+template <int KIND, bool DUAL, int RB>
+__global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(GemmParams p, int nexp) {
+    static_assert(KIND == GEMM_UP || KIND == GEMM_DOWN, "forward GEMMs only");
+    constexpr bool kGather = KIND == GEMM_UP;
+    __shared__ f32x4 red[4][RB][64];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rank = (int)blockIdx.x % nexp, tile = (int)blockIdx.x / nexp;
+    const int e = p.order[rank];
+    const int row0 = p.offsets[e];
+    const int rows = min(p.offsets[e + 1] - row0, 16 * RB);
+    if (rows <= 0) return;
+    const int n0 = tile * 16;
+    const int g = lane >> 4, li = lane & 15;
+
+    // This lane's weight row (output column n0 + li) and activation rows.
+    const uint16_t* wrow = p.w[e] + (int64_t)(n0 + li) * p.ldb;
+    const uint16_t* arow[RB];
+    bool aok[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int m = rb * 16 + li;
+        aok[rb] = m < rows;
+        const int slot = row0 + (aok[rb] ? m : 0);
+        const int src = kGather ? p.perm[slot] : slot;
+        arow[rb] = p.a + (int64_t)src * p.lda;
+    }
+
+    // The wave's share of the reduction, in units of 64 elements.
+    const int units = p.K >> 6;
+    const int u0 = wave * units / 4, u1 = (wave + 1) * units / 4;
+    f32x4 acc[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint4 zero = make_uint4(0, 0, 0, 0);
+
+    // Chunks of 4 units (256 elements): lane group g covers 64 contiguous
+    // elements, i.e. 8 x 16-byte loads of its weight row. The next chunk's
+    // weights are requested before the current chunk's MFMAs.
+    int u = u0;
+    if (u + 4 <= u1) {
+        uint4 wv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wv[i] = ld16(wrow + u * 64 + g * 64 + 8 * i);
+        for (; u + 4 <= u1; u += 4) {
+            const int kb = u * 64 + g * 64;
+            uint4 wn[8];
+            const bool more = u + 8 <= u1;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wn[i] = more ? ld16(wrow + kb + 256 + 8 * i) : zero;
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                uint4 av[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) av[i] = aok[rb] ? ld16(arow[rb] + kb + 8 * i) : zero;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[rb] = mfma16(wv[i], av[i], acc[rb]);
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) wv[i] = wn[i];
+        }
+    }
+    // Remaining single units: lane group g covers 16 elements.
+    for (; u < u1; ++u) {
+        const int kb = u * 64 + g * 16;
+        const uint4 w0 = ld16(wrow + kb), w1 = ld16(wrow + kb + 8);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const uint4 a0 = aok[rb] ? ld16(arow[rb] + kb) : zero;
+            const uint4 a1 = aok[rb] ? ld16(arow[rb] + kb + 8) : zero;
+            acc[rb] = mfma16(w0, a0, acc[rb]);
+            acc[rb] = mfma16(w1, a1, acc[rb]);
+        }
+    }
+
+    // acc[rb][r] = C[row rb*16 + li][column n0 + 4g + r] (16x16 MFMA layout:
+    // first-operand index 4*(lane/16) + r, second-operand index lane % 16).
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) red[wave][rb][lane] = acc[rb];
+    __syncthreads();
+
+    // Thread t -> row m = t / 16, column n = t % 16 of each row block; the four
+    // wave partials are added in wave order.
+    const int m = tid >> 4, n = tid & 15;
+    const int src_lane = (n >> 2) * 16 + m, r = n & 3;
+    uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int row = rb * 16 + m;
+        if (row >= rows) continue;
+        float v = red[0][rb][src_lane][r];
+        v += red[1][rb][src_lane][r];
+        v += red[2][rb][src_lane][r];
+        v += red[3][rb][src_lane][r];
+        const int64_t off = (int64_t)(row0 + row) * p.ldc + n0 + n;
+        C[off] = f2bf(v);
+        if constexpr (DUAL) p.c2[off] = f2bf(silu_fast(v));
+    }
+}
+
+template <int KIND, bool DUAL>
+hipError_t launch_rb(int rb, const GemmParams& p, int nexp, unsigned grid, hipStream_t s) {
+    switch (rb) {
+        case 1: skinny_gemm_kernel<KIND, DUAL, 1><<<grid, kThreads, 0, s>>>(p, nexp); break;
+        case 2: skinny_gemm_kernel<KIND, DUAL, 2><<<grid, kThreads, 0, s>>>(p, nexp); break;
+        case 4: skinny_gemm_kernel<KIND, DUAL, 4><<<grid, kThreads, 0, s>>>(p, nexp); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s) {
+    if (T <= 0) return hipSuccess;
+    if (T > kSkinnyMaxTokens || p.N % 16 != 0 || p.K % 64 != 0 || p.N <= 0) return hipErrorInvalidValue;
+    const int rb = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
+    const int nexp = min(p.E, p.slots);
+    const unsigned grid = (unsigned)(p.N / 16) * (unsigned)nexp;
+    switch (kind) {
+        case GEMM_UP:
+            return dual ? launch_rb<GEMM_UP, true>(rb, p, nexp, grid, s)
+                        : launch_rb<GEMM_UP, false>(rb, p, nexp, grid, s);
+        case GEMM_DOWN: return launch_rb<GEMM_DOWN, false>(rb, p, nexp, grid, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace tmt

@@ -266,3 +266,42 @@ def test_decode_steps_against_oracle(orc, T):
     r = oracle_case(orc, case, cfg["K"], cfg["h"], Y0=Y0, beta=1.0)
     check_routing(g, r, cfg["E"])
     assert rel_l2(g["Y"], r["Y"]) <= REL_L2
+
+
+@pytest.mark.parametrize("T,d,E,K,h", [
+    (1, 192, 5, 2, 320),     # one token, d and h not multiples of 256
+    (3, 256, 4, 2, 0),       # reference single-linear experts
+    (17, 128, 3, 3, 128),    # two 16-row blocks per expert, E == K
+    (40, 512, 64, 8, 128),   # widest router, top-8, up to 40 rows per expert
+    (64, 256, 1, 1, 0),      # dense path at the decode-kernel limit
+    (65, 192, 5, 2, 320),    # first token count on the tiled path
+])
+def test_decode_shapes_against_oracle(orc, T, d, E, K, h):
+    """Decode-sized batches (T <= 64 use the weight-streaming expert GEMMs);
+    the backward reads the U / SiLU(U) / O those kernels wrote."""
+    say(f"decode shape T={T} d={d} E={E} K={K} h={h} fwd+bwd")
+    case = make_case(T, d, E, K, h, seed=7 * T + d)
+    aux, z = (0.1, 1e-3) if E > 1 else (0.0, 0.0)
+    Y0 = bf16_bits(np.random.default_rng(T + 1).standard_normal((T, d)).astype(np.float32))
+    g = run_gpu(case, K, h, beta=1.0, Y0=Y0, backward=True, aux=aux, z=z, max_tokens=128)
+    r = oracle_case(orc, case, K, h, Y0=Y0, beta=1.0, backward=True, aux=aux, z=z)
+    check_routing(g, r, E)
+    err = rel_l2(g["Y"], r["Y"])
+    say(f"  Y rel-L2 {err:.2e}")
+    assert err <= REL_L2
+    check_grads(g, r, h, E)
+
+
+def test_decode_all_tokens_on_two_experts(orc):
+    """T = 64 with every token routed to experts 0 and 1: 64 rows per expert,
+    the largest row count the decode kernel handles."""
+    say("decode T=64, bias routes every token to experts 0 and 1")
+    T, d, E, K, h = 64, 256, 8, 2, 256
+    case = make_case(T, d, E, K, h, seed=11)
+    case["bias"] = np.array([40, 40, -40, -40, -40, -40, -40, -40], np.float32)
+    g = run_gpu(case, K, h, backward=True, aux=0.1, z=1e-3)
+    r = oracle_case(orc, case, K, h, backward=True, aux=0.1, z=1e-3)
+    check_routing(g, r, E)
+    assert list(g["counts"]) == [T, T, 0, 0, 0, 0, 0, 0]
+    assert rel_l2(g["Y"], r["Y"]) <= REL_L2
+    check_grads(g, r, h, E)
