@@ -50,14 +50,52 @@ __device__ __forceinline__ float dsilu_fast(float x) {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 
+// Value of lane (lane ^ OFF), moved by VALU cross-lane operations instead of
+// the LDS permute unit: DPP quad permutes / row rotate / half-row mirror for
+// OFF <= 8, and the gfx950 row-swap instructions for 16 and 32
+// (permlane16_swap(v, v) yields rows {0,0,2,2} and {1,1,3,3};
+// permlane32_swap(v, v) yields halves {lo,lo} and {hi,hi}).
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+template <int C>
+__device__ __forceinline__ uint32_t dpp_mov(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, C, 0xF, 0xF, false);
+}
+template <int OFF>
+__device__ __forceinline__ uint32_t xor_lane_u32(uint32_t v) {
+    static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "xor offset");
+    if constexpr (OFF == 1) return dpp_mov<0xB1>(v);                  // quad_perm [1,0,3,2]
+    else if constexpr (OFF == 2) return dpp_mov<0x4E>(v);             // quad_perm [2,3,0,1]
+    else if constexpr (OFF == 4) return dpp_mov<0x1B>(dpp_mov<0x141>(v));  // half mirror, quad [3,2,1,0]
+    else if constexpr (OFF == 8) return dpp_mov<0x128>(v);            // row_ror:8
+    else if constexpr (OFF == 16) {
+        const u32x2_t s = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (threadIdx.x & 16) ? s[0] : s[1];
+    } else {
+        const u32x2_t s = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (threadIdx.x & 32) ? s[0] : s[1];
+    }
+}
+template <int OFF>
+__device__ __forceinline__ float xor_lane(float v) {
+    return __uint_as_float(xor_lane_u32<OFF>(__float_as_uint(v)));
+}
+template <int OFF>
+__device__ __forceinline__ int xor_lane(int v) {
+    return (int)xor_lane_u32<OFF>((uint32_t)v);
+}
+
 __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
 __device__ __forceinline__ int shfl_xor(int v, int m) { return __shfl_xor(v, m, 64); }
 
 // Full-wave xor butterfly sum with offsets 32,16,...,1: every lane ends with
 // the same value (each step adds two equal-shaped partial trees).
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + shfl_xor(v, off);
+    v = v + xor_lane<32>(v);
+    v = v + xor_lane<16>(v);
+    v = v + xor_lane<8>(v);
+    v = v + xor_lane<4>(v);
+    v = v + xor_lane<2>(v);
+    v = v + xor_lane<1>(v);
     return v;
 }
 

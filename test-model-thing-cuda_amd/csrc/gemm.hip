@@ -88,11 +88,11 @@ template <> struct Traits<GEMM_DX> {
 };
 // dW_down[e][m][n] = sum_slot dO[slot][m] * A[slot][n]
 template <> struct Traits<GEMM_DW_DOWN> {
-    static constexpr bool group_k = true, a_kc = false, b_kc = false, gather = false, b_fp4 = false;
+    static constexpr bool group_k = true, a_kc = false, b_kc = false, b_fp4 = false;
 };
 // dW_up[e][m][n] = sum_slot dU[slot][m] * Xg[slot][n]   (Xg: X gathered to slot order)
 template <> struct Traits<GEMM_DW_UP> {
-    static constexpr bool group_k = true, a_kc = false, b_kc = false, gather = false, b_fp4 = false;
+    static constexpr bool group_k = true, a_kc = false, b_kc = false, b_fp4 = false;
 };
 
 // MXFP4 variants: same as GEMM_UP / GEMM_DOWN, B = e2m1 weights + e8m0 scales.

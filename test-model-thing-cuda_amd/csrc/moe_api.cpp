@@ -229,6 +229,21 @@ int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* W
                                                         m->offsets, m->order, m->stats, s));
         return TMT_MOE_OK;
     }
+    if (T >= 1 && T <= kSmallRouteTokens) {
+        RouterParams rp{};
+        rp.X = X; rp.Wr = Wr; rp.bias = bias;
+        rp.T = T; rp.d = d; rp.E = E; rp.K = K; rp.rows_per_block = T;
+        rp.logits = m->logits; rp.probs = m->probs; rp.idx = m->idx; rp.gate = m->gate;
+        rp.lse = m->lse;
+        ScanParams sp{};
+        sp.T = T; sp.E = E; sp.K = K; sp.nblk = 1;
+        sp.counts = m->counts; sp.offsets = m->offsets; sp.order = m->order; sp.stats = m->stats;
+        PermuteParams pp{};
+        pp.T = T; pp.E = E; pp.K = K; pp.rows_per_block = T;
+        pp.perm = m->perm; pp.slot_of = m->slot_of;
+        LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(rp, sp, pp, s));
+        return TMT_MOE_OK;
+    }
     const int rpb = router_rows_per_block(T, E, K);
     const int nblk = T > 0 ? (T + rpb - 1) / rpb : 0;
     if (nblk > m->nblk_max) return fail(TMT_MOE_EINVAL, "internal: router block count %d > %d", nblk, m->nblk_max);

@@ -30,33 +30,106 @@ int router_rows_per_wave(int E) { return 64 / router_ep(E); }
 // A reduce-scatter xor butterfly (offsets 32..1) then leaves lane l with the
 // full dot product of row l/EP and expert l%EP; each addition pairs the same
 // partial trees as the full butterfly, so the bits equal the canonical order.
-template <int EP>
-__global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
-    constexpr int R = 64 / EP;
-    extern __shared__ uint4 smem_w[];  // Wr [E][d] bf16
-    __shared__ int s_cnt[kMaxExperts];
-    __shared__ float s_stat[4][kMaxExperts + 1];
+// Stage Wr [E][d] (bf16) in LDS: all of a thread's 16-byte loads are issued
+// before any of them is stored, so the fill costs one memory round trip.
+__device__ __forceinline__ void stage_router_weights(const uint16_t* Wr, int nvec, uint4* dst) {
+    const uint4* src = reinterpret_cast<const uint4*>(Wr);
+    constexpr int kBatch = 8;
+    const int nt = (int)blockDim.x;
+    for (int base = threadIdx.x; base < nvec; base += kBatch * nt) {
+        uint4 v[kBatch];
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int j = min(base + i * nt, nvec - 1);  // clamped: no load under a branch
+            v[i] = src[j];
+        }
+#pragma unroll
+        for (int i = 0; i < kBatch; ++i) {
+            const int j = base + i * nt;
+            if (j < nvec) dst[j] = v[i];
+        }
+    }
+}
 
+// Route rows [row_begin, row_end) with the block's 4 waves: logits, probs,
+// top-k indices and gates, lse. Per-expert pick counts are added to s_cnt
+// (LDS atomics); each wave leaves its sum of probabilities per expert in
+// s_stat[wave][e] and its sum of lse^2 in s_stat[wave][kMaxExperts]. When
+// s_idx is given, the picks are also stored there ([row - row_begin][j]).
+// Reduce-scatter level at offset OFF over the first 2*OFF entries of acc:
+// afterwards acc[t] (t < OFF) holds, on lane l, the sum of the entry the lane
+// keeps (t, or t + OFF when bit OFF of l is set) and its partner's copy of
+// that entry. OFF = 32 / 16 use the row-swap instructions, which deliver
+// both operands of every addition without a select.
+template <int OFF>
+__device__ __forceinline__ void reduce_scatter_level(float* acc, int lane) {
+    if constexpr (OFF >= 16) {
+#pragma unroll
+        for (int t = 0; t < OFF; ++t) {
+            const u32x2_t sw = OFF == 32
+                ? __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[t]), __float_as_uint(acc[t + OFF]), false, false)
+                : __builtin_amdgcn_permlane16_swap(__float_as_uint(acc[t]), __float_as_uint(acc[t + OFF]), false, false);
+            // lanes without bit OFF: {own lo, partner lo}; with it: {partner hi, own hi}
+            acc[t] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+        }
+    } else {
+        const bool upper = (lane & OFF) != 0;
+#pragma unroll
+        for (int t = 0; t < OFF; ++t) {
+            const float lo = acc[t], hi = acc[t + OFF];
+            const float send = upper ? lo : hi;
+            const float keep = upper ? hi : lo;
+            acc[t] = keep + xor_lane<OFF>(send);
+        }
+    }
+}
+
+// Butterfly max / sum / arg-max over groups of EP lanes (xor offsets EP/2 .. 1).
+template <int EP>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (EP >= 64) v = fmaxf(v, xor_lane<32>(v));
+    if constexpr (EP >= 32) v = fmaxf(v, xor_lane<16>(v));
+    if constexpr (EP >= 16) v = fmaxf(v, xor_lane<8>(v));
+    v = fmaxf(v, xor_lane<4>(v));
+    v = fmaxf(v, xor_lane<2>(v));
+    v = fmaxf(v, xor_lane<1>(v));
+    return v;
+}
+template <int EP>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (EP >= 64) v += xor_lane<32>(v);
+    if constexpr (EP >= 32) v += xor_lane<16>(v);
+    if constexpr (EP >= 16) v += xor_lane<8>(v);
+    v += xor_lane<4>(v);
+    v += xor_lane<2>(v);
+    v += xor_lane<1>(v);
+    return v;
+}
+// One arg-max step at offset OFF over (logit desc, expert asc).
+template <int OFF>
+__device__ __forceinline__ void argmax_step(float& bv, float& bp, int& be, bool& has) {
+    const float ov = xor_lane<OFF>(bv);
+    const float op = xor_lane<OFF>(bp);
+    const int oe = xor_lane<OFF>(be);
+    const int oh = xor_lane<OFF>((int)has);
+    const bool take = oh && (!has || ov > bv || (ov == bv && oe < be));
+    if (take) { bv = ov; bp = op; be = oe; has = true; }
+}
+
+template <int EP, int NW>
+__device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t* wl, int row_begin,
+                                           int row_end, int* s_cnt,
+                                           float (*s_stat)[kMaxExperts + 1], int* s_idx) {
+    constexpr int R = 64 / EP;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int d = p.d, E = p.E, K = p.K;
-    {
-        const uint4* src = reinterpret_cast<const uint4*>(p.Wr);
-        const int nvec = E * d / 8;
-        for (int i = tid; i < nvec; i += kThreads) smem_w[i] = src[i];
-    }
-    if (tid < kMaxExperts) s_cnt[tid] = 0;
-    __syncthreads();
-    const uint16_t* wl = reinterpret_cast<const uint16_t*>(smem_w);
-
-    const int row_begin = blockIdx.x * p.rows_per_block;
-    const int row_end = min(p.T, row_begin + p.rows_per_block);
     const int e_mine = lane % EP;
     const int r_mine = lane / EP;
     const bool e_valid = e_mine < E;
     const int nch = (d + 511) / 512;
     float psum = 0.0f, lsum = 0.0f;
 
-    for (int r0 = row_begin + wave * R; r0 < row_end; r0 += 4 * R) {
+    for (int r0 = row_begin + wave * R; r0 < row_end; r0 += NW * R) {
         float acc[R * EP];
 #pragma unroll
         for (int i = 0; i < R * EP; ++i) acc[i] = 0.0f;
@@ -89,18 +162,12 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
 
         // Reduce-scatter butterfly: at offset `off` the lane keeps the half of
         // its entries whose bit log2(off) equals its own lane bit.
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            const bool upper = (lane & off) != 0;
-#pragma unroll
-            for (int t = 0; t < off; ++t) {
-                const float lo = acc[t], hi = acc[t + off];
-                const float send = upper ? lo : hi;
-                const float keep = upper ? hi : lo;
-                const float recv = shfl_xor(send, off);
-                acc[t] = keep + recv;
-            }
-        }
+        reduce_scatter_level<32>(acc, lane);
+        reduce_scatter_level<16>(acc, lane);
+        reduce_scatter_level<8>(acc, lane);
+        reduce_scatter_level<4>(acc, lane);
+        reduce_scatter_level<2>(acc, lane);
+        reduce_scatter_level<1>(acc, lane);
         float logit = acc[0];
         if (p.bias != nullptr && e_valid) logit = logit + p.bias[e_mine];
 
@@ -109,13 +176,9 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
 
         // Softmax over the EP lanes of this row (moe.cu:41-49).
         const float lv = e_valid ? logit : -INFINITY;
-        float mx = lv;
-#pragma unroll
-        for (int off = EP / 2; off >= 1; off >>= 1) mx = fmaxf(mx, shfl_xor(mx, off));
+        const float mx = group_max<EP>(lv);
         const float ex = e_valid ? __expf(lv - mx) : 0.0f;
-        float se = ex;
-#pragma unroll
-        for (int off = EP / 2; off >= 1; off >>= 1) se += shfl_xor(se, off);
+        const float se = group_sum<EP>(ex);
         const float prob = ex / se;
         const float lse = mx + __logf(se);
 
@@ -129,15 +192,12 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
                 bool has = e_valid && !sel;
                 float bv = logit, bp = prob;
                 int be = e_mine;
-#pragma unroll
-                for (int off = EP / 2; off >= 1; off >>= 1) {
-                    const float ov = shfl_xor(bv, off);
-                    const float op = shfl_xor(bp, off);
-                    const int oe = shfl_xor(be, off);
-                    const int oh = shfl_xor((int)has, off);
-                    const bool take = oh && (!has || ov > bv || (ov == bv && oe < be));
-                    if (take) { bv = ov; bp = op; be = oe; has = true; }
-                }
+                if constexpr (EP >= 64) argmax_step<32>(bv, bp, be, has);
+                if constexpr (EP >= 32) argmax_step<16>(bv, bp, be, has);
+                if constexpr (EP >= 16) argmax_step<8>(bv, bp, be, has);
+                argmax_step<4>(bv, bp, be, has);
+                argmax_step<2>(bv, bp, be, has);
+                argmax_step<1>(bv, bp, be, has);
                 if (e_mine == be) sel = true;
                 if (e_mine == j) { out_e = be; out_p = bp; }
                 zsum += bp;
@@ -153,6 +213,7 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
             if (e_mine < K) {
                 p.idx[(int64_t)row * K + e_mine] = out_e;
                 p.gate[(int64_t)row * K + e_mine] = out_p / zsum;
+                if (s_idx) s_idx[(row - row_begin) * K + e_mine] = out_e;
             }
             if (e_mine == 0) {
                 p.lse[row] = lse;
@@ -162,15 +223,38 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
         }
     }
 
-    // Block statistics in a fixed order: row slots (xor butterfly), then waves.
-#pragma unroll
-    for (int off = 32; off >= EP; off >>= 1) {
-        psum += shfl_xor(psum, off);
-        lsum += shfl_xor(lsum, off);
-    }
+    // Per-wave statistics in a fixed order: row slots (xor butterfly).
+    if constexpr (EP <= 32) { psum += xor_lane<32>(psum); lsum += xor_lane<32>(lsum); }
+    if constexpr (EP <= 16) { psum += xor_lane<16>(psum); lsum += xor_lane<16>(lsum); }
+    if constexpr (EP <= 8) { psum += xor_lane<8>(psum); lsum += xor_lane<8>(lsum); }
     if (lane < EP) s_stat[wave][lane] = psum;
     if (lane == 0) s_stat[wave][kMaxExperts] = lsum;
+}
+
+// One wave routes R = 64/EP rows at a time. Lane L owns the elements
+// k = c*512 + 8L + t of each row (t = 0..7, chunk c = 0, 1, ...), and keeps
+// one fp32 partial per (row, expert), accumulated with fmaf in ascending k.
+// A reduce-scatter xor butterfly (offsets 32..1) then leaves lane l with the
+// full dot product of row l/EP and expert l%EP; each addition pairs the same
+// partial trees as the full butterfly, so the bits equal the canonical order.
+template <int EP>
+__global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
+    extern __shared__ uint4 smem_w[];  // Wr [E][d] bf16
+    __shared__ int s_cnt[kMaxExperts];
+    __shared__ float s_stat[4][kMaxExperts + 1];
+
+    const int tid = threadIdx.x;
+    const int E = p.E;
+    stage_router_weights(p.Wr, E * p.d / 8, smem_w);
+    if (tid < kMaxExperts) s_cnt[tid] = 0;
     __syncthreads();
+
+    const int row_begin = blockIdx.x * p.rows_per_block;
+    const int row_end = min(p.T, row_begin + p.rows_per_block);
+    route_rows<EP, 4>(p, reinterpret_cast<const uint16_t*>(smem_w), row_begin, row_end, s_cnt, s_stat,
+                      nullptr);
+    __syncthreads();
+    // Block statistics: waves added in order.
     const int b = blockIdx.x;
     if (tid < E) {
         p.blkstat[(int64_t)b * (E + 1) + tid] =
@@ -352,6 +436,125 @@ hipError_t launch_permute(const PermuteParams& p, int nblk, hipStream_t s) {
     const int RG = 64 / p.K;
     if ((p.rows_per_block + RG - 1) / RG > kMaxGroups) return hipErrorInvalidValue;
     permute_kernel<<<nblk, kThreads, 0, s>>>(p);
+    return hipGetLastError();
+}
+
+// T <= kSmallRouteTokens (decode): router, counts, offsets, statistics,
+// expert order and the stable permutation in one workgroup, one launch
+// instead of router + scan + permute. The statistics use the same fixed
+// summation order as router_kernel's block statistics followed by
+// scan_kernel's formulas.
+constexpr int kSmallGroups = 8;  // ceil(T / floor(64 / K)) for T <= 64, K <= 8
+
+constexpr int kSmallWaves = 16;
+
+template <int EP>
+__global__ __launch_bounds__(64 * kSmallWaves) void route_small_kernel(RouterParams p, ScanParams sp,
+                                                                       PermuteParams pp) {
+    extern __shared__ uint4 smem_w[];  // Wr [E][d] bf16
+    __shared__ int s_cnt[kMaxExperts];
+    __shared__ float s_stat[kSmallWaves][kMaxExperts + 1];
+    __shared__ int s_idx[kSmallRouteTokens * kMaxTopK];
+    __shared__ int s_off[kMaxExperts + 1];
+    __shared__ int s_g[kSmallGroups][kMaxExperts];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = p.E, K = p.K, T = p.T;
+    stage_router_weights(p.Wr, E * p.d / 8, smem_w);
+    if (tid < kMaxExperts) s_cnt[tid] = 0;
+    __syncthreads();
+    route_rows<EP, kSmallWaves>(p, reinterpret_cast<const uint16_t*>(smem_w), 0, T, s_cnt, s_stat, s_idx);
+    __syncthreads();
+
+    if (tid == 0) {
+        int run = 0;
+        for (int e = 0; e < E; ++e) {
+            s_off[e] = run;
+            run += s_cnt[e];
+        }
+        s_off[E] = run;
+        // Switch aux (moe.cu:456-465) and z-loss mean (moe.cu:268-278).
+        const float inv_t = 1.0f / (float)T;
+        const float inv_tk = 1.0f / ((float)T * (float)K);
+        float aux = 0.0f;
+        for (int e = 0; e < E; ++e) {
+            float sp_e = s_stat[0][e];
+            for (int w = 1; w < kSmallWaves; ++w) sp_e += s_stat[w][e];
+            aux += (sp_e * inv_t) * ((float)s_cnt[e] * inv_tk);
+        }
+        float l2 = s_stat[0][kMaxExperts];
+        for (int w = 1; w < kSmallWaves; ++w) l2 += s_stat[w][kMaxExperts];
+        sp.stats[0] = aux * (float)E;
+        sp.stats[1] = l2 * inv_t;
+    }
+    __syncthreads();
+    if (tid <= E) sp.offsets[tid] = s_off[tid];
+    if (tid < E) {
+        sp.counts[tid] = s_cnt[tid];
+        reinterpret_cast<int32_t*>(sp.stats + 2)[tid] = s_cnt[tid];
+        int rank = 0;
+        for (int e = 0; e < E; ++e)
+            rank += (s_cnt[e] > s_cnt[tid]) || (s_cnt[e] == s_cnt[tid] && e < tid);
+        sp.order[rank] = tid;
+    }
+
+    // Stable permutation: groups of floor(64/K) tokens, a ballot per expert.
+    const int RG = 64 / K, pairs = RG * K;
+    const int G = (T + RG - 1) / RG;
+    const int rr = lane / K, j = lane % K;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int g = wave; g < G; g += kSmallWaves) {
+        const int row = g * RG + rr;
+        const bool valid = lane < pairs && row < T;
+        const int e = valid ? s_idx[row * K + j] : -1;
+        for (int ee = 0; ee < E; ++ee) {
+            const uint64_t m = __ballot(e == ee);
+            if (lane == ee) s_g[g][ee] = __popcll(m);
+        }
+    }
+    __syncthreads();
+    if (tid < E) {
+        int run = s_off[tid];
+        for (int g = 0; g < G; ++g) {
+            const int c = s_g[g][tid];
+            s_g[g][tid] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += kSmallWaves) {
+        const int row = g * RG + rr;
+        const bool valid = lane < pairs && row < T;
+        const int e = valid ? s_idx[row * K + j] : -1;
+        int rank = 0;
+        for (int ee = 0; ee < E; ++ee) {
+            const uint64_t m = __ballot(e == ee);
+            if (e == ee) rank = __popcll(m & lt_mask);
+        }
+        if (valid) {
+            const int pos = s_g[g][e] + rank;
+            pp.perm[pos] = row;
+            pp.slot_of[(int64_t)row * K + j] = pos;
+        }
+    }
+}
+
+hipError_t launch_route_small(const RouterParams& p, const ScanParams& sp, const PermuteParams& pp,
+                              hipStream_t s) {
+    if (p.T < 1 || p.T > kSmallRouteTokens || p.K > kMaxTopK) return hipErrorInvalidValue;
+    if ((p.T + 64 / p.K - 1) / (64 / p.K) > kSmallGroups) return hipErrorInvalidValue;
+    const size_t lds = (size_t)p.E * p.d * 2;
+    dim3 grid(1), block(64 * kSmallWaves);
+    // At least 32 expert lanes (at most 2 rows per wave) keeps the 16-wave
+    // kernel within 128 VGPRs. Lanes past E add exact zeros / -inf to the
+    // softmax butterflies, so the results equal the narrower layout's.
+    switch (router_ep(p.E)) {
+        case 8:
+        case 16:
+        case 32: route_small_kernel<32><<<grid, block, lds, s>>>(p, sp, pp); break;
+        case 64: route_small_kernel<64><<<grid, block, lds, s>>>(p, sp, pp); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

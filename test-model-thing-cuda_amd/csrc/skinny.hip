@@ -133,6 +133,76 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(GemmParams p, int
     }
 }
 
+// Variant for reduction lengths K = NW * 32J (J = 8: K a multiple of 256
+// up to 4096; J = 2: a multiple of 64 up to 1024): the workgroup has NW
+// waves and wave w owns one K-chunk, [32Jw, 32J(w+1)); lane group g holds
+// k = 32Jw + 8Jg + 8i .. +7 for MFMA i. Every weight load of the tile is
+// issued at once (J per lane), then each 16-row block of the expert loads
+// its activation chunk and multiplies; blocks past the expert's count are
+// skipped as a whole (uniform branch). No load sits under a divergent
+// branch, so the compiler's wait counts stay exact.
+template <int KIND, bool DUAL, int J, int RB>
+__global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int nexp) {
+    static_assert(KIND == GEMM_UP || KIND == GEMM_DOWN, "forward GEMMs only");
+    constexpr bool kGather = KIND == GEMM_UP;
+    extern __shared__ f32x4 red[];  // [RB][nw][64] wave partials
+
+    const int nw = (int)blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rank = (int)blockIdx.x % nexp, tile = (int)blockIdx.x / nexp;
+    const int e = p.order[rank];
+    const int row0 = p.offsets[e];
+    const int rows = min(p.offsets[e + 1] - row0, 16 * RB);
+    if (rows <= 0) return;
+    const int nrb = (rows + 15) >> 4;
+    const int g = lane >> 4, li = lane & 15;
+    const int kw = wave * (32 * J) + g * (8 * J);
+
+    uint4 wv[J];
+    {
+        const uint16_t* src = p.w[e] + (int64_t)(tile * 16 + li) * p.ldb + kw;
+#pragma unroll
+        for (int i = 0; i < J; ++i) wv[i] = ld16(src + 8 * i);
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        if (rb >= nrb) break;  // uniform
+        const int m = rb * 16 + li;
+        const bool ok = m < rows;
+        const int slot = row0 + (ok ? m : 0);
+        const int srow = kGather ? p.perm[slot] : slot;
+        const uint16_t* ar = p.a + (int64_t)srow * p.lda + kw;
+        uint4 av[J];
+#pragma unroll
+        for (int i = 0; i < J; ++i) av[i] = ld16(ar + 8 * i);
+        if (!ok) {
+#pragma unroll
+            for (int i = 0; i < J; ++i) av[i] = make_uint4(0, 0, 0, 0);
+        }
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < J; ++i) acc = mfma16(wv[i], av[i], acc);
+        red[(rb * nw + wave) * 64 + lane] = acc;
+    }
+    __syncthreads();
+
+    // Output (m, n) of a row block = lane (n/4)*16 + m, element n%4; the wave
+    // partials are added in wave order.
+    uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
+    for (int o = tid; o < nrb * 256; o += (int)blockDim.x) {
+        const int rb = o >> 8, m = (o >> 4) & 15, n = o & 15;
+        const int row = rb * 16 + m;
+        if (row >= rows) continue;
+        const int sl = (n >> 2) * 16 + m, r = n & 3;
+        float v = red[(rb * nw) * 64 + sl][r];
+        for (int w2 = 1; w2 < nw; ++w2) v += red[(rb * nw + w2) * 64 + sl][r];
+        const int64_t off = (int64_t)(row0 + row) * p.ldc + tile * 16 + n;
+        C[off] = f2bf(v);
+        if constexpr (DUAL) p.c2[off] = f2bf(silu_fast(v));
+    }
+}
+
 template <int KIND, bool DUAL>
 hipError_t launch_rb(int rb, const GemmParams& p, int nexp, unsigned grid, hipStream_t s) {
     switch (rb) {
@@ -144,21 +214,54 @@ hipError_t launch_rb(int rb, const GemmParams& p, int nexp, unsigned grid, hipSt
     return hipGetLastError();
 }
 
+template <int KIND, bool DUAL, int J>
+hipError_t launch_chunk_rb(int rb, int nw, const GemmParams& p, int nexp, hipStream_t s) {
+    const unsigned grid = (unsigned)(p.N / 16) * (unsigned)nexp;
+    const dim3 block(64 * nw);
+    const size_t lds = (size_t)rb * nw * 64 * sizeof(f32x4);
+    switch (rb) {
+        case 1: skinny_chunk_kernel<KIND, DUAL, J, 1><<<grid, block, lds, s>>>(p, nexp); break;
+        case 2: skinny_chunk_kernel<KIND, DUAL, J, 2><<<grid, block, lds, s>>>(p, nexp); break;
+        case 4: skinny_chunk_kernel<KIND, DUAL, J, 4><<<grid, block, lds, s>>>(p, nexp); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+template <int KIND, bool DUAL>
+hipError_t launch_chunk(int J, int rb, int nw, const GemmParams& p, int nexp, hipStream_t s) {
+    return J == 8 ? launch_chunk_rb<KIND, DUAL, 8>(rb, nw, p, nexp, s)
+                  : launch_chunk_rb<KIND, DUAL, 2>(rb, nw, p, nexp, s);
+}
+
 }  // namespace
 
 hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s) {
     if (T <= 0) return hipSuccess;
     if (T > kSkinnyMaxTokens || p.N % 16 != 0 || p.K % 64 != 0 || p.N <= 0) return hipErrorInvalidValue;
-    const int rb = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
+    if (kind != GEMM_UP && kind != GEMM_DOWN) return hipErrorInvalidValue;
     const int nexp = min(p.E, p.slots);
-    const unsigned grid = (unsigned)(p.N / 16) * (unsigned)nexp;
-    switch (kind) {
-        case GEMM_UP:
-            return dual ? launch_rb<GEMM_UP, true>(rb, p, nexp, grid, s)
-                        : launch_rb<GEMM_UP, false>(rb, p, nexp, grid, s);
-        case GEMM_DOWN: return launch_rb<GEMM_DOWN, false>(rb, p, nexp, grid, s);
-        default: return hipErrorInvalidValue;
+    // One K-chunk per wave, at most 16 waves.
+    int J = 0, nw = 0;
+    if (p.K % 256 == 0 && p.K / 256 >= 4 && p.K / 256 <= 16) {
+        J = 8;
+        nw = p.K / 256;
+    } else if (p.K / 64 <= 16) {
+        J = 2;
+        nw = p.K / 64;
     }
+    const int rb = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
+    if (J > 0) {
+        if (kind == GEMM_UP)
+            return dual ? launch_chunk<GEMM_UP, true>(J, rb, nw, p, nexp, s)
+                        : launch_chunk<GEMM_UP, false>(J, rb, nw, p, nexp, s);
+        return launch_chunk<GEMM_DOWN, false>(J, rb, nw, p, nexp, s);
+    }
+    // General reduction lengths: K split over 4 waves in 64-element units.
+    const unsigned grid = (unsigned)(p.N / 16) * (unsigned)nexp;
+    if (kind == GEMM_UP)
+        return dual ? launch_rb<GEMM_UP, true>(rb, p, nexp, grid, s)
+                    : launch_rb<GEMM_UP, false>(rb, p, nexp, grid, s);
+    return launch_rb<GEMM_DOWN, false>(rb, p, nexp, grid, s);
 }
 
 }  // namespace tmt

@@ -275,6 +275,8 @@ def test_decode_steps_against_oracle(orc, T):
     (40, 512, 64, 8, 128),   # widest router, top-8, up to 40 rows per expert
     (64, 256, 1, 1, 0),      # dense path at the decode-kernel limit
     (65, 192, 5, 2, 320),    # first token count on the tiled path
+    (9, 128, 4, 2, 1088),    # down-projection K of 17 x 64: one tile per workgroup
+    (33, 256, 8, 2, 2048),   # three 16-row blocks, 8 waves of 256-element chunks
 ])
 def test_decode_shapes_against_oracle(orc, T, d, E, K, h):
     """Decode-sized batches (T <= 64 use the weight-streaming expert GEMMs);
