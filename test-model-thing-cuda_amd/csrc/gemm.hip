@@ -15,10 +15,10 @@
 // (32 KiB each), issued three tiles ahead of the MFMAs that use them.
 //   * K-contiguous operands (activations in every GEMM, weights in the
 //     forward) land as [256 rows][32] bf16, 16-byte chunks XOR-swizzled by
-//     (row >> 1) & 3, and are read with ds_read_b128.
+//     (row >> 2) & 3, and are read with ds_read_b128.
 //   * Row-contiguous operands (weights read as [K][N] in the backward, and
 //     the token-major operands of the weight-gradient GEMMs) land as
-//     [32 k][256] bf16, chunks swizzled by 2 * (k & 3), and are read with the
+//     [32 k][256] bf16, chunks swizzled by 4 * (k & 3), and are read with the
 //     gfx950 transposing ds_read_b64_tr_b16: inside each 16-lane group, lane
 //     r points at row k0 + r/4, columns c0 + 4(r%4) .. +3, and lane i receives
 //     column c0 + i of rows k0 .. k0+3 -- a K-contiguous MFMA fragment.
@@ -39,30 +39,47 @@ namespace tmt {
 namespace {
 
 constexpr int BM = 256;
-constexpr int BN = 256;
-constexpr int WTM = 128, WTN = 128;       // wave tile
-constexpr int MI = WTM / 32, NJ = WTN / 32;
-constexpr int LDS_BYTES = 128 * 1024;     // LDS ring (and epilogue staging) per workgroup
+constexpr int WTM = 128;                  // wave tile rows (2 x 2 waves)
+constexpr int MI = WTM / 32;
 
-// K-step geometry. BK_ is the K depth of one LDS stage (32 or 64), NST the
-// number of stages in the ring.
-template <int BK_, int NST>
+// Tile geometry. BK_ is the K depth of one LDS stage (32 or 64), NST the
+// number of stages in the ring, BN_ the tile width (256: one workgroup per
+// CU, 128 x 128 wave tiles; 128: two workgroups per CU, 128 x 64 wave tiles,
+// so one workgroup's waits and epilogue overlap the other's MFMAs).
+template <int BK_, int NST, int BN_>
 struct Geo {
     static constexpr int BK = BK_;
     static constexpr int NSTAGE = NST;
+    static constexpr int BN = BN_;
+    static constexpr int WTN = BN / 2, NJ = WTN / 32;  // wave tile columns
     static constexpr int KCH = BK / 8;                 // 16-byte chunks per K-contiguous row
-    static constexpr int OPND = 256 * BK;              // bf16 elements of one operand tile
-    static constexpr int STAGE = 2 * OPND;             // A then B
-    static constexpr int DMA_PER_OPND = OPND * 2 / 1024 / 4;  // 1 KiB wave loads per operand per wave
-    static constexpr int DMA_PER_TILE = 2 * DMA_PER_OPND;
+    static constexpr int OPND_A = BM * BK;             // bf16 elements of the A tile
+    static constexpr int OPND_B = BN * BK;             // bf16 elements of the B tile
+    static constexpr int STAGE = OPND_A + OPND_B;      // A then B
+    static constexpr int DMA_A = OPND_A * 2 / 1024 / 4;  // 1 KiB wave loads per wave, A tile
+    static constexpr int DMA_B = OPND_B * 2 / 1024 / 4;  // ... B tile
+    static constexpr int DMA_PER_TILE = DMA_A + DMA_B;
     static constexpr int KC_ROWS = 1024 / (2 * BK);    // K-contiguous rows per wave load
     static constexpr int STEPS = BK / 16;              // MFMA k16 steps per stage
-    static_assert(NST * STAGE * 2 <= 160 * 1024, "LDS ring too large");
-    // K-contiguous rows: 16-byte chunk swizzle making 8 consecutive rows hit
-    // distinct banks for ds_read_b128.
+    static constexpr int WGS = BN == 256 ? 1 : 2;      // workgroups per CU
+    // LDS of the ring, also the epilogue's fp32 staging ([64][WTN] per wave)
+    static constexpr int RING = NST * STAGE * 2;
+    static constexpr int EPI = 4 * 64 * WTN * 4;
+    static constexpr int LDS = RING > EPI ? RING : EPI;
+    static_assert(LDS * WGS <= 160 * 1024, "LDS ring too large");
+    // K-contiguous rows: 16-byte chunk swizzle making 16 consecutive rows (the
+    // lanes one ds_read_b128 cycle serves from the 64 banks = 256 bytes) hit
+    // distinct banks: rows r and r + 4j share (r & 3) * 64 bytes of bank offset
+    // (BK 32: 64-byte rows), so the chunk is XORed with (r >> 2) & 3; with
+    // 128-byte rows (BK 64) rows r and r + 2j pair up, XOR with (r >> 1) & 7.
     static __device__ __forceinline__ int kc_swz(int r) {
-        return KCH == 4 ? ((r >> 1) & 3) : ((r ^ (r >> 3)) & 7);
+        return KCH == 4 ? ((r >> 2) & 3) : ((r >> 1) & 7);
     }
+    // Row-contiguous [BK][256 or 128] tiles (rows of 512 / 256 bytes, all
+    // starting at bank 0): the 32 lanes of one ds_read_b64_tr_b16 cycle read
+    // 4 k rows x 4 chunks; XOR with 4 * (k & 3) spreads them over 16 distinct
+    // chunks (256 bytes).
+    static __device__ __forceinline__ int mc_swz(int k) { return 4 * (k & 3); }
 };
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -156,21 +173,23 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
 }
 
-template <int KIND, bool DUAL, int BK_, int NST>
-__global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p) {
+template <int KIND, bool DUAL, int BK_, int NST, int BN_>
+__global__ __launch_bounds__(kThreads, (BN_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
     using Tr = Traits<KIND>;
-    using Gm = Geo<BK_, NST>;
-    constexpr int BK = Gm::BK, NSTAGE = Gm::NSTAGE, OPND = Gm::OPND;
-    constexpr int DMA_PER_OPND = Gm::DMA_PER_OPND;
+    using Gm = Geo<BK_, NST, BN_>;
+    constexpr int BK = Gm::BK, NSTAGE = Gm::NSTAGE, BN = Gm::BN, WTN = Gm::WTN, NJ = Gm::NJ;
+    constexpr int OPND_A = Gm::OPND_A;
+    constexpr int DMA_A = Gm::DMA_A, DMA_B = Gm::DMA_B;
     // MXFP4 B operand per stage: 256 rows x 16 bytes of codes (BK = 32 = one
     // scale block), then one 1 KiB copy of the 256 row scales per wave.
-    static_assert(!Tr::b_fp4 || BK == 32, "MXFP4 tiles cover exactly one scale block");
+    static_assert(!Tr::b_fp4 || (BK == 32 && BN == 256), "MXFP4 tiles: one scale block, 256 columns");
     constexpr int FP4_CODES = 256 * 16, FP4_SCALES = 4 * 1024;
-    constexpr int STAGE = Tr::b_fp4 ? OPND + (FP4_CODES + FP4_SCALES) / 2 : Gm::STAGE;  // bf16 elements
-    constexpr int DMA_PER_TILE = Tr::b_fp4 ? DMA_PER_OPND + 2 : Gm::DMA_PER_TILE;
+    constexpr int STAGE = Tr::b_fp4 ? OPND_A + (FP4_CODES + FP4_SCALES) / 2 : Gm::STAGE;  // bf16 elements
+    constexpr int DMA_PER_TILE = Tr::b_fp4 ? DMA_A + 2 : Gm::DMA_PER_TILE;
     constexpr int KCH = Gm::KCH, KC_ROWS = Gm::KC_ROWS, STEPS = Gm::STEPS;
-    static_assert(NSTAGE * STAGE * 2 <= LDS_BYTES + 32 * 1024, "LDS ring too large");
-    __shared__ uint4 lds_raw[(NSTAGE * STAGE * 2 > LDS_BYTES ? NSTAGE * STAGE * 2 : LDS_BYTES) / 16];
+    constexpr int LDS_TOTAL = NSTAGE * STAGE * 2 > Gm::EPI ? NSTAGE * STAGE * 2 : Gm::EPI;
+    static_assert(LDS_TOTAL * Gm::WGS <= 160 * 1024, "LDS ring too large");
+    __shared__ uint4 lds_raw[LDS_TOTAL / 16];
     uint16_t* lds = reinterpret_cast<uint16_t*>(lds_raw);
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -232,20 +251,21 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
     const int nk = (kend - kbeg + BK - 1) / BK;
 
     // ---- DMA addressing -----------------------------------------------------
-    // K-contiguous tile: wave load q = 4*wave + i covers rows 16q .. 16q+15;
-    // lane -> row 16q + lane/4, physical chunk lane%4, logical chunk
-    // (lane%4) ^ ((row >> 1) & 3). Row-contiguous tile: wave load q covers k
-    // rows 2q, 2q+1; lane -> k = 2q + lane/32, physical chunk lane%32, logical
-    // chunk (lane%32) ^ (2 * (k & 3)).
+    // K-contiguous tile: wave load q covers rows KC_ROWS*q .. +KC_ROWS-1;
+    // lane -> row KC_ROWS*q + lane/KCH, physical chunk lane%KCH, logical chunk
+    // (lane%KCH) ^ kc_swz(row). Row-contiguous tile of C chunks per k row
+    // (32 for 256 columns, 16 for 128): wave load q covers k rows
+    // (64/C)q .. ; lane -> k = (64/C)q + lane/C, physical chunk lane%C,
+    // logical chunk (lane%C) ^ mc_swz(k).
     // K-contiguous operands keep one source pointer per wave load; row-
     // contiguous ones keep a column pointer and the lane's k row, clamped to
     // the last valid reduction index when issued (the tail is zeroed in LDS).
-    const uint16_t* a_ptr[DMA_PER_OPND];
-    const uint16_t* b_ptr[DMA_PER_OPND];
-    int a_k[DMA_PER_OPND], b_k[DMA_PER_OPND];
+    const uint16_t* a_ptr[DMA_A];
+    const uint16_t* b_ptr[DMA_B];
+    int a_k[DMA_A], b_k[DMA_B];
 #pragma unroll
-    for (int i = 0; i < DMA_PER_OPND; ++i) {
-        const int q = wave * DMA_PER_OPND + i;
+    for (int i = 0; i < DMA_A; ++i) {
+        const int q = wave * DMA_A + i;
         if constexpr (Tr::a_kc) {
             const int r = KC_ROWS * q + lane / KCH;
             const int c = (lane % KCH) ^ Gm::kc_swz(r);
@@ -255,10 +275,14 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             a_k[i] = 0;
         } else {
             const int k = 2 * q + (lane >> 5);
-            const int c = (lane & 31) ^ (2 * (k & 3));
+            const int c = (lane & 31) ^ Gm::mc_swz(k);
             a_ptr[i] = p.a + min(mt * BM + c * 8, p.M - 8);
             a_k[i] = k;
         }
+    }
+#pragma unroll
+    for (int i = 0; i < DMA_B; ++i) {
+        const int q = wave * DMA_B + i;
         if constexpr (Tr::b_fp4) {
             b_ptr[i] = nullptr;
             b_k[i] = 0;
@@ -269,8 +293,9 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             b_ptr[i] = p.w[e] + (int64_t)n * p.ldb + c * 8;
             b_k[i] = 0;
         } else {
-            const int k = 2 * q + (lane >> 5);
-            const int c = (lane & 31) ^ (2 * (k & 3));
+            constexpr int C = BN / 8;
+            const int k = (64 / C) * q + lane / C;
+            const int c = (lane % C) ^ Gm::mc_swz(k);
             const uint16_t* base = Tr::group_k ? p.b : p.w[e];
             b_ptr[i] = base + min(nt * BN + c * 8, p.N - 8);
             b_k[i] = k;
@@ -294,19 +319,24 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
         const int k0 = kbeg + min(t, nk - 1) * BK;  // first reduction index of the tile
         const uint32_t sbase = lds0 + (uint32_t)((t % NSTAGE) * STAGE) * 2u;
 #pragma unroll
-        for (int i = 0; i < DMA_PER_OPND; ++i) {
-            const uint32_t qoff = (uint32_t)(wave * DMA_PER_OPND + i) * 1024u;
+        for (int i = 0; i < DMA_A; ++i) {
+            const uint32_t qoff = (uint32_t)(wave * DMA_A + i) * 1024u;
             const uint16_t* ga = Tr::a_kc ? a_ptr[i] + k0
                                           : a_ptr[i] + (int64_t)min(k0 + a_k[i], kend - 1) * p.lda;
-            const uint16_t* gb = Tr::b_kc ? b_ptr[i] + k0
-                                          : b_ptr[i] + (int64_t)min(k0 + b_k[i], kend - 1) * p.ldb;
             dma16(ga, sbase + qoff);
-            if constexpr (!Tr::b_fp4) dma16(gb, sbase + OPND * 2u + qoff);
         }
-        if constexpr (Tr::b_fp4) {
+        if constexpr (!Tr::b_fp4) {
+#pragma unroll
+            for (int i = 0; i < DMA_B; ++i) {
+                const uint32_t qoff = (uint32_t)(wave * DMA_B + i) * 1024u;
+                const uint16_t* gb = Tr::b_kc ? b_ptr[i] + k0
+                                              : b_ptr[i] + (int64_t)min(k0 + b_k[i], kend - 1) * p.ldb;
+                dma16(gb, sbase + OPND_A * 2u + qoff);
+            }
+        } else {
             const int kb = k0 / 32;  // scale block of this tile
-            dma16(q_ptr + kb * 16, sbase + OPND * 2u + (uint32_t)wave * 1024u);
-            dma16(sc_ptr + (int64_t)kb * p.N, sbase + OPND * 2u + FP4_CODES + (uint32_t)wave * 1024u);
+            dma16(q_ptr + kb * 16, sbase + OPND_A * 2u + (uint32_t)wave * 1024u);
+            dma16(sc_ptr + (int64_t)kb * p.N, sbase + OPND_A * 2u + FP4_CODES + (uint32_t)wave * 1024u);
         }
     };
     // Reduction tail of the weight-gradient GEMMs: zero k rows >= kvalid of
@@ -316,10 +346,10 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             const int kvalid = kend - (kbeg + t * BK);
             if (kvalid < BK) {
                 uint16_t* st = lds + (t % NSTAGE) * STAGE;
-                const int nvec = (BK - kvalid) * 32;  // 16-byte vectors per operand
-                for (int v = tid; v < 2 * nvec; v += kThreads) {
-                    const int opnd = v >= nvec, w = v - opnd * nvec;
-                    *reinterpret_cast<uint4*>(st + opnd * OPND + kvalid * 256 + w * 8) = make_uint4(0, 0, 0, 0);
+                const int na = (BK - kvalid) * (BM / 8), nb = (BK - kvalid) * (BN / 8);  // 16-byte vectors
+                for (int v = tid; v < na + nb; v += kThreads) {
+                    if (v < na) *reinterpret_cast<uint4*>(st + kvalid * BM + v * 8) = make_uint4(0, 0, 0, 0);
+                    else *reinterpret_cast<uint4*>(st + OPND_A + kvalid * BN + (v - na) * 8) = make_uint4(0, 0, 0, 0);
                 }
             }
         }
@@ -337,7 +367,7 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
     };
     // Row-contiguous: two transposing reads give k = 16s + 8(lane/32) + 0..7
     // for column cbase + lane%32.
-    auto read_mc = [&](const uint16_t* t, int cbase, int s) {
+    auto read_mc = [&](const uint16_t* t, int stride, int cbase, int s) {
         const int g = lane >> 4, r = lane & 15;
         const int col = cbase + 16 * (g & 1) + 4 * (r & 3);
         const int kb = 16 * s + 8 * (g >> 1) + (r >> 2);
@@ -345,9 +375,9 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int k = kb + 4 * h;
-            const int c = (col >> 3) ^ (2 * (k & 3));
+            const int c = (col >> 3) ^ Gm::mc_swz(k);
             const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (lds_s16x4*)(t + k * 256 + c * 8 + (col & 7)));
+                (lds_s16x4*)(t + k * stride + c * 8 + (col & 7)));
             w[2 * h] = (uint32_t)(uint16_t)v[0] | ((uint32_t)(uint16_t)v[1] << 16);
             w[2 * h + 1] = (uint32_t)(uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16);
         }
@@ -365,14 +395,14 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
     };
     auto load_frag = [&](Frag& f, int t, int s) {
         const uint16_t* tA = lds + (t % NSTAGE) * STAGE;
-        const uint16_t* tB = tA + OPND;
+        const uint16_t* tB = tA + OPND_A;
 #pragma unroll
         for (int i = 0; i < MI; ++i)
-            f.a[i] = Tr::a_kc ? read_kc(tA, wm * WTM + 32 * i, s) : read_mc(tA, wm * WTM + 32 * i, s);
+            f.a[i] = Tr::a_kc ? read_kc(tA, wm * WTM + 32 * i, s) : read_mc(tA, BM, wm * WTM + 32 * i, s);
 #pragma unroll
         for (int j = 0; j < NJ; ++j)
             f.b[j] = Tr::b_fp4 ? read_fp4(tB, wn * WTN + 32 * j, s)
-                               : (Tr::b_kc ? read_kc(tB, wn * WTN + 32 * j, s) : read_mc(tB, wn * WTN + 32 * j, s));
+                               : (Tr::b_kc ? read_kc(tB, wn * WTN + 32 * j, s) : read_mc(tB, BN, wn * WTN + 32 * j, s));
     };
 
     f32x16 acc[MI][NJ];
@@ -418,11 +448,11 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
                 if (s == 0) dma_tile(kt + NSTAGE - 1);
                 mma(f[s & 1]);
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
+                for (int q = 0; q < MI * NJ / 2; ++q) {
                     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
                     __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
                 }
-                __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, MI * NJ / 2, 0);
                 __builtin_amdgcn_sched_barrier(0);
             }
             if constexpr (NSTAGE == 2) {
@@ -438,11 +468,11 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
             load_frag(f[0], min(kt + 1, nk - 1), 0);
             mma(f[1]);
 #pragma unroll
-            for (int q = 0; q < 8; ++q) {
+            for (int q = 0; q < MI * NJ / 2; ++q) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 8, 1);
+            __builtin_amdgcn_sched_group_barrier(0x008, MI * NJ / 2, 1);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -451,10 +481,13 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
 
     // ---- epilogue ---------------------------------------------------------
     // acc[i][j][r] = C[m][n] with m = wm*128 + 32i + (lane&31) and
-    // n = wn*128 + 32j + 8(r>>2) + 4(lane>>5) + (r&3). Two passes of 64 rows per
-    // wave go through a 32 KiB fp32 LDS region ([64][128], 16-byte chunks
-    // swizzled by row & 31), then leave as row-contiguous 16-byte stores.
-    float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (64 * 128);
+    // n = wn*WTN + 32j + 8(r>>2) + 4(lane>>5) + (r&3). Two passes of 64 rows per
+    // wave go through an fp32 LDS region ([64][WTN], 16-byte chunks swizzled by
+    // row), then leave as row-contiguous 16-byte stores.
+    constexpr int CH = WTN / 4;              // 16-byte fp32 chunks per staged row
+    constexpr int LPR = WTN / 8, RPI = 64 / LPR;     // bf16 out: lanes per row, rows per instruction
+    constexpr int FLPR = WTN / 4, FRPI = 64 / FLPR;  // fp32 out
+    float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (64 * WTN);
     const int mbase = wm * WTM, nbase = wn * WTN;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
@@ -467,35 +500,35 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int ch = j * 8 + 2 * q + (lane >> 5);
-                    *reinterpret_cast<f32x4*>(stage_f + lr * 128 + ((ch ^ (lr & 31)) * 4)) =
+                    *reinterpret_cast<f32x4*>(stage_f + lr * WTN + ((ch ^ (lr & (CH - 1))) * 4)) =
                         f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
                               acc[i][j][4 * q + 3]};
                 }
         }
         __syncthreads();
         if constexpr (!Tr::group_k) {
-            // 16 lanes per row (8 bf16 each), 4 rows per instruction
+            // LPR lanes per row (8 bf16 each), RPI rows per instruction
             uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
-            const int cl = lane & 15;
+            const int cl = lane % LPR;
             const int n = nbase + cl * 8;
-            uint4 uin[16];  // GEMM_DACT: pre-activations, all loads issued first
+            uint4 uin[64 / RPI];  // GEMM_DACT: pre-activations, all loads issued first
             if constexpr (KIND == GEMM_DACT) {
 #pragma unroll
-                for (int k = 0; k < 16; ++k) {
-                    const int m = mbase + pass * 64 + (lane >> 4) + 4 * k;
+                for (int k = 0; k < 64 / RPI; ++k) {
+                    const int m = mbase + pass * 64 + lane / LPR + RPI * k;
                     const bool ok = m < mlim && n < nlim;
                     const int64_t off = (int64_t)(row0 + (ok ? m : 0)) * p.ldc + nt * BN + (ok ? n : 0);
                     uin[k] = ld16_nt(p.u + off);
                 }
             }
 #pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                const int rr = (lane >> 4) + 4 * k;
+            for (int k = 0; k < 64 / RPI; ++k) {
+                const int rr = lane / LPR + RPI * k;
                 const int m = mbase + pass * 64 + rr;
                 if (m >= mlim || n >= nlim) continue;
-                const float* src = stage_f + rr * 128;
-                const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + (((2 * cl) ^ (rr & 31)) * 4));
-                const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + (((2 * cl + 1) ^ (rr & 31)) * 4));
+                const float* src = stage_f + rr * WTN;
+                const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + (((2 * cl) ^ (rr & (CH - 1))) * 4));
+                const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + (((2 * cl + 1) ^ (rr & (CH - 1))) * 4));
                 float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                 const int64_t off = (int64_t)(row0 + m) * p.ldc + nt * BN + n;
                 if constexpr (KIND == GEMM_DACT) {
@@ -512,15 +545,15 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
                 }
             }
         } else {
-            // 32 lanes per row (4 fp32 each), 2 rows per instruction
+            // FLPR lanes per row (4 fp32 each), FRPI rows per instruction
             float* C = p.dw[e];
-            const int cl = lane & 31;
+            const int cl = lane % FLPR;
 #pragma unroll 4
-            for (int rr = lane >> 5; rr < 64; rr += 2) {
+            for (int rr = lane / FLPR; rr < 64; rr += FRPI) {
                 const int m = mbase + pass * 64 + rr;
                 const int n = nbase + cl * 4;
                 if (m >= mlim || n >= nlim) continue;
-                const f32x4 v = *reinterpret_cast<const f32x4*>(stage_f + rr * 128 + ((cl ^ (rr & 31)) * 4));
+                const f32x4 v = *reinterpret_cast<const f32x4*>(stage_f + rr * WTN + ((cl ^ (rr & (CH - 1))) * 4));
                 st16_nt(C + (int64_t)(mt * BM + m) * p.ldc + nt * BN + n, v);
             }
         }
@@ -532,12 +565,35 @@ __global__ __launch_bounds__(kThreads, 1) void grouped_gemm_kernel(GemmParams p)
 
 constexpr int kBK = 32, kNST = 4;  // fastest of BK 32/64 x 2-4 stages on the c3 shapes
 
-hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s) {
+template <int KIND, bool DUAL, int BN>
+hipError_t launch_kind(const GemmParams& p, unsigned grid, hipStream_t s) {
+    constexpr int NST = BN == 256 ? kNST : 3;  // two workgroups per CU at BN 128: 3 x 24 KiB stages
+    grouped_gemm_kernel<KIND, DUAL, kBK, NST, BN><<<grid, kThreads, 0, s>>>(p);
+    return hipGetLastError();
+}
+
+// Tile width per GEMM kind (BN 128 = two workgroups per CU). Measured on the
+// c3 shapes with random operands: the second workgroup hides the heavy
+// epilogues (UP writes U and SiLU(U), DACT reads U) and the weight-gradient
+// tails; DOWN and DX are main-loop bound and lose to the 50% larger operand
+// traffic of the narrower tile.
+int gemm_tile_n(GemmKind kind) {
+    switch (kind) {
+        case GEMM_UP:
+        case GEMM_DACT:
+        case GEMM_DW_DOWN:
+        case GEMM_DW_UP: return 128;
+        default: return 256;
+    }
+}
+
+hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn, hipStream_t s) {
     if (p.N % 8 != 0 || p.N <= 0) return hipErrorInvalidValue;
-    dim3 block(kThreads);
+    if (bn != 256 && bn != 128) return hipErrorInvalidValue;
     const bool group_k = kind == GEMM_DW_DOWN || kind == GEMM_DW_UP;
-    if ((kind == GEMM_UP_FP4 || kind == GEMM_DOWN_FP4) && p.K % 32 != 0) return hipErrorInvalidValue;
-    const int64_t ntn = (p.N + BN - 1) / BN;
+    const bool fp4 = kind == GEMM_UP_FP4 || kind == GEMM_DOWN_FP4;
+    if (fp4 && (p.K % 32 != 0 || bn != 256)) return hipErrorInvalidValue;
+    const int64_t ntn = (p.N + bn - 1) / bn;
     const int64_t gn = ntn < 8 ? ntn : 8, gm = 32 / gn;
     const int64_t ngn = (ntn + gn - 1) / gn;
     int64_t groups;
@@ -556,24 +612,25 @@ hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_
     if (grid <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     const unsigned g = (unsigned)grid;
+#define TMT_BN(KIND_, DUAL_) \
+    (bn == 256 ? launch_kind<KIND_, DUAL_, 256>(p, g, s) : launch_kind<KIND_, DUAL_, 128>(p, g, s))
     switch (kind) {
-        case GEMM_UP:
-            if (dual) grouped_gemm_kernel<GEMM_UP, true, kBK, kNST><<<g, block, 0, s>>>(p);
-            else grouped_gemm_kernel<GEMM_UP, false, kBK, kNST><<<g, block, 0, s>>>(p);
-            break;
-        case GEMM_DOWN: grouped_gemm_kernel<GEMM_DOWN, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
-        case GEMM_DACT: grouped_gemm_kernel<GEMM_DACT, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
-        case GEMM_DX: grouped_gemm_kernel<GEMM_DX, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
-        case GEMM_DW_DOWN: grouped_gemm_kernel<GEMM_DW_DOWN, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
-        case GEMM_DW_UP: grouped_gemm_kernel<GEMM_DW_UP, false, kBK, kNST><<<g, block, 0, s>>>(p); break;
+        case GEMM_UP: return dual ? TMT_BN(GEMM_UP, true) : TMT_BN(GEMM_UP, false);
+        case GEMM_DOWN: return TMT_BN(GEMM_DOWN, false);
+        case GEMM_DACT: return TMT_BN(GEMM_DACT, false);
+        case GEMM_DX: return TMT_BN(GEMM_DX, false);
+        case GEMM_DW_DOWN: return TMT_BN(GEMM_DW_DOWN, false);
+        case GEMM_DW_UP: return TMT_BN(GEMM_DW_UP, false);
         case GEMM_UP_FP4:
-            if (dual) grouped_gemm_kernel<GEMM_UP_FP4, true, 32, kNST><<<g, block, 0, s>>>(p);
-            else grouped_gemm_kernel<GEMM_UP_FP4, false, 32, kNST><<<g, block, 0, s>>>(p);
-            break;
-        case GEMM_DOWN_FP4: grouped_gemm_kernel<GEMM_DOWN_FP4, false, 32, kNST><<<g, block, 0, s>>>(p); break;
+            return dual ? launch_kind<GEMM_UP_FP4, true, 256>(p, g, s) : launch_kind<GEMM_UP_FP4, false, 256>(p, g, s);
+        case GEMM_DOWN_FP4: return launch_kind<GEMM_DOWN_FP4, false, 256>(p, g, s);
         default: return hipErrorInvalidValue;
     }
-    return hipGetLastError();
+#undef TMT_BN
+}
+
+hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s) {
+    return launch_gemm_bn(kind, dual, p, gemm_tile_n(kind), s);
 }
 
 }  // namespace tmt

@@ -100,6 +100,8 @@ struct GemmParams {
     const uint8_t* wsc[kMaxExperts];  // MXFP4 scales: e8m0 [K/32][N]
 };
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s);
+// Same with an explicit tile width (256, or 128 = two workgroups per CU).
+hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn, hipStream_t s);
 
 // Decode-sized forward GEMMs (GEMM_UP / GEMM_DOWN, bf16 weights) for
 // T <= kSkinnyMaxTokens tokens: every expert then owns at most T rows.

@@ -125,84 +125,148 @@ __global__ __launch_bounds__(kThreads) void combine_bwd_kernel(CombineBwdParams 
     if (ev) p.dlogits[(int64_t)r * E + e] = dl;
 }
 
-// Pass 1: block (chunk, column block, expert block) accumulates 16 experts x
-// 4 columns per thread over its rows in ascending order.
+// dWr = dlogits^T X is a GEMM with a long reduction (T rows) and a thin
+// output (E x d), so it is split over row chunks.
+// Pass 1: block (chunk, 256-column block, 16-expert block); lane l of every
+// wave owns columns 4l..4l+3 of the block, wave w the rows w, w+4, ... of
+// the chunk. Each wave accumulates 16 experts x 4 columns per lane over its
+// rows in ascending order, with the X loads of the next 8 rows in flight;
+// the four wave partials are then added in wave order through LDS.
 constexpr int kDwExperts = 16;
+constexpr int kDwCols = 256;
+constexpr int kDwUnroll = 8;
+constexpr int kDwRows = 512;  // most rows of one chunk (router_dw_chunks)
 __global__ __launch_bounds__(kThreads) void router_dw_partial_kernel(RouterDwParams p) {
-    __shared__ float s_dl[64][kDwExperts];
-    const int tid = threadIdx.x;
+    __shared__ f32x4 s_part[3][kDwExperts][64];
+    __shared__ f32x4 s_dl[kDwRows][kDwExperts / 4];  // the chunk's dlogits, experts e0 .. e0+15
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int chunk = blockIdx.x;
-    const int col = blockIdx.y * 1024 + tid * 4;
+    const int col = blockIdx.y * kDwCols + lane * 4;
     const int e0 = blockIdx.z * kDwExperts;
     const int E = p.E, d = p.d;
     const int ne = min(kDwExperts, E - e0);
-    const int rows_per = (p.T + p.nchunks - 1) / p.nchunks;
+    const int rows_per = (p.T + p.nchunks - 1) / p.nchunks;  // <= kDwRows
     const int r0 = chunk * rows_per, r1 = min(p.T, r0 + rows_per);
-    float acc[kDwExperts][4];
+    const int nr = max(0, r1 - r0);
+    {
+        // stage dlogits[r0 .. r1)[e0 .. e0+16) (zero past ne); loads issued first
+        float* dst = reinterpret_cast<float*>(s_dl);
+        constexpr int kPer = kDwRows * kDwExperts / kThreads;
+        float v[kPer];
 #pragma unroll
-    for (int q = 0; q < kDwExperts; ++q)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[q][t] = 0.0f;
-    for (int rb = r0; rb < r1; rb += 64) {
-        const int nr = min(64, r1 - rb);
-        __syncthreads();
-        for (int i = tid; i < 64 * kDwExperts; i += kThreads) {
-            const int rr = i / kDwExperts, q = i % kDwExperts;
-            s_dl[rr][q] = (rr < nr && q < ne) ? p.dlogits[(int64_t)(rb + rr) * E + e0 + q] : 0.0f;
+        for (int u = 0; u < kPer; ++u) {
+            const int i = tid + u * kThreads, rr = i / kDwExperts, q = i % kDwExperts;
+            const int r = r0 + min(rr, max(nr - 1, 0));
+            v[u] = (rr < nr && q < ne) ? p.dlogits[(int64_t)r * E + e0 + min(q, ne - 1)] : 0.0f;
         }
-        __syncthreads();
-        if (col < d) {
-            for (int rr = 0; rr < nr; ++rr) {
-                const uint2 xv = *reinterpret_cast<const uint2*>(p.X + (int64_t)(rb + rr) * d + col);
-                const float x0 = bf_lo(xv.x), x1 = bf_hi(xv.x), x2 = bf_lo(xv.y), x3 = bf_hi(xv.y);
 #pragma unroll
-                for (int q = 0; q < kDwExperts; ++q) {
-                    const float g = s_dl[rr][q];
-                    acc[q][0] += g * x0;
-                    acc[q][1] += g * x1;
-                    acc[q][2] += g * x2;
-                    acc[q][3] += g * x3;
+        for (int u = 0; u < kPer; ++u) dst[tid + u * kThreads] = v[u];
+    }
+    __syncthreads();
+    const bool cok = col < d;
+    const int ccol = cok ? col : 0;
+    f32x4 acc[kDwExperts];
+#pragma unroll
+    for (int q = 0; q < kDwExperts; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rb = wave; rb < nr; rb += 4 * kDwUnroll) {
+        uint2 xv[kDwUnroll];
+#pragma unroll
+        for (int u = 0; u < kDwUnroll; ++u) {
+            const int rr = min(rb + 4 * u, nr - 1);  // clamped; rows past the chunk are skipped below
+            xv[u] = *reinterpret_cast<const uint2*>(p.X + (int64_t)(r0 + rr) * d + ccol);
+        }
+#pragma unroll
+        for (int u = 0; u < kDwUnroll; ++u) {
+            const int rr = rb + 4 * u;
+            if (rr >= nr) break;  // wave-uniform
+            const float x0 = bf_lo(xv[u].x), x1 = bf_hi(xv[u].x), x2 = bf_lo(xv[u].y), x3 = bf_hi(xv[u].y);
+#pragma unroll
+            for (int q4 = 0; q4 < kDwExperts / 4; ++q4) {
+                const f32x4 g4 = s_dl[rr][q4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float g = g4[t];
+                    acc[4 * q4 + t][0] += g * x0;
+                    acc[4 * q4 + t][1] += g * x1;
+                    acc[4 * q4 + t][2] += g * x2;
+                    acc[4 * q4 + t][3] += g * x3;
                 }
             }
         }
     }
-    if (col < d) {
-        for (int q = 0; q < ne; ++q)
-            *reinterpret_cast<f32x4*>(p.partial + ((int64_t)chunk * E + e0 + q) * d + col) =
-                f32x4{acc[q][0], acc[q][1], acc[q][2], acc[q][3]};
+    if (wave > 0) {
+#pragma unroll
+        for (int q = 0; q < kDwExperts; ++q) s_part[wave - 1][q][lane] = acc[q];
+    }
+    __syncthreads();
+    if (wave == 0 && cok) {
+        for (int q = 0; q < ne; ++q) {
+            f32x4 v = acc[q];
+            v += s_part[0][q][lane];
+            v += s_part[1][q][lane];
+            v += s_part[2][q][lane];
+            *reinterpret_cast<f32x4*>(p.partial + ((int64_t)chunk * E + e0 + q) * d + col) = v;
+        }
     }
 }
 
-// Pass 2: dWr[e][k] = sum over chunks in ascending order.
+// Pass 2: dWr[e][k] = sum over chunks in ascending order; each thread owns
+// 4 consecutive outputs and keeps 8 chunk loads in flight.
 __global__ __launch_bounds__(kThreads) void router_dw_reduce_kernel(RouterDwParams p) {
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    const int64_t n = (int64_t)p.E * p.d;
+    const int64_t n = (int64_t)p.E * p.d;  // a multiple of 64
+    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
     if (i >= n) return;
-    float s = 0.0f;
-    for (int c = 0; c < p.nchunks; ++c) s += p.partial[(int64_t)c * n + i];
-    p.dWr[i] = s;
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+    int c = 0;
+    for (; c + 8 <= p.nchunks; c += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f32x4*>(p.partial + (int64_t)(c + u) * n + i);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; c < p.nchunks; ++c) s += *reinterpret_cast<const f32x4*>(p.partial + (int64_t)c * n + i);
+    *reinterpret_cast<f32x4*>(p.dWr + i) = s;
 }
 
-// One wave per row; Wr is staged in LDS for the router input gradient.
+// One wave per row. For the router input gradient, Wr and the block's rows
+// of dlogits are staged in LDS (all loads of a thread issued before its LDS
+// stores), so the per-expert loop reads only LDS.
 template <bool ROUTER>
 __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterParams p, int rows_per_block) {
     extern __shared__ uint4 smem_w[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d = p.d, K = p.K, E = p.E;
+    const int rbeg = blockIdx.x * rows_per_block;
+    const int rend = min(p.T, rbeg + rows_per_block);
+    float* s_dl = reinterpret_cast<float*>(smem_w + E * d / 8);  // [rows_per_block][E]
     if (ROUTER) {
         const uint4* src = reinterpret_cast<const uint4*>(p.Wr);
-        for (int i = threadIdx.x; i < E * d / 8; i += kThreads) smem_w[i] = src[i];
+        const int nvec = E * d / 8;
+        for (int i0 = threadIdx.x; i0 < nvec; i0 += 8 * kThreads) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = src[min(i0 + u * kThreads, nvec - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (i0 + u * kThreads < nvec) smem_w[i0 + u * kThreads] = v[u];
+        }
+        const int ndl = (rend - rbeg) * E;
+        for (int i = threadIdx.x; i < ndl; i += kThreads) s_dl[i] = p.dlogits[(int64_t)rbeg * E + i];
         __syncthreads();
     }
     const uint16_t* wl = reinterpret_cast<const uint16_t*>(smem_w);
-    const int rbeg = blockIdx.x * rows_per_block;
-    const int rend = min(p.T, rbeg + rows_per_block);
     for (int r = rbeg + wave; r < rend; r += 4) {
         int pos[kMaxTopK];
 #pragma unroll
         for (int j = 0; j < kMaxTopK; ++j)
             if (j < K) pos[j] = p.slot_of[(int64_t)r * K + j];
+        const float* dl = s_dl + (r - rbeg) * E;
         for (int c0 = lane * 8; c0 < d; c0 += 512) {
+            uint4 xv[kMaxTopK];
+#pragma unroll
+            for (int j = 0; j < kMaxTopK; ++j)
+                if (j < K) xv[j] = *reinterpret_cast<const uint4*>(p.dXg + (int64_t)pos[j] * d + c0);
             float acc[8];
 #pragma unroll
             for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
@@ -210,14 +274,14 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterParams p, int 
             for (int j = 0; j < kMaxTopK; ++j) {
                 if (j < K) {
                     float v[8];
-                    unpack8(*reinterpret_cast<const uint4*>(p.dXg + (int64_t)pos[j] * d + c0), v);
+                    unpack8(xv[j], v);
 #pragma unroll
                     for (int t = 0; t < 8; ++t) acc[t] += v[t];
                 }
             }
             if (ROUTER) {
                 for (int e = 0; e < E; ++e) {
-                    const float g = p.dlogits[(int64_t)r * E + e];
+                    const float g = dl[e];
                     float w[8];
                     unpack8(*reinterpret_cast<const uint4*>(wl + e * d + c0), w);
 #pragma unroll
@@ -247,16 +311,17 @@ hipError_t launch_combine_bwd(const CombineBwdParams& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Chunks of at most kDwRows rows (the LDS-staged dlogits block).
 int router_dw_chunks(int T) {
-    int c = (T + 127) / 128;
-    return c < 1 ? 1 : (c > 256 ? 256 : c);
+    const int c = (T + kDwRows - 1) / kDwRows;
+    return c < 1 ? 1 : c;
 }
 
 hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s) {
-    dim3 grid1(p.nchunks, (p.d + 1023) / 1024, (p.E + kDwExperts - 1) / kDwExperts);
+    dim3 grid1(p.nchunks, (p.d + kDwCols - 1) / kDwCols, (p.E + kDwExperts - 1) / kDwExperts);
     router_dw_partial_kernel<<<grid1, kThreads, 0, s>>>(p);
     const int64_t n = (int64_t)p.E * p.d;
-    router_dw_reduce_kernel<<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, s>>>(p);
+    router_dw_reduce_kernel<<<(unsigned)((n / 4 + kThreads - 1) / kThreads), kThreads, 0, s>>>(p);
     return hipGetLastError();
 }
 
@@ -266,7 +331,8 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
     const int rows_per_block = router ? 64 : 4;
     const int grid = (p.T + rows_per_block - 1) / rows_per_block;
     if (router)
-        scatter_kernel<true><<<grid, kThreads, (size_t)p.E * p.d * 2, s>>>(p, rows_per_block);
+        scatter_kernel<true><<<grid, kThreads, (size_t)p.E * p.d * 2 + (size_t)rows_per_block * p.E * 4, s>>>(
+            p, rows_per_block);
     else
         scatter_kernel<false><<<grid, kThreads, 0, s>>>(p, rows_per_block);
     return hipGetLastError();
