@@ -39,32 +39,37 @@ namespace tmt {
 namespace {
 
 constexpr int BM = 256;
-constexpr int WTM = 128;                  // wave tile rows (2 x 2 waves)
-constexpr int MI = WTM / 32;
 
 // Tile geometry. BK_ is the K depth of one LDS stage (32 or 64), NST the
-// number of stages in the ring, BN_ the tile width (256: one workgroup per
-// CU, 128 x 128 wave tiles; 128: two workgroups per CU, 128 x 64 wave tiles,
-// so one workgroup's waits and epilogue overlap the other's MFMAs).
-template <int BK_, int NST, int BN_>
+// number of stages in the ring, BN_ the tile width and NWM_ the waves along
+// M (2 x NWM_ waves per workgroup):
+//   BN 256, NWM 2: one 4-wave workgroup per CU, 128 x 128 wave tiles;
+//   BN 256, NWM 4: one 8-wave workgroup per CU, 64 x 128 wave tiles (two
+//                  waves per SIMD on the same operand tiles);
+//   BN 128, NWM 2: two 4-wave workgroups per CU, 128 x 64 wave tiles, so one
+//                  workgroup's waits and epilogue overlap the other's MFMAs.
+template <int BK_, int NST, int BN_, int NWM_ = 2>
 struct Geo {
     static constexpr int BK = BK_;
     static constexpr int NSTAGE = NST;
     static constexpr int BN = BN_;
+    static constexpr int NWM = NWM_, NW = 2 * NWM_, NT = 64 * NW;  // waves, threads
+    static constexpr int WTM = BM / NWM, MI = WTM / 32;  // wave tile rows
     static constexpr int WTN = BN / 2, NJ = WTN / 32;  // wave tile columns
+    static constexpr int EPR = NWM == 2 ? 64 : 32;     // epilogue rows per wave and pass
     static constexpr int KCH = BK / 8;                 // 16-byte chunks per K-contiguous row
     static constexpr int OPND_A = BM * BK;             // bf16 elements of the A tile
     static constexpr int OPND_B = BN * BK;             // bf16 elements of the B tile
     static constexpr int STAGE = OPND_A + OPND_B;      // A then B
-    static constexpr int DMA_A = OPND_A * 2 / 1024 / 4;  // 1 KiB wave loads per wave, A tile
-    static constexpr int DMA_B = OPND_B * 2 / 1024 / 4;  // ... B tile
+    static constexpr int DMA_A = OPND_A * 2 / 1024 / NW;  // 1 KiB wave loads per wave, A tile
+    static constexpr int DMA_B = OPND_B * 2 / 1024 / NW;  // ... B tile
     static constexpr int DMA_PER_TILE = DMA_A + DMA_B;
     static constexpr int KC_ROWS = 1024 / (2 * BK);    // K-contiguous rows per wave load
     static constexpr int STEPS = BK / 16;              // MFMA k16 steps per stage
     static constexpr int WGS = BN == 256 ? 1 : 2;      // workgroups per CU
     // LDS of the ring, also the epilogue's fp32 staging ([64][WTN] per wave)
     static constexpr int RING = NST * STAGE * 2;
-    static constexpr int EPI = 4 * 64 * WTN * 4;
+    static constexpr int EPI = NW * EPR * WTN * 4;
     static constexpr int LDS = RING > EPI ? RING : EPI;
     static_assert(LDS * WGS <= 160 * 1024, "LDS ring too large");
     // K-contiguous rows: 16-byte chunk swizzle making 16 consecutive rows (the
@@ -120,24 +125,18 @@ template <> struct Traits<GEMM_DOWN_FP4> {
     static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = false, b_fp4 = true;
 };
 
-// e2m1 code (bit 3 = sign) times 2^(scale - 127) as bf16 bits. The e2m1
-// magnitudes {0, .5, 1, 1.5, 2, 3, 4, 6} have at most two significant bits,
-// so the bf16 value is exact while the scaled exponent stays in range.
-__device__ __forceinline__ uint32_t e2m1_bf16(uint32_t c, int dexp) {
-    const uint32_t m = c & 7u;
-    const uint64_t lut = (m & 4u) ? 0x40C0408040404000ull : 0x3FC03F803F000000ull;
-    uint32_t bits = (uint32_t)(lut >> ((m & 3u) * 16)) & 0xffffu;
-    bits = bits ? (uint32_t)((int)bits + (dexp << 7)) : 0u;
-    return bits | ((c & 8u) << 12);
-}
-// 8 codes (low nibble first) with one shared scale -> 8 bf16.
+// 8 e2m1 codes (low nibble first) sharing one e8m0 scale -> 8 bf16, with the
+// gfx950 scaled conversion (two codes per instruction). e2m1 values have at
+// most two significant bits, so every product with 2^(scale - 127) inside
+// bf16's exponent range is exact; the scale byte becomes the fp32 2^(s-127)
+// (s = 0 is the subnormal 2^-127).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint4 dequant8(uint32_t w, uint32_t scale) {
-    const int dexp = (int)scale - 127;
-    uint32_t o[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-        o[q] = e2m1_bf16((w >> (8 * q)) & 15u, dexp) | (e2m1_bf16((w >> (8 * q + 4)) & 15u, dexp) << 16);
-    return make_uint4(o[0], o[1], o[2], o[3]);
+    const float sc = __uint_as_float(scale == 0 ? 0x00400000u : (scale << 23));
+    return make_uint4(__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0)),
+                      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1)),
+                      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2)),
+                      __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3)));
 }
 
 // Streaming (non-temporal) 16-byte accesses for the epilogue: outputs are
@@ -173,16 +172,17 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
 }
 
-template <int KIND, bool DUAL, int BK_, int NST, int BN_>
-__global__ __launch_bounds__(kThreads, (BN_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
+template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2>
+__global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
     using Tr = Traits<KIND>;
-    using Gm = Geo<BK_, NST, BN_>;
+    using Gm = Geo<BK_, NST, BN_, NWM_>;
     constexpr int BK = Gm::BK, NSTAGE = Gm::NSTAGE, BN = Gm::BN, WTN = Gm::WTN, NJ = Gm::NJ;
+    constexpr int WTM = Gm::WTM, MI = Gm::MI, NT = Gm::NT, EPR = Gm::EPR;
     constexpr int OPND_A = Gm::OPND_A;
     constexpr int DMA_A = Gm::DMA_A, DMA_B = Gm::DMA_B;
     // MXFP4 B operand per stage: 256 rows x 16 bytes of codes (BK = 32 = one
     // scale block), then one 1 KiB copy of the 256 row scales per wave.
-    static_assert(!Tr::b_fp4 || (BK == 32 && BN == 256), "MXFP4 tiles: one scale block, 256 columns");
+    static_assert(!Tr::b_fp4 || (BK == 32 && BN == 256 && NWM_ == 2), "MXFP4 tiles: one scale block, 256 columns, 4 waves");
     constexpr int FP4_CODES = 256 * 16, FP4_SCALES = 4 * 1024;
     constexpr int STAGE = Tr::b_fp4 ? OPND_A + (FP4_CODES + FP4_SCALES) / 2 : Gm::STAGE;  // bf16 elements
     constexpr int DMA_PER_TILE = Tr::b_fp4 ? DMA_A + 2 : Gm::DMA_PER_TILE;
@@ -347,7 +347,7 @@ __global__ __launch_bounds__(kThreads, (BN_ == 256 ? 1 : 2)) void grouped_gemm_k
             if (kvalid < BK) {
                 uint16_t* st = lds + (t % NSTAGE) * STAGE;
                 const int na = (BK - kvalid) * (BM / 8), nb = (BK - kvalid) * (BN / 8);  // 16-byte vectors
-                for (int v = tid; v < na + nb; v += kThreads) {
+                for (int v = tid; v < na + nb; v += NT) {
                     if (v < na) *reinterpret_cast<uint4*>(st + kvalid * BM + v * 8) = make_uint4(0, 0, 0, 0);
                     else *reinterpret_cast<uint4*>(st + OPND_A + kvalid * BN + (v - na) * 8) = make_uint4(0, 0, 0, 0);
                 }
@@ -480,20 +480,21 @@ __global__ __launch_bounds__(kThreads, (BN_ == 256 ? 1 : 2)) void grouped_gemm_k
     __syncthreads();
 
     // ---- epilogue ---------------------------------------------------------
-    // acc[i][j][r] = C[m][n] with m = wm*128 + 32i + (lane&31) and
-    // n = wn*WTN + 32j + 8(r>>2) + 4(lane>>5) + (r&3). Two passes of 64 rows per
-    // wave go through an fp32 LDS region ([64][WTN], 16-byte chunks swizzled by
-    // row), then leave as row-contiguous 16-byte stores.
+    // acc[i][j][r] = C[m][n] with m = wm*WTM + 32i + (lane&31) and
+    // n = wn*WTN + 32j + 8(r>>2) + 4(lane>>5) + (r&3). Passes of EPR rows per
+    // wave go through an fp32 LDS region ([EPR][WTN], 16-byte chunks swizzled
+    // by row), then leave as row-contiguous 16-byte stores.
     constexpr int CH = WTN / 4;              // 16-byte fp32 chunks per staged row
     constexpr int LPR = WTN / 8, RPI = 64 / LPR;     // bf16 out: lanes per row, rows per instruction
     constexpr int FLPR = WTN / 4, FRPI = 64 / FLPR;  // fp32 out
-    float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (64 * WTN);
+    constexpr int FPP = EPR / 32, PASSES = MI / FPP;  // row fragments per pass, passes
+    float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (EPR * WTN);
     const int mbase = wm * WTM, nbase = wn * WTN;
 #pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
+    for (int pass = 0; pass < PASSES; ++pass) {
 #pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-            const int i = pass * 2 + ii;
+        for (int ii = 0; ii < FPP; ++ii) {
+            const int i = pass * FPP + ii;
             const int lr = ii * 32 + (lane & 31);
 #pragma unroll
             for (int j = 0; j < NJ; ++j)
@@ -511,20 +512,20 @@ __global__ __launch_bounds__(kThreads, (BN_ == 256 ? 1 : 2)) void grouped_gemm_k
             uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
             const int cl = lane % LPR;
             const int n = nbase + cl * 8;
-            uint4 uin[64 / RPI];  // GEMM_DACT: pre-activations, all loads issued first
+            uint4 uin[EPR / RPI];  // GEMM_DACT: pre-activations, all loads issued first
             if constexpr (KIND == GEMM_DACT) {
 #pragma unroll
-                for (int k = 0; k < 64 / RPI; ++k) {
-                    const int m = mbase + pass * 64 + lane / LPR + RPI * k;
+                for (int k = 0; k < EPR / RPI; ++k) {
+                    const int m = mbase + pass * EPR + lane / LPR + RPI * k;
                     const bool ok = m < mlim && n < nlim;
                     const int64_t off = (int64_t)(row0 + (ok ? m : 0)) * p.ldc + nt * BN + (ok ? n : 0);
                     uin[k] = ld16_nt(p.u + off);
                 }
             }
 #pragma unroll
-            for (int k = 0; k < 64 / RPI; ++k) {
+            for (int k = 0; k < EPR / RPI; ++k) {
                 const int rr = lane / LPR + RPI * k;
-                const int m = mbase + pass * 64 + rr;
+                const int m = mbase + pass * EPR + rr;
                 if (m >= mlim || n >= nlim) continue;
                 const float* src = stage_f + rr * WTN;
                 const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + (((2 * cl) ^ (rr & (CH - 1))) * 4));
@@ -549,8 +550,8 @@ __global__ __launch_bounds__(kThreads, (BN_ == 256 ? 1 : 2)) void grouped_gemm_k
             float* C = p.dw[e];
             const int cl = lane % FLPR;
 #pragma unroll 4
-            for (int rr = lane / FLPR; rr < 64; rr += FRPI) {
-                const int m = mbase + pass * 64 + rr;
+            for (int rr = lane / FLPR; rr < EPR; rr += FRPI) {
+                const int m = mbase + pass * EPR + rr;
                 const int n = nbase + cl * 4;
                 if (m >= mlim || n >= nlim) continue;
                 const f32x4 v = *reinterpret_cast<const f32x4*>(stage_f + rr * WTN + ((cl ^ (rr & (CH - 1))) * 4));
@@ -565,10 +566,10 @@ __global__ __launch_bounds__(kThreads, (BN_ == 256 ? 1 : 2)) void grouped_gemm_k
 
 constexpr int kBK = 32, kNST = 4;  // fastest of BK 32/64 x 2-4 stages on the c3 shapes
 
-template <int KIND, bool DUAL, int BN>
+template <int KIND, bool DUAL, int BN, int NWM = 2>
 hipError_t launch_kind(const GemmParams& p, unsigned grid, hipStream_t s) {
     constexpr int NST = BN == 256 ? kNST : 3;  // two workgroups per CU at BN 128: 3 x 24 KiB stages
-    grouped_gemm_kernel<KIND, DUAL, kBK, NST, BN><<<grid, kThreads, 0, s>>>(p);
+    grouped_gemm_kernel<KIND, DUAL, kBK, NST, BN, NWM><<<grid, 128 * NWM, 0, s>>>(p);
     return hipGetLastError();
 }
 
