@@ -45,8 +45,9 @@ def kernel_work(phase, T, d, E, K, h):
         "scan": ("hbm", 0),
         # expert outputs gathered, residual read + written, gates and slots
         "combine": ("hbm", 2 * TK * d + 4 * T * d + 8 * TK),
-        # dY, outputs read, dO written, probs/logit statistics, dlogits
-        "combine_bwd": ("hbm", 2 * T * d + 4 * TK * d + 8 * TK + 8 * T * E),
+        # dY, X, expert outputs read; dO and X gathered to slot order written;
+        # probs read, dlogits written; idx, gate, slot table; lse
+        "combine_bwd": ("hbm", 4 * T * d + 6 * TK * d + 8 * T * E + 12 * TK + 4 * T),
         "router_dw": ("hbm", 2 * T * d + 4 * T * E + 4 * E * d),
         "scatter": ("hbm", 2 * TK * d + 2 * T * d + 4 * T * E + 4 * TK),
     }
@@ -74,8 +75,12 @@ def cpu_baseline(case, cfg, target_s=15.0, max_threads=16):
                             z_coef=cfg.get("z", 0.0), threads=threads)
         return time.perf_counter() - t0
 
-    t_small = run(64)
-    ts = int(max(64, min(8192, 64 * target_s / max(t_small, 1e-3))))
+    # Two probes separate the per-call fixed cost (weight conversion, dW
+    # buffers) from the per-token cost; the sample is then sized for target_s.
+    t0 = run(64)
+    t1 = run(512)
+    per_tok = max((t1 - t0) / 448.0, 1e-6)
+    ts = int(max(512, min(16384, 64 + (target_s - t0) / per_tok)))
     ts -= ts % 64
     dt = run(ts)
     return {"value": round(ts / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
