@@ -62,6 +62,7 @@ struct tmt_moe {
     size_t arena_bytes = 0;
     // routing state (kept from forward for backward; the reference's MoeKeep)
     float *logits, *probs, *lse, *gate, *blkstat, *stats;
+    int32_t* ticket = nullptr;  // decode router's completion counter (zero between calls)
     int32_t *idx, *blkcnt, *blkbase, *counts, *offsets, *order, *perm, *slot_of;
     // activations
     uint16_t *U, *Aact, *O, *dO, *dU, *dXg, *Xg;
@@ -126,6 +127,7 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
     size_t o_blkstat = L.add(nblk * (E + 1) * 4);
     size_t o_counts = L.add(E * 4), o_offsets = L.add((E + 1) * 4), o_order = L.add(E * 4);
     size_t o_stats = L.add((2 + E) * 4);
+    size_t o_ticket = L.add(4);
     size_t o_perm = L.add(TK * 4), o_slot = L.add(TK * 4);
     size_t o_U = L.add(TK * hn * 2);
     size_t o_A = h > 0 ? L.add(TK * h * 2) : 0;
@@ -152,6 +154,7 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->offsets = (int32_t*)(a + o_offsets);
         m->order = (int32_t*)(a + o_order);
         m->stats = (float*)(a + o_stats);
+        m->ticket = (int32_t*)(a + o_ticket);
         m->perm = (int32_t*)(a + o_perm);
         m->slot_of = (int32_t*)(a + o_slot);
         m->U = (uint16_t*)(a + o_U);
@@ -241,7 +244,7 @@ int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* W
         PermuteParams pp{};
         pp.T = T; pp.E = E; pp.K = K; pp.rows_per_block = T;
         pp.perm = m->perm; pp.slot_of = m->slot_of;
-        LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(rp, sp, pp, s));
+        LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(rp, sp, pp, m->ticket, s));
         return TMT_MOE_OK;
     }
     const int rpb = router_rows_per_block(T, E, K);
@@ -314,6 +317,15 @@ int tmt_moe_create(const tmt_moe_desc* desc, tmt_moe** out) {
         return fail(TMT_MOE_ENOMEM, "hipMalloc(%zu) failed: %s", m->arena_bytes, hipGetErrorString(err));
     }
     plan(desc, m);
+    // The decode router's ticket starts at zero (each call leaves it at zero).
+    err = hipMemset(m->ticket, 0, sizeof(int32_t));
+    if (err == hipSuccess) err = hipStreamSynchronize(nullptr);
+    if (err != hipSuccess) {
+        (void)hipFree(m->arena);
+        delete m;
+        (void)hipGetLastError();
+        return fail(TMT_MOE_EDEVICE, "initialising the workspace failed: %s", hipGetErrorString(err));
+    }
     *out = m;
     return TMT_MOE_OK;
 }

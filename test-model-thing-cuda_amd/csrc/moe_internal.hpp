@@ -57,11 +57,13 @@ struct PermuteParams {
 };
 hipError_t launch_permute(const PermuteParams& p, int nblk, hipStream_t s);
 
-// T <= kSmallRouteTokens: router + scan + permute fused into one workgroup
-// (uses sp.counts/offsets/order/stats and pp.perm/slot_of; no block tables).
+// T <= kSmallRouteTokens: router + scan + permute in one launch, one block
+// per token row; the last block to finish (atomic *ticket, zero between
+// calls and re-armed by that block) completes the dispatch. Uses
+// sp.counts/offsets/order/stats and pp.perm/slot_of; no block tables.
 constexpr int kSmallRouteTokens = 64;
 hipError_t launch_route_small(const RouterParams& p, const ScanParams& sp, const PermuteParams& pp,
-                              hipStream_t s);
+                              int* ticket, hipStream_t s);
 
 // E == 1: identity dispatch, gates of 1, offsets {0, T}.
 hipError_t launch_dense_dispatch(int T, int32_t* perm, int32_t* slot_of,

@@ -116,6 +116,50 @@ __device__ __forceinline__ void argmax_step(float& bv, float& bp, int& be, bool&
     if (take) { bv = ov; bp = op; be = oe; has = true; }
 }
 
+// Softmax and top-k of one row held by EP lanes (lane e_mine = expert):
+// softmax over the row (moe.cu:41-49); K rounds of a butterfly arg-max over
+// (logit desc, expert asc), i.e. strict '>' with ties to the lower index
+// (moe.cu:52-63); renormalised gate of pick j on lane j (moe.cu:64-66).
+struct RowPick {
+    float prob, lse, gate;
+    int idx;
+    bool sel;
+};
+template <int EP>
+__device__ __forceinline__ RowPick softmax_topk(float logit, bool e_valid, int e_mine, int K) {
+    RowPick o;
+    const float lv = e_valid ? logit : -INFINITY;
+    const float mx = group_max<EP>(lv);
+    const float ex = e_valid ? __expf(lv - mx) : 0.0f;
+    const float se = group_sum<EP>(ex);
+    o.prob = ex / se;
+    o.lse = mx + __logf(se);
+    bool sel = false;
+    int out_e = 0;
+    float out_p = 0.0f, zsum = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j) {
+        if (j < K) {
+            bool has = e_valid && !sel;
+            float bv = logit, bp = o.prob;
+            int be = e_mine;
+            if constexpr (EP >= 64) argmax_step<32>(bv, bp, be, has);
+            if constexpr (EP >= 32) argmax_step<16>(bv, bp, be, has);
+            if constexpr (EP >= 16) argmax_step<8>(bv, bp, be, has);
+            argmax_step<4>(bv, bp, be, has);
+            argmax_step<2>(bv, bp, be, has);
+            argmax_step<1>(bv, bp, be, has);
+            if (e_mine == be) sel = true;
+            if (e_mine == j) { out_e = be; out_p = bp; }
+            zsum += bp;
+        }
+    }
+    o.sel = sel;
+    o.idx = out_e;
+    o.gate = out_p / zsum;
+    return o;
+}
+
 template <int EP, int NW>
 __device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t* wl, int row_begin,
                                            int row_end, int* s_cnt,
@@ -174,35 +218,9 @@ __device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t
         const int row = r0 + r_mine;
         const bool row_valid = row < row_end;
 
-        // Softmax over the EP lanes of this row (moe.cu:41-49).
-        const float lv = e_valid ? logit : -INFINITY;
-        const float mx = group_max<EP>(lv);
-        const float ex = e_valid ? __expf(lv - mx) : 0.0f;
-        const float se = group_sum<EP>(ex);
-        const float prob = ex / se;
-        const float lse = mx + __logf(se);
-
-        // Top-k: K rounds of a butterfly argmax over (logit desc, expert asc).
-        bool sel = false;
-        int out_e = 0;
-        float out_p = 0.0f, zsum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kMaxTopK; ++j) {
-            if (j < K) {
-                bool has = e_valid && !sel;
-                float bv = logit, bp = prob;
-                int be = e_mine;
-                if constexpr (EP >= 64) argmax_step<32>(bv, bp, be, has);
-                if constexpr (EP >= 32) argmax_step<16>(bv, bp, be, has);
-                if constexpr (EP >= 16) argmax_step<8>(bv, bp, be, has);
-                argmax_step<4>(bv, bp, be, has);
-                argmax_step<2>(bv, bp, be, has);
-                argmax_step<1>(bv, bp, be, has);
-                if (e_mine == be) sel = true;
-                if (e_mine == j) { out_e = be; out_p = bp; }
-                zsum += bp;
-            }
-        }
+        const RowPick pk = softmax_topk<EP>(logit, e_valid, e_mine, K);
+        const float prob = pk.prob, lse = pk.lse;
+        const bool sel = pk.sel;
 
         if (row_valid) {
             if (e_valid) {
@@ -211,9 +229,9 @@ __device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t
                 psum += prob;
             }
             if (e_mine < K) {
-                p.idx[(int64_t)row * K + e_mine] = out_e;
-                p.gate[(int64_t)row * K + e_mine] = out_p / zsum;
-                if (s_idx) s_idx[(row - row_begin) * K + e_mine] = out_e;
+                p.idx[(int64_t)row * K + e_mine] = pk.idx;
+                p.gate[(int64_t)row * K + e_mine] = pk.gate;
+                if (s_idx) s_idx[(row - row_begin) * K + e_mine] = pk.idx;
             }
             if (e_mine == 0) {
                 p.lse[row] = lse;
@@ -440,32 +458,128 @@ hipError_t launch_permute(const PermuteParams& p, int nblk, hipStream_t s) {
 }
 
 // T <= kSmallRouteTokens (decode): router, counts, offsets, statistics,
-// expert order and the stable permutation in one workgroup, one launch
-// instead of router + scan + permute. The statistics use the same fixed
-// summation order as router_kernel's block statistics followed by
-// scan_kernel's formulas.
+// expert order and the stable permutation in one launch instead of router +
+// scan + permute. One 4-wave block per token row:
+//  1. the row's E logits: wave w computes experts w, w + 4, ..., each as the
+//     canonical lane partials and the full xor butterfly (32 .. 1), which adds
+//     the same partial trees as router_kernel's reduce-scatter (bit-identical);
+//  2. softmax / top-k / gates of the row on EP lanes (router_kernel's code);
+//  3. the last block to finish (an atomic ticket, device-scope fences on both
+//     sides) reads every row's picks back and computes counts, offsets, aux /
+//     z, the expert order and the stable permutation, then re-arms the ticket.
 constexpr int kSmallGroups = 8;  // ceil(T / floor(64 / K)) for T <= 64, K <= 8
-
-constexpr int kSmallWaves = 16;
+constexpr int kPairBatch = 4;    // expert dot products per wave with loads in flight
 
 template <int EP>
-__global__ __launch_bounds__(64 * kSmallWaves) void route_small_kernel(RouterParams p, ScanParams sp,
-                                                                       PermuteParams pp) {
-    extern __shared__ uint4 smem_w[];  // Wr [E][d] bf16
+__global__ __launch_bounds__(kThreads) void route_small_kernel(RouterParams p, ScanParams sp,
+                                                               PermuteParams pp, int* ticket) {
+    __shared__ float s_logit[kMaxExperts];
+    __shared__ float s_sum[kMaxExperts + 1];
     __shared__ int s_cnt[kMaxExperts];
-    __shared__ float s_stat[kSmallWaves][kMaxExperts + 1];
     __shared__ int s_idx[kSmallRouteTokens * kMaxTopK];
+    __shared__ float s_prob[kSmallRouteTokens * kMaxExperts];
+    __shared__ float s_lse[kSmallRouteTokens];
     __shared__ int s_off[kMaxExperts + 1];
     __shared__ int s_g[kSmallGroups][kMaxExperts];
+    __shared__ int s_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int E = p.E, K = p.K, T = p.T;
-    stage_router_weights(p.Wr, E * p.d / 8, smem_w);
-    if (tid < kMaxExperts) s_cnt[tid] = 0;
-    __syncthreads();
-    route_rows<EP, kSmallWaves>(p, reinterpret_cast<const uint16_t*>(smem_w), 0, T, s_cnt, s_stat, s_idx);
+    const int E = p.E, K = p.K, T = p.T, d = p.d;
+    const int row = blockIdx.x;
+    const int nch = (d + 511) / 512;  // 1 or 2 chunks of 512 (d <= 1024 for E = 32; any d works)
+
+    // 1. logits of this row
+    for (int e0 = wave; e0 < E; e0 += 4 * kPairBatch) {
+        float acc[kPairBatch];
+#pragma unroll
+        for (int u = 0; u < kPairBatch; ++u) acc[u] = 0.0f;
+        for (int c = 0; c < nch; ++c) {
+            const int k0 = c * 512 + lane * 8;
+            if (k0 >= d) continue;
+            uint4 wv[kPairBatch];
+#pragma unroll
+            for (int u = 0; u < kPairBatch; ++u) {
+                const int e = min(e0 + 4 * u, E - 1);  // clamped: extra pairs are discarded
+                wv[u] = *reinterpret_cast<const uint4*>(p.Wr + (int64_t)e * d + k0);
+            }
+            float xf[8];
+            unpack8(*reinterpret_cast<const uint4*>(p.X + (int64_t)row * d + k0), xf);
+#pragma unroll
+            for (int u = 0; u < kPairBatch; ++u) {
+                float wf[8];
+                unpack8(wv[u], wf);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[u] = __builtin_fmaf(xf[t], wf[t], acc[u]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kPairBatch; ++u) {
+            float v = acc[u];
+            v += xor_lane<32>(v);
+            v += xor_lane<16>(v);
+            v += xor_lane<8>(v);
+            v += xor_lane<4>(v);
+            v += xor_lane<2>(v);
+            v += xor_lane<1>(v);
+            const int e = e0 + 4 * u;
+            if (lane == 0 && e < E) s_logit[e] = p.bias != nullptr ? v + p.bias[e] : v;
+        }
+    }
     __syncthreads();
 
+    // 2. softmax, top-k, gates on EP lanes of wave 0
+    if (wave == 0) {
+        const int e = lane % EP;
+        const bool ev = lane < EP && e < E;
+        const float logit = ev ? s_logit[e] : 0.0f;
+        const RowPick pk = softmax_topk<EP>(logit, ev, e, K);
+        if (lane < EP) {
+            if (ev) {
+                p.logits[(int64_t)row * E + e] = logit;
+                p.probs[(int64_t)row * E + e] = pk.prob;
+                s_prob[e] = pk.prob;  // used directly when this is the only block
+            }
+            if (e < K) {
+                p.idx[(int64_t)row * K + e] = pk.idx;
+                p.gate[(int64_t)row * K + e] = pk.gate;
+                s_idx[e] = pk.idx;
+            }
+            if (e == 0) {
+                p.lse[row] = pk.lse;
+                s_lse[0] = pk.lse;
+            }
+        }
+    }
+
+    // 3. the last block finishes the dispatch (a single block already holds
+    // everything in LDS; otherwise every row is read back in one batch)
+    if (gridDim.x > 1) {
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) s_last = atomicAdd(ticket, 1) == T - 1;
+        __syncthreads();
+        if (!s_last) return;
+        __threadfence();
+        const int ni = T * K, np = T * E;
+        for (int i = tid; i < ni + np + T; i += kThreads) {
+            if (i < ni) s_idx[i] = p.idx[i];
+            else if (i < ni + np) s_prob[i - ni] = p.probs[i - ni];
+            else s_lse[i - ni - np] = p.lse[i - ni - np];
+        }
+    }
+    if (tid < kMaxExperts) s_cnt[tid] = 0;
+    __syncthreads();
+    for (int i = tid; i < T * K; i += kThreads) atomicAdd(&s_cnt[s_idx[i]], 1);
+    if (tid < E) {
+        float sum = 0.0f;
+        for (int r = 0; r < T; ++r) sum += s_prob[r * E + tid];
+        s_sum[tid] = sum;
+    } else if (tid == E) {
+        float l2 = 0.0f;
+        for (int r = 0; r < T; ++r) l2 += s_lse[r] * s_lse[r];
+        s_sum[E] = l2;
+    }
+    __syncthreads();
     if (tid == 0) {
         int run = 0;
         for (int e = 0; e < E; ++e) {
@@ -477,15 +591,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) void route_small_kernel(RouterPar
         const float inv_t = 1.0f / (float)T;
         const float inv_tk = 1.0f / ((float)T * (float)K);
         float aux = 0.0f;
-        for (int e = 0; e < E; ++e) {
-            float sp_e = s_stat[0][e];
-            for (int w = 1; w < kSmallWaves; ++w) sp_e += s_stat[w][e];
-            aux += (sp_e * inv_t) * ((float)s_cnt[e] * inv_tk);
-        }
-        float l2 = s_stat[0][kMaxExperts];
-        for (int w = 1; w < kSmallWaves; ++w) l2 += s_stat[w][kMaxExperts];
+        for (int e = 0; e < E; ++e) aux += (s_sum[e] * inv_t) * ((float)s_cnt[e] * inv_tk);
         sp.stats[0] = aux * (float)E;
-        sp.stats[1] = l2 * inv_t;
+        sp.stats[1] = s_sum[E] * inv_t;
+        if (gridDim.x > 1) *ticket = 0;  // re-armed for the next call (stream order keeps calls apart)
     }
     __syncthreads();
     if (tid <= E) sp.offsets[tid] = s_off[tid];
@@ -503,10 +612,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) void route_small_kernel(RouterPar
     const int G = (T + RG - 1) / RG;
     const int rr = lane / K, j = lane % K;
     const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int g = wave; g < G; g += kSmallWaves) {
-        const int row = g * RG + rr;
-        const bool valid = lane < pairs && row < T;
-        const int e = valid ? s_idx[row * K + j] : -1;
+    for (int g = wave; g < G; g += 4) {
+        const int r = g * RG + rr;
+        const bool valid = lane < pairs && r < T;
+        const int e = valid ? s_idx[r * K + j] : -1;
         for (int ee = 0; ee < E; ++ee) {
             const uint64_t m = __ballot(e == ee);
             if (lane == ee) s_g[g][ee] = __popcll(m);
@@ -522,10 +631,10 @@ __global__ __launch_bounds__(64 * kSmallWaves) void route_small_kernel(RouterPar
         }
     }
     __syncthreads();
-    for (int g = wave; g < G; g += kSmallWaves) {
-        const int row = g * RG + rr;
-        const bool valid = lane < pairs && row < T;
-        const int e = valid ? s_idx[row * K + j] : -1;
+    for (int g = wave; g < G; g += 4) {
+        const int r = g * RG + rr;
+        const bool valid = lane < pairs && r < T;
+        const int e = valid ? s_idx[r * K + j] : -1;
         int rank = 0;
         for (int ee = 0; ee < E; ++ee) {
             const uint64_t m = __ballot(e == ee);
@@ -533,26 +642,22 @@ __global__ __launch_bounds__(64 * kSmallWaves) void route_small_kernel(RouterPar
         }
         if (valid) {
             const int pos = s_g[g][e] + rank;
-            pp.perm[pos] = row;
-            pp.slot_of[(int64_t)row * K + j] = pos;
+            pp.perm[pos] = r;
+            pp.slot_of[(int64_t)r * K + j] = pos;
         }
     }
 }
 
 hipError_t launch_route_small(const RouterParams& p, const ScanParams& sp, const PermuteParams& pp,
-                              hipStream_t s) {
+                              int* ticket, hipStream_t s) {
     if (p.T < 1 || p.T > kSmallRouteTokens || p.K > kMaxTopK) return hipErrorInvalidValue;
     if ((p.T + 64 / p.K - 1) / (64 / p.K) > kSmallGroups) return hipErrorInvalidValue;
-    const size_t lds = (size_t)p.E * p.d * 2;
-    dim3 grid(1), block(64 * kSmallWaves);
-    // At least 32 expert lanes (at most 2 rows per wave) keeps the 16-wave
-    // kernel within 128 VGPRs. Lanes past E add exact zeros / -inf to the
-    // softmax butterflies, so the results equal the narrower layout's.
+    dim3 grid(p.T), block(kThreads);
     switch (router_ep(p.E)) {
-        case 8:
-        case 16:
-        case 32: route_small_kernel<32><<<grid, block, lds, s>>>(p, sp, pp); break;
-        case 64: route_small_kernel<64><<<grid, block, lds, s>>>(p, sp, pp); break;
+        case 8: route_small_kernel<8><<<grid, block, 0, s>>>(p, sp, pp, ticket); break;
+        case 16: route_small_kernel<16><<<grid, block, 0, s>>>(p, sp, pp, ticket); break;
+        case 32: route_small_kernel<32><<<grid, block, 0, s>>>(p, sp, pp, ticket); break;
+        case 64: route_small_kernel<64><<<grid, block, 0, s>>>(p, sp, pp, ticket); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -190,9 +190,10 @@ def test_dead_experts_get_zero_gradients(orc):
     check_grads(g, r, h, E)
 
 
-def test_router_ties_go_to_lower_index(orc):
-    say("router ties: experts 2 and 4 have identical rows")
-    T, d, E, K, h = 256, 256, 6, 2, 128
+@pytest.mark.parametrize("T", [256, 8])  # tiled router and the single-workgroup decode router
+def test_router_ties_go_to_lower_index(orc, T):
+    say(f"router ties (T={T}): experts 2 and 4 have identical rows")
+    d, E, K, h = 256, 6, 2, 128
     case = make_case(T, d, E, K, h, seed=6)
     case["Wr"][2] = case["Wr"][4]
     case["bias"] = np.array([-30, -30, 20, -30, 20, -30], np.float32)
