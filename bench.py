@@ -157,6 +157,39 @@ def measured_traffic(phase):
     return None
 
 
+def bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream, reps=100):
+    """c4: decode steps (forward, beta = 1) at T = 1, 8, 64 on the c3 weights;
+    µs per step from HIP events around `reps` back-to-back steps."""
+    import numpy as np
+    import torch
+
+    import tmt_moe
+
+    out = {}
+    md = tmt_moe.MoE(64, d, E, K, h)
+    for td in (1, 8, 64):
+        Xd = X[:td].contiguous()
+        Yd = torch.zeros(td, d, dtype=torch.bfloat16, device="cuda")
+        for _ in range(10):
+            md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) / reps * 1000
+        routed = md.routing()
+        distinct = int(np.unique(routed["idx"]).size)
+        wbytes = distinct * 2 * d * h * 2 + E * d * 2
+        out[f"T{td}"] = {"us_per_step": round(us, 2), "distinct_experts": distinct,
+                         "weight_bytes": wbytes,
+                         "hbm_gbs": round(wbytes / (us * 1e-6) / 1e9, 1)}
+    md.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -170,6 +203,8 @@ def main():
                     help="time the step without per-kernel events")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a device copy of known size (HBM counter calibration)")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the c4 decode measurement (T = 1, 8, 64 on the c3 weights)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -201,6 +236,9 @@ def main():
     dWu = torch.empty(E, hn, d, dtype=torch.float32, device="cuda")
     dWd = torch.empty(E, d, h, dtype=torch.float32, device="cuda") if h > 0 else None
     aux_c, z_c = cfg.get("aux", 0.0), cfg.get("z", 0.0)
+    if args.decode_only:
+        print(json.dumps({"decode": bench_decode(X, Wr, Wu, Wd, d, E, K, h, torch.cuda.current_stream())}))
+        return
     m = tmt_moe.MoE(T, d, E, K, h)
 
     def step():
@@ -264,29 +302,7 @@ def main():
 
     decode = None
     if not args.no_decode and args.config == "c3":
-        decode = {}
-        md = tmt_moe.MoE(64, d, E, K, h)
-        for td in (1, 8, 64):
-            Xd = X[:td].contiguous()
-            Yd = torch.zeros(td, d, dtype=torch.bfloat16, device="cuda")
-            for _ in range(10):
-                md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            reps = 100
-            e0.record(stream)
-            for _ in range(reps):
-                md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
-            e1.record(stream)
-            torch.cuda.synchronize()
-            us = e0.elapsed_time(e1) / reps * 1000
-            routed = md.routing()
-            distinct = int(np.unique(routed["idx"]).size)
-            wbytes = distinct * 2 * d * h * 2 + E * d * 2
-            decode[f"T{td}"] = {"us_per_step": round(us, 2), "distinct_experts": distinct,
-                                "weight_bytes": wbytes,
-                                "hbm_gbs": round(wbytes / (us * 1e-6) / 1e9, 1)}
-        md.close()
+        decode = bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream)
 
     fp4 = None
     if not args.no_fp4 and args.config == "c3":
