@@ -142,6 +142,39 @@ float canonical_logit(const uint16_t* x, const uint16_t* w, int d) {
     return lane[0];
 }
 
+// LayerNorm row statistics in the canonical order shared with the GPU kernel
+// (the lane layout of canonical_logit): element k goes to lane (k/8) mod 64;
+// each lane adds its elements (sum) and accumulates x*x with fmaf (sum of
+// squares) in ascending k from +0; an xor butterfly 32..1 combines the lanes.
+// mean = sum/D, var = sumsq/D - mean*mean, rstd = 1/sqrt(var + 1e-5), each
+// operation rounded on its own (tmt-cuda/src/norm.cu:13-44, whose block-tree
+// order and rsqrtf are replaced by this order and IEEE sqrt / division).
+void ln_row_stats(const uint16_t* x, int d, float* mean, float* rstd) {
+    float ls[64], lq[64];
+    for (int i = 0; i < 64; ++i) ls[i] = lq[i] = 0.0f;
+    for (int k = 0; k < d; ++k) {
+        const int L = (k >> 3) & 63;
+        const float v = bf(x[k]);
+        ls[L] = ls[L] + v;
+        lq[L] = std::fma(v, v, lq[L]);
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        float ns[64], nq[64];
+        for (int i = 0; i < 64; ++i) {
+            ns[i] = ls[i] + ls[i ^ off];
+            nq[i] = lq[i] + lq[i ^ off];
+        }
+        std::memcpy(ls, ns, sizeof(ls));
+        std::memcpy(lq, nq, sizeof(lq));
+    }
+    const float m = ls[0] / (float)d;
+    const float qd = lq[0] / (float)d;
+    const float m2 = m * m;
+    const float var = qd - m2;
+    *mean = m;
+    *rstd = 1.0f / std::sqrt(var + 1e-5f);
+}
+
 void router_rows(const orc_dims* dm, const uint16_t* X, const uint16_t* Wr,
                  const float* bias, float* logits, float* probs, int32_t* idx,
                  float* w, float* lse) {
@@ -708,6 +741,56 @@ uint8_t e2m1_encode(float v) {
     return (uint8_t)(sign | best);
 }
 }  // namespace
+
+// LayerNorm forward (tmt-cuda/src/norm.cu:8-51): H = bf16(((x - mean) * rstd)
+// * gamma + beta), each operation rounded on its own; statistics in the
+// canonical order of ln_row_stats.
+int orc_layernorm_fwd(int32_t T, int32_t d, const uint16_t* S, const float* gamma,
+                      const float* beta, uint16_t* H, float* mean, float* rstd) {
+    if (T < 0 || d <= 0 || !S || !gamma || !beta || !H || !mean || !rstd) return -1;
+    for (int64_t r = 0; r < T; ++r) {
+        const uint16_t* x = S + r * d;
+        float m, rs;
+        ln_row_stats(x, d, &m, &rs);
+        mean[r] = m;
+        rstd[r] = rs;
+        for (int k = 0; k < d; ++k) {
+            const float xm = bf(x[k]) - m;
+            const float xh = xm * rs;
+            const float t = xh * gamma[k];
+            H[r * d + k] = tobf(t + beta[k]);
+        }
+    }
+    return 0;
+}
+
+// LayerNorm backward (tmt-cuda/src/norm.cu:53-106) from the fp32 gradient dH
+// of its output: with g = dH * gamma and xh = (x - mean) * rstd,
+// dS = rstd * ((g - mean(g)) - xh * mean(g * xh)); dgamma = sum_r dH * xh,
+// dbeta = sum_r dH (overwritten; ascending rows).
+int orc_layernorm_bwd(int32_t T, int32_t d, const uint16_t* S, const float* dH,
+                      const float* gamma, const float* mean, const float* rstd,
+                      float* dS, float* dgamma, float* dbeta) {
+    if (T < 0 || d <= 0 || !S || !dH || !gamma || !mean || !rstd || !dS || !dgamma || !dbeta) return -1;
+    for (int k = 0; k < d; ++k) dgamma[k] = dbeta[k] = 0.0f;
+    std::vector<float> xh(d), g(d);
+    for (int64_t r = 0; r < T; ++r) {
+        const uint16_t* x = S + r * d;
+        const float* dy = dH + r * d;
+        double s1 = 0.0, s2 = 0.0;
+        for (int k = 0; k < d; ++k) {
+            xh[k] = (bf(x[k]) - mean[r]) * rstd[r];
+            g[k] = dy[k] * gamma[k];
+            s1 += g[k];
+            s2 += (double)g[k] * xh[k];
+            dgamma[k] += dy[k] * xh[k];
+            dbeta[k] += dy[k];
+        }
+        const float a = (float)(s1 / d), b = (float)(s2 / d);
+        for (int k = 0; k < d; ++k) dS[r * d + k] = rstd[r] * ((g[k] - a) - xh[k] * b);
+    }
+    return 0;
+}
 
 int orc_mxfp4_quantize(const float* in, int64_t rows, int64_t n,
                        uint8_t* packed, uint8_t* scales) {

@@ -117,6 +117,16 @@ int orc_mxfp4_quantize(const float* in, int64_t rows, int64_t n,
 int orc_mxfp4_dequantize(const uint8_t* packed, const uint8_t* scales,
                          int64_t rows, int64_t n, float* out);
 
+/* LayerNorm that precedes the MoE in TMT (tmt-cuda/src/norm.cu:8-106).
+ * Forward: H [T][d] bf16, mean/rstd [T]; statistics in the canonical order
+ * documented at ln_row_stats() (the GPU kernel's order). Backward from the
+ * fp32 gradient dH: dS [T][d], dgamma/dbeta [d] (fp32, overwritten). */
+int orc_layernorm_fwd(int32_t T, int32_t d, const uint16_t* S, const float* gamma,
+                      const float* beta, uint16_t* H, float* mean, float* rstd);
+int orc_layernorm_bwd(int32_t T, int32_t d, const uint16_t* S, const float* dH,
+                      const float* gamma, const float* mean, const float* rstd,
+                      float* dS, float* dgamma, float* dbeta);
+
 #ifdef __cplusplus
 }
 #endif

@@ -194,3 +194,31 @@ def mxfp4_dequantize(packed, scales, n: int) -> np.ndarray:
     rc = load().orc_mxfp4_dequantize(_p(packed), _p(scales), ctypes.c_int64(rows), ctypes.c_int64(n), _p(out))
     assert rc == 0, rc
     return out.reshape(*packed.shape[:-1], n)
+
+
+def layernorm(S, gamma, beta):
+    """LayerNorm forward: H (bf16 bits), mean, rstd (canonical order)."""
+    S = _c(S, np.uint16)
+    T, d = S.shape
+    g, b = _c(gamma, np.float32), _c(beta, np.float32)
+    H = np.empty((T, d), np.uint16)
+    mean = np.empty(T, np.float32)
+    rstd = np.empty(T, np.float32)
+    rc = load().orc_layernorm_fwd(T, d, _p(S), _p(g), _p(b), _p(H), _p(mean), _p(rstd))
+    assert rc == 0, rc
+    return {"H": H, "mean": mean, "rstd": rstd}
+
+
+def layernorm_bwd(S, dH, gamma, mean, rstd):
+    """LayerNorm backward from the fp32 gradient dH of its output."""
+    S = _c(S, np.uint16)
+    T, d = S.shape
+    dH = _c(dH, np.float32)
+    dS = np.empty((T, d), np.float32)
+    dg = np.empty(d, np.float32)
+    db = np.empty(d, np.float32)
+    rc = load().orc_layernorm_bwd(T, d, _p(S), _p(dH), _p(_c(gamma, np.float32)), _p(_c(mean, np.float32)),
+                                  _p(_c(rstd, np.float32)), _p(dS), _p(dg), _p(db))
+    assert rc == 0, rc
+    return {"dS": dS, "dgamma": dg, "dbeta": db}
+
