@@ -123,6 +123,41 @@ int tmt_moe_backward(tmt_moe* moe, void* stream, const uint16_t* dY,
                      float* const* dW_up, float* const* dW_down);
 
 /*
+ * LayerNorm in front of the block, in one call: replaces the recurrent
+ * block's layernorm_fwd + moe_forward pair (model.cu:509-514; norm.cu:8-50,
+ * 96-100):
+ *   H = LayerNorm(S; ln_gamma, ln_beta)  (eps 1e-5, biased variance),
+ *   Y = beta*Y + MoE(H)                  (as tmt_moe_forward).
+ * S [T][d] bf16; ln_gamma, ln_beta [d] fp32 device pointers. H, the row
+ * mean and 1/std stay in the handle's arena for tmt_moe_backward_ln.
+ * Row statistics follow one fixed summation order, so H is bit-identical
+ * run to run (the reference's block-tree order is not reproducible).
+ * bf16 weights only.
+ */
+int tmt_moe_forward_ln(tmt_moe* moe, void* stream, int32_t T, const uint16_t* S,
+                       const float* ln_gamma, const float* ln_beta,
+                       const uint16_t* Wr, const float* logit_bias,
+                       const uint16_t* const* W_up, const uint16_t* const* W_down,
+                       uint16_t* Y, float beta);
+
+/*
+ * Backward of tmt_moe_forward_ln: replaces moe_backward + layernorm_bwd
+ * (model.cu:674-680; norm.cu:53-106). Must follow tmt_moe_forward_ln on the
+ * same handle; S is the forward's LayerNorm input, passed again. The gradient
+ * at H stays in the arena (bf16, like the reference's m.dH). Outputs are
+ * overwritten:
+ *   dS [T][d] bf16, dGamma, dBeta [d] fp32 (summed over rows in a fixed
+ *   order; the reference zeroes them and adds with atomics, norm.cu:102-105),
+ *   dWr, dW_up, dW_down as tmt_moe_backward.
+ */
+int tmt_moe_backward_ln(tmt_moe* moe, void* stream, const uint16_t* dY,
+                        const uint16_t* S, const float* ln_gamma,
+                        const uint16_t* Wr, const uint16_t* const* W_up,
+                        const uint16_t* const* W_down, float aux_coef, float z_coef,
+                        uint16_t* dS, float* dGamma, float* dBeta, float* dWr,
+                        float* const* dW_up, float* const* dW_down);
+
+/*
  * Replaces the host read of the router statistics (moe.cu:448-465 and
  * moe_aux_from, moe.cu:470-475). Waits for `stream`, then writes the Switch
  * aux loss E*sum_e(mean_p_e*frac_e), the z-loss mean(lse^2) and the
@@ -149,6 +184,14 @@ int tmt_moe_read_routing(tmt_moe* moe, void* stream, float* logits,
                          int32_t* offsets, int32_t* perm, int32_t* slot_of);
 
 /*
+ * Parity/debug: waits for `stream` and copies what the last
+ * tmt_moe_forward_ln kept: H [T][d] bf16, mean and rstd [T] fp32 (the
+ * reference's Ly.mean / Ly.rstd, model.cu:510-511). Any pointer may be NULL.
+ */
+int tmt_moe_read_norm(tmt_moe* moe, void* stream, uint16_t* H, float* mean,
+                      float* rstd);
+
+/*
  * Per-kernel timing, the counterpart of the reference's TMT_PROFILE phase
  * timers (moe.cu:380-394, 459-464), but with HIP events on the call's stream
  * instead of device-wide synchronisation. While enabled, every kernel launch
@@ -160,7 +203,7 @@ enum {
     TMT_MOE_PH_ROUTER = 0, TMT_MOE_PH_SCAN, TMT_MOE_PH_PERMUTE, TMT_MOE_PH_GEMM_UP,
     TMT_MOE_PH_GEMM_DOWN, TMT_MOE_PH_COMBINE, TMT_MOE_PH_COMBINE_BWD, TMT_MOE_PH_GEMM_DACT,
     TMT_MOE_PH_GEMM_DW_DOWN, TMT_MOE_PH_GEMM_DW_UP, TMT_MOE_PH_GEMM_DX, TMT_MOE_PH_ROUTER_DW,
-    TMT_MOE_PH_SCATTER, TMT_MOE_NPHASES
+    TMT_MOE_PH_SCATTER, TMT_MOE_PH_NORM, TMT_MOE_PH_NORM_BWD, TMT_MOE_NPHASES
 };
 int tmt_moe_set_profiling(tmt_moe* moe, int enable);
 int tmt_moe_read_profile(tmt_moe* moe, float* ms, int32_t* launches, int reset);

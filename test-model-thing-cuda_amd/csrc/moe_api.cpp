@@ -67,7 +67,11 @@ struct tmt_moe {
     // activations
     uint16_t *U, *Aact, *O, *dO, *dU, *dXg, *Xg;
     float *dlogits, *dwr_partial;
+    // LayerNorm in front of the block (tmt_moe_forward_ln / tmt_moe_backward_ln)
+    uint16_t *H, *dH;
+    float *ln_mean, *ln_rstd, *ln_partial;
     int last_T = -1;
+    bool last_ln = false;  // the last forward was tmt_moe_forward_ln
     // per-kernel event timing (tmt_moe_set_profiling)
     bool prof_on = false;
     std::vector<hipEvent_t> prof_events;  // pairs: start, stop
@@ -140,6 +144,9 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
     size_t o_Xg = bwd ? L.add(TK * D * 2) : 0;
     size_t o_dl = bwd ? L.add(T * E * 4) : 0;
     size_t o_dwr = bwd ? L.add((size_t)router_dw_chunks((int)T) * E * D * 4) : 0;
+    size_t o_H = L.add(T * D * 2), o_mean = L.add(T * 4), o_rstd = L.add(T * 4);
+    size_t o_dH = bwd ? L.add(T * D * 2) : 0;
+    size_t o_lnp = bwd ? L.add((size_t)ln_chunks((int)T) * 2 * D * 4) : 0;
     if (m) {
         char* a = m->arena;
         m->logits = (float*)(a + o_logits);
@@ -166,6 +173,11 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->Xg = bwd ? (uint16_t*)(a + o_Xg) : nullptr;
         m->dlogits = bwd ? (float*)(a + o_dl) : nullptr;
         m->dwr_partial = bwd ? (float*)(a + o_dwr) : nullptr;
+        m->H = (uint16_t*)(a + o_H);
+        m->ln_mean = (float*)(a + o_mean);
+        m->ln_rstd = (float*)(a + o_rstd);
+        m->dH = bwd ? (uint16_t*)(a + o_dH) : nullptr;
+        m->ln_partial = bwd ? (float*)(a + o_lnp) : nullptr;
         m->nblk_max = (int)nblk;
     }
     return L.total;
@@ -281,6 +293,156 @@ int check_ptrs(const void* const* tab, int n, const char* what) {
     return TMT_MOE_OK;
 }
 
+// Argument checks of the bf16 forward; `xname` names the tensor the router
+// reads (X, or S for the LayerNorm variant).
+int check_forward(tmt_moe* m, int T, const uint16_t* X, const char* xname, const uint16_t* Wr,
+                  const uint16_t* const* W_up, const uint16_t* const* W_down, const uint16_t* Y) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    const tmt_moe_desc& ds = m->desc;
+    if (ds.weight_format != TMT_MOE_WEIGHTS_BF16)
+        return fail(TMT_MOE_EINVAL, "handle expects MXFP4 weights: use tmt_moe_forward_mxfp4");
+    if (T < 0 || T > ds.max_tokens) return fail(TMT_MOE_EINVAL, "T=%d outside [0, %d]", T, ds.max_tokens);
+    if (T > 0 && (!X || !Y)) return fail(TMT_MOE_EINVAL, "%s and Y must be non-NULL", xname);
+    if (!aligned16(X) || !aligned16(Y)) return fail(TMT_MOE_EINVAL, "%s and Y must be 16-byte aligned", xname);
+    if (ds.experts > 1 && (!Wr || !aligned16(Wr)))
+        return fail(TMT_MOE_EINVAL, "Wr must be a 16-byte aligned pointer when experts > 1");
+    int rc = check_ptrs((const void* const*)W_up, ds.experts, "W_up");
+    if (rc) return rc;
+    if (ds.hidden > 0 && (rc = check_ptrs((const void* const*)W_down, ds.experts, "W_down"))) return rc;
+    return check_device(m);
+}
+
+// Routing, expert GEMMs and combine of the bf16 forward (arguments checked).
+int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* Wr,
+                const float* logit_bias, const uint16_t* const* W_up, const uint16_t* const* W_down,
+                uint16_t* Y, float beta) {
+    const tmt_moe_desc& ds = m->desc;
+    const int E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden, hn = m->hn;
+    int rc;
+    m->last_T = -1;
+
+    if ((rc = route(m, s, T, X, Wr, logit_bias))) return rc;
+    if (T > 0) {
+        GemmParams up{};
+        up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
+        up.N = hn; up.K = d; up.slots = T * K;
+        up.a = X; up.lda = d; up.c = m->U; up.ldc = hn; up.c2 = m->Aact;
+        for (int e = 0; e < E; ++e) up.w[e] = W_up[e];
+        up.ldb = d;
+        // Decode-sized batches stream the weights with the skinny kernel.
+        const bool skinny = T <= kSkinnyMaxTokens;
+        LAUNCH(TMT_MOE_PH_GEMM_UP, skinny ? launch_skinny_gemm(GEMM_UP, h > 0, up, T, s)
+                                          : launch_gemm(GEMM_UP, h > 0, up, s));
+        if (h > 0) {
+            GemmParams dn{};
+            dn.offsets = m->offsets; dn.order = m->order; dn.perm = m->perm; dn.E = E;
+            dn.N = d; dn.K = h; dn.slots = T * K;
+            dn.a = m->Aact; dn.lda = h; dn.c = m->O; dn.ldc = d;
+            for (int e = 0; e < E; ++e) dn.w[e] = W_down[e];
+            dn.ldb = h;
+            LAUNCH(TMT_MOE_PH_GEMM_DOWN, skinny ? launch_skinny_gemm(GEMM_DOWN, false, dn, T, s)
+                                                : launch_gemm(GEMM_DOWN, false, dn, s));
+        }
+        CombineParams cp{};
+        cp.O = h > 0 ? m->O : m->U; cp.slot_of = m->slot_of; cp.gate = m->gate;
+        cp.Y = Y; cp.beta = beta; cp.T = T; cp.d = d; cp.K = K; cp.silu = h == 0;
+        LAUNCH(TMT_MOE_PH_COMBINE, launch_combine(cp, s));
+    }
+    m->last_T = T;
+    return TMT_MOE_OK;
+}
+
+// Argument checks of the backward; `X` / `dX` name the block's input and its
+// gradient (internal arena buffers for the LayerNorm variant).
+int check_backward(tmt_moe* m, const uint16_t* dY, const uint16_t* X, const uint16_t* Wr,
+                   const uint16_t* const* W_up, const uint16_t* const* W_down, const uint16_t* dX,
+                   const float* dWr, float* const* dW_up, float* const* dW_down) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    const tmt_moe_desc& ds = m->desc;
+    if (ds.weight_format != TMT_MOE_WEIGHTS_BF16)
+        return fail(TMT_MOE_EINVAL, "backward needs bf16 weights");
+    if (m->last_T < 0) return fail(TMT_MOE_ESTATE, "backward called without a successful forward");
+    const int T = m->last_T, E = ds.experts, h = ds.hidden;
+    if (T > 0 && (!dY || !X || !dX)) return fail(TMT_MOE_EINVAL, "dY, X and dX must be non-NULL");
+    if (!aligned16(dY) || !aligned16(X) || !aligned16(dX))
+        return fail(TMT_MOE_EINVAL, "dY, X and dX must be 16-byte aligned");
+    if (E > 1 && (!Wr || !dWr || !aligned16(Wr) || !aligned16(dWr)))
+        return fail(TMT_MOE_EINVAL, "Wr and dWr must be 16-byte aligned pointers when experts > 1");
+    int rc = check_ptrs((const void* const*)W_up, E, "W_up");
+    if (rc) return rc;
+    if ((rc = check_ptrs((const void* const*)dW_up, E, "dW_up"))) return rc;
+    if (h > 0) {
+        if ((rc = check_ptrs((const void* const*)W_down, E, "W_down"))) return rc;
+        if ((rc = check_ptrs((const void* const*)dW_down, E, "dW_down"))) return rc;
+    }
+    return check_device(m);
+}
+
+// The backward's launches (arguments checked).
+int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* X,
+                 const uint16_t* Wr, const uint16_t* const* W_up, const uint16_t* const* W_down,
+                 float aux_coef, float z_coef, uint16_t* dX, float* dWr, float* const* dW_up,
+                 float* const* dW_down) {
+    const tmt_moe_desc& ds = m->desc;
+    const int T = m->last_T, E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden, hn = m->hn;
+
+    if (T > 0) {
+        CombineBwdParams cb{};
+        cb.dY = dY; cb.O = h > 0 ? m->O : m->U; cb.slot_of = m->slot_of; cb.idx = m->idx;
+        cb.gate = m->gate; cb.probs = m->probs; cb.lse = m->lse; cb.counts = m->counts;
+        cb.T = T; cb.d = d; cb.E = E; cb.K = K; cb.silu = h == 0;
+        cb.aux_coef = aux_coef; cb.z_coef = z_coef; cb.dO = m->dO; cb.dlogits = m->dlogits;
+        cb.X = X; cb.Xg = m->Xg;
+        LAUNCH(TMT_MOE_PH_COMBINE_BWD, launch_combine_bwd(cb, s));
+    }
+    if (h > 0) {
+        if (T > 0) {
+            GemmParams da{};
+            da.offsets = m->offsets; da.order = m->order; da.perm = m->perm; da.E = E;
+            da.N = h; da.K = d; da.slots = T * K;
+            da.a = m->dO; da.lda = d; da.c = m->dU; da.ldc = h; da.u = m->U;
+            for (int e = 0; e < E; ++e) da.w[e] = W_down[e];
+            da.ldb = h;
+            LAUNCH(TMT_MOE_PH_GEMM_DACT, launch_gemm(GEMM_DACT, false, da, s));
+        }
+        GemmParams dwd{};
+        dwd.offsets = m->offsets; dwd.order = m->order; dwd.perm = m->perm; dwd.E = E;
+        dwd.M = d; dwd.N = h;
+        dwd.a = m->dO; dwd.lda = d; dwd.b = m->Aact; dwd.ldb = h; dwd.ldc = h;
+        for (int e = 0; e < E; ++e) dwd.dw[e] = dW_down[e];
+        LAUNCH(TMT_MOE_PH_GEMM_DW_DOWN, launch_gemm(GEMM_DW_DOWN, false, dwd, s));
+    }
+    GemmParams dwu{};
+    dwu.offsets = m->offsets; dwu.order = m->order; dwu.perm = m->perm; dwu.E = E;
+    dwu.M = hn; dwu.N = d;
+    dwu.a = m->dU; dwu.lda = hn; dwu.b = m->Xg; dwu.ldb = d; dwu.ldc = d;
+    for (int e = 0; e < E; ++e) dwu.dw[e] = dW_up[e];
+    LAUNCH(TMT_MOE_PH_GEMM_DW_UP, launch_gemm(GEMM_DW_UP, false, dwu, s));
+    if (T > 0) {
+        GemmParams dx{};
+        dx.offsets = m->offsets; dx.order = m->order; dx.perm = m->perm; dx.E = E;
+        dx.N = d; dx.K = hn; dx.slots = T * K;
+        dx.a = m->dU; dx.lda = hn; dx.c = m->dXg; dx.ldc = d;
+        for (int e = 0; e < E; ++e) dx.w[e] = W_up[e];
+        dx.ldb = d;
+        LAUNCH(TMT_MOE_PH_GEMM_DX, launch_gemm(GEMM_DX, false, dx, s));
+    }
+    if (E > 1) {
+        // With T == 0 the partial pass sums no rows and writes zeros.
+        RouterDwParams rw{};
+        rw.dlogits = m->dlogits; rw.X = X; rw.T = T; rw.d = d; rw.E = E;
+        rw.nchunks = router_dw_chunks(T); rw.partial = m->dwr_partial; rw.dWr = dWr;
+        LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_router_dw(rw, s));
+    }
+    if (T > 0) {
+        ScatterParams sc{};
+        sc.dXg = m->dXg; sc.slot_of = m->slot_of; sc.dlogits = E > 1 ? m->dlogits : nullptr;
+        sc.Wr = Wr; sc.T = T; sc.d = d; sc.E = E; sc.K = K; sc.dX = dX;
+        LAUNCH(TMT_MOE_PH_SCATTER, launch_scatter(sc, s));
+    }
+    return TMT_MOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -344,50 +506,30 @@ int tmt_moe_forward(tmt_moe* m, void* stream, int32_t T, const uint16_t* X,
                     const uint16_t* Wr, const float* logit_bias,
                     const uint16_t* const* W_up, const uint16_t* const* W_down,
                     uint16_t* Y, float beta) {
-    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
-    const tmt_moe_desc& ds = m->desc;
-    if (ds.weight_format != TMT_MOE_WEIGHTS_BF16)
-        return fail(TMT_MOE_EINVAL, "handle expects MXFP4 weights: use tmt_moe_forward_mxfp4");
-    if (T < 0 || T > ds.max_tokens) return fail(TMT_MOE_EINVAL, "T=%d outside [0, %d]", T, ds.max_tokens);
-    const int E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden, hn = m->hn;
-    if (T > 0 && (!X || !Y)) return fail(TMT_MOE_EINVAL, "X and Y must be non-NULL");
-    if (!aligned16(X) || !aligned16(Y)) return fail(TMT_MOE_EINVAL, "X and Y must be 16-byte aligned");
-    if (E > 1 && (!Wr || !aligned16(Wr))) return fail(TMT_MOE_EINVAL, "Wr must be a 16-byte aligned pointer when experts > 1");
-    int rc = check_ptrs((const void* const*)W_up, E, "W_up");
+    int rc = check_forward(m, T, X, "X", Wr, W_up, W_down, Y);
     if (rc) return rc;
-    if (h > 0 && (rc = check_ptrs((const void* const*)W_down, E, "W_down"))) return rc;
-    if ((rc = check_device(m))) return rc;
+    m->last_ln = false;
+    return run_forward(m, (hipStream_t)stream, T, X, Wr, logit_bias, W_up, W_down, Y, beta);
+}
+
+int tmt_moe_forward_ln(tmt_moe* m, void* stream, int32_t T, const uint16_t* S,
+                       const float* ln_gamma, const float* ln_beta,
+                       const uint16_t* Wr, const float* logit_bias,
+                       const uint16_t* const* W_up, const uint16_t* const* W_down,
+                       uint16_t* Y, float beta) {
+    int rc = check_forward(m, T, S, "S", Wr, W_up, W_down, Y);
+    if (rc) return rc;
+    if (!ln_gamma || !ln_beta || !aligned16(ln_gamma) || !aligned16(ln_beta))
+        return fail(TMT_MOE_EINVAL, "ln_gamma and ln_beta must be 16-byte aligned device pointers");
     hipStream_t s = (hipStream_t)stream;
     m->last_T = -1;
-
-    if ((rc = route(m, s, T, X, Wr, logit_bias))) return rc;
-    if (T > 0) {
-        GemmParams up{};
-        up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
-        up.N = hn; up.K = d; up.slots = T * K;
-        up.a = X; up.lda = d; up.c = m->U; up.ldc = hn; up.c2 = m->Aact;
-        for (int e = 0; e < E; ++e) up.w[e] = W_up[e];
-        up.ldb = d;
-        // Decode-sized batches stream the weights with the skinny kernel.
-        const bool skinny = T <= kSkinnyMaxTokens;
-        LAUNCH(TMT_MOE_PH_GEMM_UP, skinny ? launch_skinny_gemm(GEMM_UP, h > 0, up, T, s)
-                                          : launch_gemm(GEMM_UP, h > 0, up, s));
-        if (h > 0) {
-            GemmParams dn{};
-            dn.offsets = m->offsets; dn.order = m->order; dn.perm = m->perm; dn.E = E;
-            dn.N = d; dn.K = h; dn.slots = T * K;
-            dn.a = m->Aact; dn.lda = h; dn.c = m->O; dn.ldc = d;
-            for (int e = 0; e < E; ++e) dn.w[e] = W_down[e];
-            dn.ldb = h;
-            LAUNCH(TMT_MOE_PH_GEMM_DOWN, skinny ? launch_skinny_gemm(GEMM_DOWN, false, dn, T, s)
-                                                : launch_gemm(GEMM_DOWN, false, dn, s));
-        }
-        CombineParams cp{};
-        cp.O = h > 0 ? m->O : m->U; cp.slot_of = m->slot_of; cp.gate = m->gate;
-        cp.Y = Y; cp.beta = beta; cp.T = T; cp.d = d; cp.K = K; cp.silu = h == 0;
-        LAUNCH(TMT_MOE_PH_COMBINE, launch_combine(cp, s));
-    }
-    m->last_T = T;
+    m->last_ln = false;
+    LayerNormParams ln{};
+    ln.S = S; ln.gamma = ln_gamma; ln.beta = ln_beta; ln.T = T; ln.d = m->desc.d;
+    ln.H = m->H; ln.mean = m->ln_mean; ln.rstd = m->ln_rstd;
+    LAUNCH(TMT_MOE_PH_NORM, launch_ln_fwd(ln, s));
+    if ((rc = run_forward(m, s, T, m->H, Wr, logit_bias, W_up, W_down, Y, beta))) return rc;
+    m->last_ln = true;
     return TMT_MOE_OK;
 }
 
@@ -413,6 +555,7 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
     if ((rc = check_device(m))) return rc;
     hipStream_t s = (hipStream_t)stream;
     m->last_T = -1;
+    m->last_ln = false;
     if ((rc = route(m, s, T, X, Wr, logit_bias))) return rc;
     if (T > 0) {
         GemmParams up{};
@@ -440,81 +583,36 @@ int tmt_moe_backward(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_
                      const uint16_t* Wr, const uint16_t* const* W_up,
                      const uint16_t* const* W_down, float aux_coef, float z_coef,
                      uint16_t* dX, float* dWr, float* const* dW_up, float* const* dW_down) {
-    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
-    const tmt_moe_desc& ds = m->desc;
-    if (ds.weight_format != TMT_MOE_WEIGHTS_BF16)
-        return fail(TMT_MOE_EINVAL, "backward needs bf16 weights");
-    if (m->last_T < 0) return fail(TMT_MOE_ESTATE, "backward called without a successful forward");
-    const int T = m->last_T, E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden, hn = m->hn;
-    if (T > 0 && (!dY || !X || !dX)) return fail(TMT_MOE_EINVAL, "dY, X and dX must be non-NULL");
-    if (!aligned16(dY) || !aligned16(X) || !aligned16(dX))
-        return fail(TMT_MOE_EINVAL, "dY, X and dX must be 16-byte aligned");
-    if (E > 1 && (!Wr || !dWr || !aligned16(Wr) || !aligned16(dWr)))
-        return fail(TMT_MOE_EINVAL, "Wr and dWr must be 16-byte aligned pointers when experts > 1");
-    int rc = check_ptrs((const void* const*)W_up, E, "W_up");
+    int rc = check_backward(m, dY, X, Wr, W_up, W_down, dX, dWr, dW_up, dW_down);
     if (rc) return rc;
-    if ((rc = check_ptrs((const void* const*)dW_up, E, "dW_up"))) return rc;
-    if (h > 0) {
-        if ((rc = check_ptrs((const void* const*)W_down, E, "W_down"))) return rc;
-        if ((rc = check_ptrs((const void* const*)dW_down, E, "dW_down"))) return rc;
-    }
-    if ((rc = check_device(m))) return rc;
-    hipStream_t s = (hipStream_t)stream;
+    return run_backward(m, (hipStream_t)stream, dY, X, Wr, W_up, W_down, aux_coef, z_coef, dX, dWr,
+                        dW_up, dW_down);
+}
 
-    if (T > 0) {
-        CombineBwdParams cb{};
-        cb.dY = dY; cb.O = h > 0 ? m->O : m->U; cb.slot_of = m->slot_of; cb.idx = m->idx;
-        cb.gate = m->gate; cb.probs = m->probs; cb.lse = m->lse; cb.counts = m->counts;
-        cb.T = T; cb.d = d; cb.E = E; cb.K = K; cb.silu = h == 0;
-        cb.aux_coef = aux_coef; cb.z_coef = z_coef; cb.dO = m->dO; cb.dlogits = m->dlogits;
-        cb.X = X; cb.Xg = m->Xg;
-        LAUNCH(TMT_MOE_PH_COMBINE_BWD, launch_combine_bwd(cb, s));
-    }
-    if (h > 0) {
-        if (T > 0) {
-            GemmParams da{};
-            da.offsets = m->offsets; da.order = m->order; da.perm = m->perm; da.E = E;
-            da.N = h; da.K = d; da.slots = T * K;
-            da.a = m->dO; da.lda = d; da.c = m->dU; da.ldc = h; da.u = m->U;
-            for (int e = 0; e < E; ++e) da.w[e] = W_down[e];
-            da.ldb = h;
-            LAUNCH(TMT_MOE_PH_GEMM_DACT, launch_gemm(GEMM_DACT, false, da, s));
-        }
-        GemmParams dwd{};
-        dwd.offsets = m->offsets; dwd.order = m->order; dwd.perm = m->perm; dwd.E = E;
-        dwd.M = d; dwd.N = h;
-        dwd.a = m->dO; dwd.lda = d; dwd.b = m->Aact; dwd.ldb = h; dwd.ldc = h;
-        for (int e = 0; e < E; ++e) dwd.dw[e] = dW_down[e];
-        LAUNCH(TMT_MOE_PH_GEMM_DW_DOWN, launch_gemm(GEMM_DW_DOWN, false, dwd, s));
-    }
-    GemmParams dwu{};
-    dwu.offsets = m->offsets; dwu.order = m->order; dwu.perm = m->perm; dwu.E = E;
-    dwu.M = hn; dwu.N = d;
-    dwu.a = m->dU; dwu.lda = hn; dwu.b = m->Xg; dwu.ldb = d; dwu.ldc = d;
-    for (int e = 0; e < E; ++e) dwu.dw[e] = dW_up[e];
-    LAUNCH(TMT_MOE_PH_GEMM_DW_UP, launch_gemm(GEMM_DW_UP, false, dwu, s));
-    if (T > 0) {
-        GemmParams dx{};
-        dx.offsets = m->offsets; dx.order = m->order; dx.perm = m->perm; dx.E = E;
-        dx.N = d; dx.K = hn; dx.slots = T * K;
-        dx.a = m->dU; dx.lda = hn; dx.c = m->dXg; dx.ldc = d;
-        for (int e = 0; e < E; ++e) dx.w[e] = W_up[e];
-        dx.ldb = d;
-        LAUNCH(TMT_MOE_PH_GEMM_DX, launch_gemm(GEMM_DX, false, dx, s));
-    }
-    if (E > 1) {
-        // With T == 0 the partial pass sums no rows and writes zeros.
-        RouterDwParams rw{};
-        rw.dlogits = m->dlogits; rw.X = X; rw.T = T; rw.d = d; rw.E = E;
-        rw.nchunks = router_dw_chunks(T); rw.partial = m->dwr_partial; rw.dWr = dWr;
-        LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_router_dw(rw, s));
-    }
-    if (T > 0) {
-        ScatterParams sc{};
-        sc.dXg = m->dXg; sc.slot_of = m->slot_of; sc.dlogits = E > 1 ? m->dlogits : nullptr;
-        sc.Wr = Wr; sc.T = T; sc.d = d; sc.E = E; sc.K = K; sc.dX = dX;
-        LAUNCH(TMT_MOE_PH_SCATTER, launch_scatter(sc, s));
-    }
+int tmt_moe_backward_ln(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_t* S,
+                        const float* ln_gamma, const uint16_t* Wr, const uint16_t* const* W_up,
+                        const uint16_t* const* W_down, float aux_coef, float z_coef,
+                        uint16_t* dS, float* dGamma, float* dBeta, float* dWr,
+                        float* const* dW_up, float* const* dW_down) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    if (m->last_T >= 0 && !m->last_ln)
+        return fail(TMT_MOE_ESTATE, "tmt_moe_backward_ln must follow tmt_moe_forward_ln");
+    int rc = check_backward(m, dY, m->H, Wr, W_up, W_down, m->dH, dWr, dW_up, dW_down);
+    if (rc) return rc;
+    const int T = m->last_T;
+    if (T > 0 && (!S || !dS)) return fail(TMT_MOE_EINVAL, "S and dS must be non-NULL");
+    if (!aligned16(S) || !aligned16(dS)) return fail(TMT_MOE_EINVAL, "S and dS must be 16-byte aligned");
+    if (!ln_gamma || !dGamma || !dBeta || !aligned16(ln_gamma) || !aligned16(dGamma) || !aligned16(dBeta))
+        return fail(TMT_MOE_EINVAL, "ln_gamma, dGamma and dBeta must be 16-byte aligned device pointers");
+    hipStream_t s = (hipStream_t)stream;
+    if ((rc = run_backward(m, s, dY, m->H, Wr, W_up, W_down, aux_coef, z_coef, m->dH, dWr, dW_up,
+                           dW_down)))
+        return rc;
+    LayerNormParams ln{};
+    ln.S = S; ln.gamma = ln_gamma; ln.T = T; ln.d = m->desc.d;
+    ln.mean = m->ln_mean; ln.rstd = m->ln_rstd; ln.dH = m->dH; ln.dS = dS;
+    ln.partial = m->ln_partial; ln.dgamma = dGamma; ln.dbeta = dBeta;
+    LAUNCH(TMT_MOE_PH_NORM_BWD, launch_ln_bwd(ln, s));
     return TMT_MOE_OK;
 }
 
@@ -565,7 +663,8 @@ int tmt_moe_read_profile(tmt_moe* m, float* ms, int32_t* launches, int reset) {
 const char* tmt_moe_phase_name(int phase) {
     static const char* names[TMT_MOE_NPHASES] = {
         "router", "scan", "permute", "gemm_up", "gemm_down", "combine", "combine_bwd",
-        "gemm_dact", "gemm_dw_down", "gemm_dw_up", "gemm_dx", "router_dw", "scatter"};
+        "gemm_dact", "gemm_dw_down", "gemm_dw_up", "gemm_dx", "router_dw", "scatter",
+        "norm", "norm_bwd"};
     return (phase >= 0 && phase < TMT_MOE_NPHASES) ? names[phase] : "unknown";
 }
 
@@ -597,6 +696,19 @@ int tmt_moe_read_routing(tmt_moe* m, void* stream, float* logits, float* probs,
     if (offsets) HIP_TRY(hipMemcpy(offsets, m->offsets, (E + 1) * 4, hipMemcpyDeviceToHost));
     if (perm && T) HIP_TRY(hipMemcpy(perm, m->perm, T * K * 4, hipMemcpyDeviceToHost));
     if (slot_of && T) HIP_TRY(hipMemcpy(slot_of, m->slot_of, T * K * 4, hipMemcpyDeviceToHost));
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_read_norm(tmt_moe* m, void* stream, uint16_t* H, float* mean, float* rstd) {
+    if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
+    if (m->last_T < 0 || !m->last_ln) return fail(TMT_MOE_ESTATE, "the last forward was not tmt_moe_forward_ln");
+    int rc = check_device(m);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    const int64_t T = m->last_T, d = m->desc.d;
+    if (H && T) HIP_TRY(hipMemcpy(H, m->H, T * d * 2, hipMemcpyDeviceToHost));
+    if (mean && T) HIP_TRY(hipMemcpy(mean, m->ln_mean, T * 4, hipMemcpyDeviceToHost));
+    if (rstd && T) HIP_TRY(hipMemcpy(rstd, m->ln_rstd, T * 4, hipMemcpyDeviceToHost));
     return TMT_MOE_OK;
 }
 

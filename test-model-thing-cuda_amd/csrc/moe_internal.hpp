@@ -6,6 +6,7 @@
 //   gemm.hip      grouped bf16 MFMA GEMMs over expert segments
 //   skinny.hip    weight-streaming expert GEMMs for decode-sized batches
 //   pointwise.hip combine, combine/router backward, router dW, dX scatter
+//   norm.hip      LayerNorm forward / backward in front of the block
 // The host orchestration lives in moe_api.cpp.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -161,5 +162,24 @@ struct ScatterParams {
     uint16_t* dX;            // [T][d]
 };
 hipError_t launch_scatter(const ScatterParams& p, hipStream_t s);
+
+// ------------------------------------------------------------------ norm --
+struct LayerNormParams {
+    const uint16_t* S;       // [T][d] bf16 LayerNorm input
+    const float* gamma;      // [d]
+    const float* beta;       // [d] (forward)
+    int T, d;
+    uint16_t* H;             // [T][d] bf16 output (forward)
+    float* mean;             // [T] (written by forward, read by backward)
+    float* rstd;             // [T]
+    const uint16_t* dH;      // [T][d] bf16 gradient at H (backward)
+    uint16_t* dS;            // [T][d] bf16 (backward)
+    float* partial;          // [ln_chunks(T)][2][d] dgamma / dbeta chunk sums
+    float* dgamma;           // [d]
+    float* dbeta;            // [d]
+};
+int ln_chunks(int T);
+hipError_t launch_ln_fwd(const LayerNormParams& p, hipStream_t s);
+hipError_t launch_ln_bwd(const LayerNormParams& p, hipStream_t s);
 
 }  // namespace tmt

@@ -1,0 +1,213 @@
+// norm.hip -- the LayerNorm that precedes the MoE block in TMT, as part of
+// the block (tmt-cuda/src/norm.cu:8-106; caller tmt-cuda/src/model.cu:509-514,
+// 678-680).
+//
+//   ln_fwd      H = bf16(((x - mean) * rstd) * gamma + beta), one wave per row.
+//               Row statistics in the canonical order the CPU oracle restates:
+//               element k on lane (k/8) mod 64, lane sums (x) and sums of x*x
+//               in ascending k from +0 (x*x of a bf16 value is exact, so the
+//               fused multiply-add equals multiply-then-add), xor butterfly
+//               32..1; mean = sum/D, var = sumsq/D - mean^2, rstd =
+//               1/sqrt(var + 1e-5), every operation correctly rounded on its
+//               own (the reference's block tree and rsqrtf are not
+//               reproducible, this order is). H is therefore bit-identical to
+//               the oracle's, and so are the router logits computed from it.
+//   ln_bwd_rows dS = rstd * ((g - mean(g)) - xh * mean(g * xh)) with g = dH * gamma,
+//               xh = (x - mean) * rstd, one wave per row.
+//   ln_dgb      dgamma = sum_r dH * xh, dbeta = sum_r dH: chunk partials over
+//               512-row chunks (rows ascending, waves added in order), then a
+//               fixed-order sum over chunks -- no atomics (the reference uses
+//               atomicAdd, norm.cu:68-69).
+#include "device_util.hpp"
+#include "moe_internal.hpp"
+
+// Every float operation below is rounded on its own: no contraction into
+// fused multiply-adds except the explicit one in row_stats. Division and
+// sqrtf are correctly rounded (hipcc's default for fp32).
+#pragma clang fp contract(off)
+
+namespace tmt {
+namespace {
+
+__device__ __forceinline__ void row_stats(const uint16_t* x, int d, int lane, float& mean, float& rstd) {
+    float ls = 0.0f, lq = 0.0f;
+    for (int k0 = lane * 8; k0 < d; k0 += 512) {
+        float v[8];
+        unpack8(*reinterpret_cast<const uint4*>(x + k0), v);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            ls = ls + v[t];
+            lq = __builtin_fmaf(v[t], v[t], lq);
+        }
+    }
+    ls += xor_lane<32>(ls);
+    lq += xor_lane<32>(lq);
+    ls += xor_lane<16>(ls);
+    lq += xor_lane<16>(lq);
+    ls += xor_lane<8>(ls);
+    lq += xor_lane<8>(lq);
+    ls += xor_lane<4>(ls);
+    lq += xor_lane<4>(lq);
+    ls += xor_lane<2>(ls);
+    lq += xor_lane<2>(lq);
+    ls += xor_lane<1>(ls);
+    lq += xor_lane<1>(lq);
+    const float D = (float)d;
+    mean = ls / D;
+    const float var = lq / D - mean * mean;
+    rstd = 1.0f / sqrtf(var + 1e-5f);
+}
+
+__global__ __launch_bounds__(kThreads) void ln_fwd_kernel(LayerNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= p.T) return;
+    const int d = p.d;
+    const uint16_t* x = p.S + (int64_t)r * d;
+    float mean, rstd;
+    row_stats(x, d, lane, mean, rstd);
+    for (int k0 = lane * 8; k0 < d; k0 += 512) {
+        float v[8];
+        unpack8(*reinterpret_cast<const uint4*>(x + k0), v);
+        const float4 g0 = *reinterpret_cast<const float4*>(p.gamma + k0);
+        const float4 g1 = *reinterpret_cast<const float4*>(p.gamma + k0 + 4);
+        const float4 b0 = *reinterpret_cast<const float4*>(p.beta + k0);
+        const float4 b1 = *reinterpret_cast<const float4*>(p.beta + k0 + 4);
+        const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+        const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+        float y[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float xh = (v[t] - mean) * rstd;
+            y[t] = xh * g[t] + b[t];
+        }
+        *reinterpret_cast<uint4*>(p.H + (int64_t)r * d + k0) = pack8(y);
+    }
+    if (lane == 0) {
+        p.mean[r] = mean;
+        p.rstd[r] = rstd;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void ln_bwd_rows_kernel(LayerNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= p.T) return;
+    const int d = p.d;
+    const uint16_t* x = p.S + (int64_t)r * d;
+    const uint16_t* dh = p.dH + (int64_t)r * d;
+    const float mean = p.mean[r], rstd = p.rstd[r];
+    float s1 = 0.0f, s2 = 0.0f;
+    for (int k0 = lane * 8; k0 < d; k0 += 512) {
+        float v[8], gy[8];
+        unpack8(*reinterpret_cast<const uint4*>(x + k0), v);
+        unpack8(*reinterpret_cast<const uint4*>(dh + k0), gy);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float g = gy[t] * p.gamma[k0 + t];
+            const float xh = (v[t] - mean) * rstd;
+            s1 = s1 + g;
+            s2 = s2 + g * xh;
+        }
+    }
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    const float a = s1 / (float)d, b = s2 / (float)d;
+    for (int k0 = lane * 8; k0 < d; k0 += 512) {
+        float v[8], gy[8], out[8];
+        unpack8(*reinterpret_cast<const uint4*>(x + k0), v);
+        unpack8(*reinterpret_cast<const uint4*>(dh + k0), gy);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float g = gy[t] * p.gamma[k0 + t];
+            const float xh = (v[t] - mean) * rstd;
+            out[t] = rstd * ((g - a) - xh * b);
+        }
+        *reinterpret_cast<uint4*>(p.dS + (int64_t)r * d + k0) = pack8(out);
+    }
+}
+
+// Pass 1: block (chunk of kLnRows rows, 256 columns); lane l of every wave
+// owns columns 4l..4l+3, wave w rows w, w+4, ... of the chunk (ascending).
+constexpr int kLnRows = 512;
+constexpr int kLnCols = 256;
+__global__ __launch_bounds__(kThreads) void ln_dgb_partial_kernel(LayerNormParams p) {
+    __shared__ f32x4 s_part[3][2][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int chunk = blockIdx.x;
+    const int col = blockIdx.y * kLnCols + lane * 4;
+    const int d = p.d;
+    const int r0 = chunk * kLnRows, r1 = min(p.T, r0 + kLnRows);
+    const bool cok = col < d;
+    const int ccol = cok ? col : 0;
+    f32x4 ag = f32x4{0.f, 0.f, 0.f, 0.f}, ab = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rb = r0 + wave; rb < r1; rb += 16) {
+        uint2 xv[4], gv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = min(rb + 4 * u, r1 - 1);
+            xv[u] = *reinterpret_cast<const uint2*>(p.S + (int64_t)r * d + ccol);
+            gv[u] = *reinterpret_cast<const uint2*>(p.dH + (int64_t)r * d + ccol);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int r = rb + 4 * u;
+            if (r >= r1) break;  // wave-uniform
+            const float mean = p.mean[r], rstd = p.rstd[r];
+            const float x[4] = {bf_lo(xv[u].x), bf_hi(xv[u].x), bf_lo(xv[u].y), bf_hi(xv[u].y)};
+            const float g[4] = {bf_lo(gv[u].x), bf_hi(gv[u].x), bf_lo(gv[u].y), bf_hi(gv[u].y)};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float xh = (x[t] - mean) * rstd;
+                ag[t] = ag[t] + g[t] * xh;
+                ab[t] = ab[t] + g[t];
+            }
+        }
+    }
+    if (wave > 0) {
+        s_part[wave - 1][0][lane] = ag;
+        s_part[wave - 1][1][lane] = ab;
+    }
+    __syncthreads();
+    if (wave == 0 && cok) {
+        for (int w = 0; w < 3; ++w) {
+            ag += s_part[w][0][lane];
+            ab += s_part[w][1][lane];
+        }
+        *reinterpret_cast<f32x4*>(p.partial + ((int64_t)chunk * 2) * d + col) = ag;
+        *reinterpret_cast<f32x4*>(p.partial + ((int64_t)chunk * 2 + 1) * d + col) = ab;
+    }
+}
+
+// Pass 2: dgamma / dbeta = sum over chunks in ascending order.
+__global__ __launch_bounds__(kThreads) void ln_dgb_reduce_kernel(LayerNormParams p, int nchunks) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= 2 * p.d) return;
+    const int which = i / p.d, k = i - which * p.d;
+    float s = 0.0f;
+    for (int c = 0; c < nchunks; ++c) s += p.partial[((int64_t)c * 2 + which) * p.d + k];
+    (which == 0 ? p.dgamma : p.dbeta)[k] = s;
+}
+
+}  // namespace
+
+int ln_chunks(int T) {
+    const int c = (T + kLnRows - 1) / kLnRows;
+    return c < 1 ? 1 : c;
+}
+
+hipError_t launch_ln_fwd(const LayerNormParams& p, hipStream_t s) {
+    if (p.T <= 0) return hipSuccess;
+    ln_fwd_kernel<<<(p.T + 3) / 4, kThreads, 0, s>>>(p);
+    return hipGetLastError();
+}
+
+hipError_t launch_ln_bwd(const LayerNormParams& p, hipStream_t s) {
+    if (p.T > 0) ln_bwd_rows_kernel<<<(p.T + 3) / 4, kThreads, 0, s>>>(p);
+    const int nch = ln_chunks(p.T);
+    ln_dgb_partial_kernel<<<dim3(nch, (p.d + kLnCols - 1) / kLnCols), kThreads, 0, s>>>(p);
+    ln_dgb_reduce_kernel<<<(2 * p.d + kThreads - 1) / kThreads, kThreads, 0, s>>>(p, nch);
+    return hipGetLastError();
+}
+
+}  // namespace tmt

@@ -31,16 +31,19 @@ EXPORTED = (
     "tmt_moe_forward",
     "tmt_moe_forward_mxfp4",
     "tmt_moe_backward",
+    "tmt_moe_forward_ln",
+    "tmt_moe_backward_ln",
     "tmt_moe_read_stats",
     "tmt_moe_stats_device_ptr",
     "tmt_moe_read_routing",
+    "tmt_moe_read_norm",
     "tmt_moe_set_profiling",
     "tmt_moe_read_profile",
     "tmt_moe_phase_name",
     "tmt_moe_last_error",
 )
 
-NPHASES = 13
+NPHASES = 15
 
 
 class Desc(ctypes.Structure):
@@ -75,6 +78,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.tmt_moe_forward.argtypes = [vp, vp, i32, vp, vp, vp, pp, pp, vp, f32]
     lib.tmt_moe_forward_mxfp4.argtypes = [vp, vp, i32, vp, vp, vp, pp, pp, pp, pp, vp, f32]
     lib.tmt_moe_backward.argtypes = [vp, vp, vp, vp, vp, pp, pp, f32, f32, vp, vp, pp, pp]
+    lib.tmt_moe_forward_ln.argtypes = [vp, vp, i32, vp, vp, vp, vp, vp, pp, pp, vp, f32]
+    lib.tmt_moe_backward_ln.argtypes = [vp, vp, vp, vp, vp, vp, pp, pp, f32, f32, vp, vp, vp, vp,
+                                        pp, pp]
+    lib.tmt_moe_read_norm.argtypes = [vp, vp, vp, vp, vp]
     lib.tmt_moe_read_stats.argtypes = [vp, vp, vp, vp, vp]
     lib.tmt_moe_stats_device_ptr.argtypes = [vp, pp]
     lib.tmt_moe_read_routing.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
@@ -195,6 +202,37 @@ class MoE:
             _table(W_up, self.E), _table(W_down, self.E) if self.h > 0 else None,
             ctypes.c_float(aux_coef), ctypes.c_float(z_coef), _ptr(dX), _ptr(dWr),
             _table(dW_up, self.E), _table(dW_down, self.E) if self.h > 0 else None))
+
+    def forward_ln(self, S, ln_gamma, ln_beta, Wr, W_up, W_down, Y, beta: float = 1.0,
+                   bias=None, stream=None) -> None:
+        """Y <- beta*Y + MoE(LayerNorm(S)). S, Y: [T, d] bf16; ln_gamma,
+        ln_beta: [d] fp32 (the recurrent block's layernorm_fwd + moe_forward)."""
+        T = int(S.shape[0])
+        _check(self.lib.tmt_moe_forward_ln(
+            self.handle, _stream(stream), T, _ptr(S), _ptr(ln_gamma), _ptr(ln_beta), _ptr(Wr),
+            _ptr(bias), _table(W_up, self.E), _table(W_down, self.E) if self.h > 0 else None,
+            _ptr(Y), ctypes.c_float(beta)))
+        self.T = T
+
+    def backward_ln(self, dY, S, ln_gamma, Wr, W_up, W_down, dS, dGamma, dBeta, dWr, dW_up,
+                    dW_down, aux_coef: float = 0.0, z_coef: float = 0.0, stream=None) -> None:
+        """Backward of forward_ln (outputs overwritten): dS [T, d] bf16,
+        dGamma / dBeta [d] fp32, and the MoE weight gradients."""
+        _check(self.lib.tmt_moe_backward_ln(
+            self.handle, _stream(stream), _ptr(dY), _ptr(S), _ptr(ln_gamma), _ptr(Wr),
+            _table(W_up, self.E), _table(W_down, self.E) if self.h > 0 else None,
+            ctypes.c_float(aux_coef), ctypes.c_float(z_coef), _ptr(dS), _ptr(dGamma),
+            _ptr(dBeta), _ptr(dWr), _table(dW_up, self.E),
+            _table(dW_down, self.E) if self.h > 0 else None))
+
+    def norm(self, stream=None) -> dict:
+        """Host copies of what the last forward_ln kept: H (bf16 bits), mean, rstd."""
+        T, d = self.T, self.d
+        out = {"H": np.zeros((T, d), np.uint16), "mean": np.zeros(T, np.float32),
+               "rstd": np.zeros(T, np.float32)}
+        _check(self.lib.tmt_moe_read_norm(self.handle, _stream(stream), out["H"].ctypes.data,
+                                          out["mean"].ctypes.data, out["rstd"].ctypes.data))
+        return out
 
     def stats(self, stream=None):
         """(aux, z, counts[E]) of the last forward; synchronises the stream."""

@@ -32,8 +32,9 @@ def test_library_exports_every_declared_symbol():
 def test_workspace_size_matches_layout():
     c3 = tmt_moe.workspace_size(32768, 1024, 16, 4, 4096)
     TK = 32768 * 4
-    # U, A, dU (TK x h) + O, dO, dXg, Xg (TK x d) in bf16 dominate
-    big = 3 * TK * 4096 * 2 + 4 * TK * 1024 * 2
+    # U, A, dU (TK x h) + O, dO, dXg, Xg (TK x d) + the LayerNorm output H
+    # and its gradient (T x d) in bf16 dominate
+    big = 3 * TK * 4096 * 2 + 4 * TK * 1024 * 2 + 2 * 32768 * 1024 * 2
     assert big <= c3 <= big + (64 << 20)
     ref_mode = tmt_moe.workspace_size(2048, 256, 4, 2, 0)
     assert ref_mode < tmt_moe.workspace_size(2048, 256, 4, 2, 1024)
@@ -67,7 +68,17 @@ def test_null_handle_is_an_error_not_a_crash():
                                ctypes.c_float(1.0)) == -1
     assert "NULL" in tmt_moe.last_error()
     assert lib.tmt_moe_destroy(None) == 0
+    f = ctypes.c_float(0.0)
+    assert lib.tmt_moe_forward_ln(None, None, 0, None, None, None, None, None, None, None,
+                                  None, f) == -1
+    assert lib.tmt_moe_backward_ln(None, None, None, None, None, None, None, None, f, f,
+                                   None, None, None, None, None, None) == -1
+    assert lib.tmt_moe_read_norm(None, None, None, None, None) == -1
     assert lib.tmt_moe_phase_name(0) == b"router"
+    names = [lib.tmt_moe_phase_name(i) for i in range(tmt_moe.NPHASES)]
+    assert all(names) and len(set(names)) == tmt_moe.NPHASES
+    assert names[-2:] == [b"norm", b"norm_bwd"]
+    assert lib.tmt_moe_phase_name(tmt_moe.NPHASES) == b"unknown"
     assert lib.tmt_moe_phase_name(99) == b"unknown"
 
 
