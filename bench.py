@@ -50,6 +50,11 @@ def kernel_work(phase, T, d, E, K, h):
         "combine_bwd": ("hbm", 4 * T * d + 6 * TK * d + 8 * T * E + 12 * TK + 4 * T),
         "router_dw": ("hbm", 2 * T * d + 4 * T * E + 4 * E * d),
         "scatter": ("hbm", 2 * TK * d + 2 * T * d + 4 * T * E + 4 * TK),
+        # S read, H written, row mean + 1/std written, gamma + beta read
+        "norm": ("hbm", 4 * T * d + 8 * T + 8 * d),
+        # scatter with the LayerNorm backward fused (d <= 2048): dXg rows, S,
+        # dlogits, slots and row statistics read, dS written
+        "scatter_ln": ("hbm", 2 * TK * d + 4 * T * d + 4 * T * E + 4 * TK + 8 * T),
     }
     return w.get(phase, ("hbm", 0))
 
@@ -190,6 +195,57 @@ def bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream, reps=100):
     return out
 
 
+def bench_layernorm(m, X, Wr, Wu, Wd, dY, T, d, E, K, h, aux_c, z_c, steps, warmup):
+    """The LayerNorm-fronted block (tmt_moe_forward_ln + tmt_moe_backward_ln):
+    ms per fwd+bwd step and the two LayerNorm phases' rates. S is the c3
+    activation tensor, gamma ~ 1 + 0.1 N(0,1), beta ~ 0.1 N(0,1)."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(7)
+    gamma = 1.0 + 0.1 * torch.randn(d, device="cuda", generator=g)
+    beta = 0.1 * torch.randn(d, device="cuda", generator=g)
+    hn = h if h > 0 else d
+    Y = torch.zeros(T, d, dtype=torch.bfloat16, device="cuda")
+    dS = torch.empty_like(X)
+    dG, dB = torch.empty(d, device="cuda"), torch.empty(d, device="cuda")
+    dWr = torch.empty(E, d, device="cuda")
+    dWu = torch.empty(E, hn, d, device="cuda")
+    dWd = torch.empty(E, d, h, device="cuda") if h > 0 else None
+
+    def step():
+        m.forward_ln(X, gamma, beta, Wr, Wu, Wd, Y, beta=1.0)
+        m.backward_ln(dY, X, gamma, Wr, Wu, Wd, dS, dG, dB, dWr, dWu, dWd, aux_c, z_c)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    m.set_profiling(True)
+    m.profile(reset=True)
+    for _ in range(steps):
+        step()
+    prof = m.profile(reset=True)
+    m.set_profiling(False)
+    out = {"ms_per_step": round(ms, 4), "tokens_s": round(T / (ms / 1e3), 1)}
+    # "scatter" now carries the LayerNorm backward rows; "norm_bwd" is the
+    # fixed-order dGamma/dBeta column sum of the per-workgroup partials.
+    for ph, key in (("norm", "norm"), ("scatter", "scatter_ln"), ("norm_bwd", None)):
+        tot, n = prof[ph]
+        avg = tot / max(n, 1)
+        k = {"avg_ms": round(avg, 4)}
+        if key:
+            _, work = kernel_work(key, T, d, E, K, h)
+            k.update(gbs=round(work / avg / 1e6, 1), hbm_frac=round(work / avg / 1e6 / PEAK_HBM_GBS, 4))
+        out[key or ph] = k
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +255,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-fp4", action="store_true", help="skip the c5 MXFP4 forward measurement")
+    ap.add_argument("--no-ln", action="store_true",
+                    help="skip the LayerNorm-fronted block measurement")
     ap.add_argument("--no-profile", action="store_true",
                     help="time the step without per-kernel events")
     ap.add_argument("--copy-probe", action="store_true",
@@ -300,6 +358,11 @@ def main():
                         "frac": round(ach / PEAK_HBM_GBS, 4),
                         "traffic": measured_traffic(dom) if args.config == "c3" else None}
 
+    ln = None
+    if not args.no_ln:
+        ln = bench_layernorm(m, X, Wr, Wu, Wd, dY, T, d, E, K, h, aux_c, z_c,
+                             max(args.steps // 2, 1), 2)
+
     decode = None
     if not args.no_decode and args.config == "c3":
         decode = bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream)
@@ -336,6 +399,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": kernels,
+        "layernorm_block": ln,
         "decode": decode,
         "mxfp4_forward": fp4,
         "aux": round(aux, 6),

@@ -8,6 +8,7 @@
 // reference's print-and-exit (tmt-cuda/src/common.h:26-33).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -69,7 +70,7 @@ struct tmt_moe {
     float *dlogits, *dwr_partial;
     // LayerNorm in front of the block (tmt_moe_forward_ln / tmt_moe_backward_ln)
     uint16_t *H, *dH;
-    float *ln_mean, *ln_rstd, *ln_partial;
+    float *ln_mean, *ln_rstd, *ln_partial, *ln_partial2;
     int last_T = -1;
     bool last_ln = false;  // the last forward was tmt_moe_forward_ln
     // per-kernel event timing (tmt_moe_set_profiling)
@@ -146,7 +147,9 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
     size_t o_dwr = bwd ? L.add((size_t)router_dw_chunks((int)T) * E * D * 4) : 0;
     size_t o_H = L.add(T * D * 2), o_mean = L.add(T * 4), o_rstd = L.add(T * 4);
     size_t o_dH = bwd ? L.add(T * D * 2) : 0;
-    size_t o_lnp = bwd ? L.add((size_t)ln_chunks((int)T) * 2 * D * 4) : 0;
+    const int64_t ln_rows = std::max(scatter_blocks((int)T), ln_chunks((int)T));
+    size_t o_lnp = bwd ? L.add((size_t)ln_rows * 2 * D * 4) : 0;
+    size_t o_lnp2 = bwd ? L.add((size_t)colsum_groups((int)ln_rows) * 2 * D * 4) : 0;
     if (m) {
         char* a = m->arena;
         m->logits = (float*)(a + o_logits);
@@ -178,6 +181,7 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->ln_rstd = (float*)(a + o_rstd);
         m->dH = bwd ? (uint16_t*)(a + o_dH) : nullptr;
         m->ln_partial = bwd ? (float*)(a + o_lnp) : nullptr;
+        m->ln_partial2 = bwd ? (float*)(a + o_lnp2) : nullptr;
         m->nblk_max = (int)nblk;
     }
     return L.total;
@@ -378,11 +382,23 @@ int check_backward(tmt_moe* m, const uint16_t* dY, const uint16_t* X, const uint
     return check_device(m);
 }
 
-// The backward's launches (arguments checked).
+// Backward of the LayerNorm in front of the block (tmt_moe_backward_ln).
+struct LnGrad {
+    const uint16_t* S;
+    const float* gamma;
+    uint16_t* dS;
+    float* dGamma;
+    float* dBeta;
+};
+
+// The backward's launches (arguments checked). With `ln`, dX is the gradient
+// at the LayerNorm output: for d <= kLnFusedMaxD the scatter consumes it in
+// registers (dX is not written), otherwise it lands in dX and the two-pass
+// LayerNorm backward follows.
 int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* X,
                  const uint16_t* Wr, const uint16_t* const* W_up, const uint16_t* const* W_down,
                  float aux_coef, float z_coef, uint16_t* dX, float* dWr, float* const* dW_up,
-                 float* const* dW_down) {
+                 float* const* dW_down, const LnGrad* ln) {
     const tmt_moe_desc& ds = m->desc;
     const int T = m->last_T, E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden, hn = m->hn;
 
@@ -434,11 +450,26 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
         rw.nchunks = router_dw_chunks(T); rw.partial = m->dwr_partial; rw.dWr = dWr;
         LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_router_dw(rw, s));
     }
+    const bool ln_fused = ln != nullptr && d <= kLnFusedMaxD;
     if (T > 0) {
         ScatterParams sc{};
         sc.dXg = m->dXg; sc.slot_of = m->slot_of; sc.dlogits = E > 1 ? m->dlogits : nullptr;
         sc.Wr = Wr; sc.T = T; sc.d = d; sc.E = E; sc.K = K; sc.dX = dX;
+        if (ln_fused) {
+            sc.ln_S = ln->S; sc.ln_gamma = ln->gamma; sc.ln_mean = m->ln_mean; sc.ln_rstd = m->ln_rstd;
+            sc.ln_dS = ln->dS; sc.ln_partial = m->ln_partial;
+        }
         LAUNCH(TMT_MOE_PH_SCATTER, launch_scatter(sc, s));
+    }
+    if (ln_fused) {
+        LAUNCH(TMT_MOE_PH_NORM_BWD, launch_colsum(m->ln_partial, T > 0 ? scatter_blocks(T) : 0, 2 * d,
+                                                  m->ln_partial2, d, ln->dGamma, ln->dBeta, s));
+    } else if (ln) {
+        LayerNormParams lp{};
+        lp.S = ln->S; lp.gamma = ln->gamma; lp.T = T; lp.d = d;
+        lp.mean = m->ln_mean; lp.rstd = m->ln_rstd; lp.dH = dX; lp.dS = ln->dS;
+        lp.partial = m->ln_partial; lp.partial2 = m->ln_partial2; lp.dgamma = ln->dGamma; lp.dbeta = ln->dBeta;
+        LAUNCH(TMT_MOE_PH_NORM_BWD, launch_ln_bwd(lp, s));
     }
     return TMT_MOE_OK;
 }
@@ -586,7 +617,7 @@ int tmt_moe_backward(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_
     int rc = check_backward(m, dY, X, Wr, W_up, W_down, dX, dWr, dW_up, dW_down);
     if (rc) return rc;
     return run_backward(m, (hipStream_t)stream, dY, X, Wr, W_up, W_down, aux_coef, z_coef, dX, dWr,
-                        dW_up, dW_down);
+                        dW_up, dW_down, nullptr);
 }
 
 int tmt_moe_backward_ln(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_t* S,
@@ -604,16 +635,9 @@ int tmt_moe_backward_ln(tmt_moe* m, void* stream, const uint16_t* dY, const uint
     if (!aligned16(S) || !aligned16(dS)) return fail(TMT_MOE_EINVAL, "S and dS must be 16-byte aligned");
     if (!ln_gamma || !dGamma || !dBeta || !aligned16(ln_gamma) || !aligned16(dGamma) || !aligned16(dBeta))
         return fail(TMT_MOE_EINVAL, "ln_gamma, dGamma and dBeta must be 16-byte aligned device pointers");
-    hipStream_t s = (hipStream_t)stream;
-    if ((rc = run_backward(m, s, dY, m->H, Wr, W_up, W_down, aux_coef, z_coef, m->dH, dWr, dW_up,
-                           dW_down)))
-        return rc;
-    LayerNormParams ln{};
-    ln.S = S; ln.gamma = ln_gamma; ln.T = T; ln.d = m->desc.d;
-    ln.mean = m->ln_mean; ln.rstd = m->ln_rstd; ln.dH = m->dH; ln.dS = dS;
-    ln.partial = m->ln_partial; ln.dgamma = dGamma; ln.dbeta = dBeta;
-    LAUNCH(TMT_MOE_PH_NORM_BWD, launch_ln_bwd(ln, s));
-    return TMT_MOE_OK;
+    const LnGrad lg{S, ln_gamma, dS, dGamma, dBeta};
+    return run_backward(m, (hipStream_t)stream, dY, m->H, Wr, W_up, W_down, aux_coef, z_coef, m->dH, dWr,
+                        dW_up, dW_down, &lg);
 }
 
 int tmt_moe_read_stats(tmt_moe* m, void* stream, float* aux, float* z, int32_t* counts) {

@@ -159,8 +159,19 @@ struct ScatterParams {
     const float* dlogits;    // [T][E] or nullptr
     const uint16_t* Wr;      // [E][d]
     int T, d, E, K;
-    uint16_t* dX;            // [T][d]
+    uint16_t* dX;            // [T][d] (unused when the LayerNorm backward is fused)
+    // LayerNorm backward fused into the scatter (ln_S != nullptr, d <= kLnFusedMaxD):
+    // the bf16-rounded dX row is the gradient at the LayerNorm output.
+    const uint16_t* ln_S;    // [T][d] LayerNorm input
+    const float* ln_gamma;   // [d]
+    const float* ln_mean;    // [T]
+    const float* ln_rstd;    // [T]
+    uint16_t* ln_dS;         // [T][d]
+    float* ln_partial;       // [scatter_blocks(T)][2][d] per-block dgamma / dbeta sums
 };
+constexpr int kLnFusedMaxD = 2048;
+constexpr int kScatterRows = 64;  // rows per scatter workgroup (router or LayerNorm variants)
+int scatter_blocks(int T);
 hipError_t launch_scatter(const ScatterParams& p, hipStream_t s);
 
 // ------------------------------------------------------------------ norm --
@@ -175,11 +186,18 @@ struct LayerNormParams {
     const uint16_t* dH;      // [T][d] bf16 gradient at H (backward)
     uint16_t* dS;            // [T][d] bf16 (backward)
     float* partial;          // [ln_chunks(T)][2][d] dgamma / dbeta chunk sums
+    float* partial2;         // [colsum_groups(ln_chunks(T))][2][d] (level-1 sums)
     float* dgamma;           // [d]
     float* dbeta;            // [d]
 };
 int ln_chunks(int T);
 hipError_t launch_ln_fwd(const LayerNormParams& p, hipStream_t s);
 hipError_t launch_ln_bwd(const LayerNormParams& p, hipStream_t s);
+// Fixed-order column sums of in [nrows][ncols] (ncols % 4 == 0): columns
+// [0, split) to out_lo, [split, ncols) to out_hi; scratch holds
+// [colsum_groups(nrows)][ncols] level-1 sums.
+int colsum_groups(int nrows);
+hipError_t launch_colsum(const float* in, int nrows, int ncols, float* scratch, int split, float* out_lo,
+                         float* out_hi, hipStream_t s);
 
 }  // namespace tmt

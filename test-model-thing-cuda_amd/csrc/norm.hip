@@ -16,8 +16,11 @@
 //               xh = (x - mean) * rstd, one wave per row.
 //   ln_dgb      dgamma = sum_r dH * xh, dbeta = sum_r dH: chunk partials over
 //               512-row chunks (rows ascending, waves added in order), then a
-//               fixed-order sum over chunks -- no atomics (the reference uses
-//               atomicAdd, norm.cu:68-69).
+//               fixed-order sum over chunks (colsum) -- no atomics (the
+//               reference uses atomicAdd, norm.cu:68-69).
+// For d <= kLnFusedMaxD the backward rows and the chunk partials run inside
+// the dX scatter instead (pointwise.hip) and only colsum runs from here; the
+// two kernels above are the path for wider rows.
 #include "device_util.hpp"
 #include "moe_internal.hpp"
 
@@ -179,14 +182,57 @@ __global__ __launch_bounds__(kThreads) void ln_dgb_partial_kernel(LayerNormParam
     }
 }
 
-// Pass 2: dgamma / dbeta = sum over chunks in ascending order.
-__global__ __launch_bounds__(kThreads) void ln_dgb_reduce_kernel(LayerNormParams p, int nchunks) {
-    const int i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= 2 * p.d) return;
-    const int which = i / p.d, k = i - which * p.d;
-    float s = 0.0f;
-    for (int c = 0; c < nchunks; ++c) s += p.partial[((int64_t)c * 2 + which) * p.d + k];
-    (which == 0 ? p.dgamma : p.dbeta)[k] = s;
+// Fixed-order column sums of a [nrows][ncols] fp32 matrix (ncols a multiple
+// of 4), in two levels: level 1 sums groups of kColGroup consecutive rows
+// (wave w takes rows w*16 .. w*16+15 of the group in ascending order, the
+// four waves are then added in order), level 2 adds the group sums in
+// ascending order. Columns [0, split) go to out_lo, the rest to out_hi.
+constexpr int kColGroup = 64;
+__global__ __launch_bounds__(kThreads) void colsum_level1_kernel(const float* in, int nrows, int ncols,
+                                                                 float* out) {
+    __shared__ f32x4 s_part[3][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = blockIdx.x * 256 + lane * 4;
+    const int g = blockIdx.y;
+    const bool cok = col < ncols;
+    const int r0 = g * kColGroup + wave * 16;
+    const int n = max(0, min(16, nrows - r0));
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (cok && n > 0) {
+        f32x4 v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            v[i] = *reinterpret_cast<const f32x4*>(in + (int64_t)(r0 + min(i, n - 1)) * ncols + col);
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+            if (i < n) acc += v[i];
+    }
+    if (wave > 0) s_part[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && cok) {
+        acc += s_part[0][lane];
+        acc += s_part[1][lane];
+        acc += s_part[2][lane];
+        *reinterpret_cast<f32x4*>(out + (int64_t)g * ncols + col) = acc;
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void colsum_level2_kernel(const float* in, int ngroups, int ncols,
+                                                                 int split, float* out_lo, float* out_hi) {
+    const int col = (blockIdx.x * kThreads + threadIdx.x) * 4;
+    if (col >= ncols) return;
+    f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int g0 = 0; g0 < ngroups; g0 += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            v[i] = *reinterpret_cast<const f32x4*>(in + (int64_t)min(g0 + i, ngroups - 1) * ncols + col);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if (g0 + i < ngroups) acc += v[i];
+    }
+    float* dst = col < split ? out_lo + col : out_hi + (col - split);
+    *reinterpret_cast<f32x4*>(dst) = acc;
 }
 
 }  // namespace
@@ -194,6 +240,21 @@ __global__ __launch_bounds__(kThreads) void ln_dgb_reduce_kernel(LayerNormParams
 int ln_chunks(int T) {
     const int c = (T + kLnRows - 1) / kLnRows;
     return c < 1 ? 1 : c;
+}
+
+int colsum_groups(int nrows) {
+    const int g = (nrows + kColGroup - 1) / kColGroup;
+    return g < 1 ? 1 : g;
+}
+
+hipError_t launch_colsum(const float* in, int nrows, int ncols, float* scratch, int split, float* out_lo,
+                         float* out_hi, hipStream_t s) {
+    if (ncols % 4 != 0) return hipErrorInvalidValue;
+    const int ng = colsum_groups(nrows);
+    colsum_level1_kernel<<<dim3((ncols + 255) / 256, ng), kThreads, 0, s>>>(in, nrows, ncols, scratch);
+    colsum_level2_kernel<<<(ncols / 4 + kThreads - 1) / kThreads, kThreads, 0, s>>>(scratch, ng, ncols, split,
+                                                                                   out_lo, out_hi);
+    return hipGetLastError();
 }
 
 hipError_t launch_ln_fwd(const LayerNormParams& p, hipStream_t s) {
@@ -206,8 +267,7 @@ hipError_t launch_ln_bwd(const LayerNormParams& p, hipStream_t s) {
     if (p.T > 0) ln_bwd_rows_kernel<<<(p.T + 3) / 4, kThreads, 0, s>>>(p);
     const int nch = ln_chunks(p.T);
     ln_dgb_partial_kernel<<<dim3(nch, (p.d + kLnCols - 1) / kLnCols), kThreads, 0, s>>>(p);
-    ln_dgb_reduce_kernel<<<(2 * p.d + kThreads - 1) / kThreads, kThreads, 0, s>>>(p, nch);
-    return hipGetLastError();
+    return launch_colsum(p.partial, nch, 2 * p.d, p.partial2, p.d, p.dgamma, p.dbeta, s);
 }
 
 }  // namespace tmt

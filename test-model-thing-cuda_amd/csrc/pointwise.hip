@@ -229,17 +229,64 @@ __global__ __launch_bounds__(kThreads) void router_dw_reduce_kernel(RouterDwPara
     *reinterpret_cast<f32x4*>(p.dWr + i) = s;
 }
 
+// Gradient of one token row over the lane's 8 columns at c0: the K expert
+// rows of dXg added in slot order, plus the router term sum_e dlogits_e Wr_e.
+template <bool ROUTER>
+__device__ __forceinline__ void scatter_chunk(const ScatterParams& p, const int* pos, const float* dl,
+                                              const uint16_t* wl, int c0, float* acc) {
+    const int d = p.d, K = p.K;
+    uint4 xv[kMaxTopK];
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j)
+        if (j < K) xv[j] = *reinterpret_cast<const uint4*>(p.dXg + (int64_t)pos[j] * d + c0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j) {
+        if (j < K) {
+            float v[8];
+            unpack8(xv[j], v);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc[t] += v[t];
+        }
+    }
+    if (ROUTER) {
+        for (int e = 0; e < p.E; ++e) {
+            const float g = dl[e];
+            float w[8];
+            unpack8(*reinterpret_cast<const uint4*>(wl + e * d + c0), w);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc[t] += g * w[t];
+        }
+    }
+}
+
 // One wave per row. For the router input gradient, Wr and the block's rows
 // of dlogits are staged in LDS (all loads of a thread issued before its LDS
 // stores), so the per-expert loop reads only LDS.
-template <bool ROUTER>
+//
+// NI > 0 fuses the backward of the LayerNorm in front of the block
+// (d <= 512*NI): the row's gradient dH = bf16(sum) stays in registers
+// (rounded like the reference's bf16 dH), then
+//   dS = rstd * ((g - mean(g)) - xh * mean(g * xh)),  g = dH * gamma,
+//   xh = (S - mean) * rstd,
+// and every lane keeps dgamma (dH * xh) and dbeta (dH) partials of its
+// columns over the wave's rows (ascending); the four waves are added in
+// order into one [2][d] partial per workgroup.
+constexpr int kRedOnWrExperts = 12;  // E*d*2 bytes of Wr hold the 3*2*d floats
+template <bool ROUTER, int NI>
 __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterParams p, int rows_per_block) {
     extern __shared__ uint4 smem_w[];
+    constexpr int NR = NI > 0 ? NI : 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d = p.d, K = p.K, E = p.E;
     const int rbeg = blockIdx.x * rows_per_block;
     const int rend = min(p.T, rbeg + rows_per_block);
-    float* s_dl = reinterpret_cast<float*>(smem_w + E * d / 8);  // [rows_per_block][E]
+    float* s_dl = reinterpret_cast<float*>(smem_w + (ROUTER ? E * d / 8 : 0));  // [rows_per_block][E]
+    // [3][2][d] wave partials of the LayerNorm variant: over the staged Wr
+    // once every wave is done with it (E >= 12), else after the dlogits.
+    const bool red_on_wr = ROUTER && E >= kRedOnWrExperts;
+    float* s_red = red_on_wr ? reinterpret_cast<float*>(smem_w) : s_dl + (ROUTER ? rows_per_block * E : 0);
     if (ROUTER) {
         const uint4* src = reinterpret_cast<const uint4*>(p.Wr);
         const int nvec = E * d / 8;
@@ -256,39 +303,120 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterParams p, int 
         __syncthreads();
     }
     const uint16_t* wl = reinterpret_cast<const uint16_t*>(smem_w);
+
+    float gam[NR][8], pg[NR][8], pb[NR][8];
+    if constexpr (NI > 0) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int c0 = i * 512 + lane * 8;
+            f32x4 g0 = f32x4{0.f, 0.f, 0.f, 0.f}, g1 = g0;
+            if (c0 < d) {
+                g0 = *reinterpret_cast<const f32x4*>(p.ln_gamma + c0);
+                g1 = *reinterpret_cast<const f32x4*>(p.ln_gamma + c0 + 4);
+            }
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                gam[i][t] = g0[t];
+                gam[i][t + 4] = g1[t];
+            }
+#pragma unroll
+            for (int t = 0; t < 8; ++t) pg[i][t] = pb[i][t] = 0.0f;
+        }
+    }
+
     for (int r = rbeg + wave; r < rend; r += 4) {
         int pos[kMaxTopK];
 #pragma unroll
         for (int j = 0; j < kMaxTopK; ++j)
             if (j < K) pos[j] = p.slot_of[(int64_t)r * K + j];
         const float* dl = s_dl + (r - rbeg) * E;
-        for (int c0 = lane * 8; c0 < d; c0 += 512) {
-            uint4 xv[kMaxTopK];
+        if constexpr (NI == 0) {
+            for (int c0 = lane * 8; c0 < d; c0 += 512) {
+                float acc[8];
+                scatter_chunk<ROUTER>(p, pos, dl, wl, c0, acc);
+                *reinterpret_cast<uint4*>(p.dX + (int64_t)r * d + c0) = pack8(acc);
+            }
+        } else {
+            const float mean = p.ln_mean[r], rstd = p.ln_rstd[r];
+            float hv[NI][8], xs[NI][8];
+            float s1 = 0.0f, s2 = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kMaxTopK; ++j)
-                if (j < K) xv[j] = *reinterpret_cast<const uint4*>(p.dXg + (int64_t)pos[j] * d + c0);
-            float acc[8];
+            for (int i = 0; i < NI; ++i) {
+                const int c0 = i * 512 + lane * 8;
+                if (c0 < d) {
+                    const uint4 sv = *reinterpret_cast<const uint4*>(p.ln_S + (int64_t)r * d + c0);
+                    float acc[8];
+                    scatter_chunk<ROUTER>(p, pos, dl, wl, c0, acc);
+                    unpack8(pack8(acc), hv[i]);
+                    unpack8(sv, xs[i]);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
-#pragma unroll
-            for (int j = 0; j < kMaxTopK; ++j) {
-                if (j < K) {
-                    float v[8];
-                    unpack8(xv[j], v);
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) acc[t] += v[t];
+                    for (int t = 0; t < 8; ++t) {
+                        const float g = hv[i][t] * gam[i][t];
+                        const float xh = (xs[i][t] - mean) * rstd;
+                        s1 += g;
+                        s2 += g * xh;
+                        pg[i][t] += hv[i][t] * xh;
+                        pb[i][t] += hv[i][t];
+                    }
                 }
             }
-            if (ROUTER) {
-                for (int e = 0; e < E; ++e) {
-                    const float g = dl[e];
-                    float w[8];
-                    unpack8(*reinterpret_cast<const uint4*>(wl + e * d + c0), w);
+            s1 = wave_sum(s1);
+            s2 = wave_sum(s2);
+            const float a = s1 / (float)d, b = s2 / (float)d;
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) acc[t] += g * w[t];
+            for (int i = 0; i < NI; ++i) {
+                const int c0 = i * 512 + lane * 8;
+                if (c0 < d) {
+                    float out[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const float g = hv[i][t] * gam[i][t];
+                        const float xh = (xs[i][t] - mean) * rstd;
+                        out[t] = rstd * ((g - a) - xh * b);
+                    }
+                    *reinterpret_cast<uint4*>(p.ln_dS + (int64_t)r * d + c0) = pack8(out);
                 }
             }
-            *reinterpret_cast<uint4*>(p.dX + (int64_t)r * d + c0) = pack8(acc);
+        }
+    }
+
+    if constexpr (NI > 0) {
+        if (red_on_wr) __syncthreads();  // Wr reads done before it is overwritten
+        if (wave > 0) {
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int c0 = i * 512 + lane * 8;
+                if (c0 < d) {
+                    float* dg = s_red + (int64_t)((wave - 1) * 2) * d + c0;
+                    float* db = dg + d;
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        dg[t] = pg[i][t];
+                        db[t] = pb[i][t];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            float* outg = p.ln_partial + (int64_t)blockIdx.x * 2 * d;
+            float* outb = outg + d;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int c0 = i * 512 + lane * 8;
+                if (c0 < d) {
+                    float g[8], b[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        g[t] = ((pg[i][t] + s_red[c0 + t]) + s_red[2 * d + c0 + t]) + s_red[4 * d + c0 + t];
+                        b[t] = ((pb[i][t] + s_red[d + c0 + t]) + s_red[3 * d + c0 + t]) + s_red[5 * d + c0 + t];
+                    }
+                    *reinterpret_cast<f32x4*>(outg + c0) = f32x4{g[0], g[1], g[2], g[3]};
+                    *reinterpret_cast<f32x4*>(outg + c0 + 4) = f32x4{g[4], g[5], g[6], g[7]};
+                    *reinterpret_cast<f32x4*>(outb + c0) = f32x4{b[0], b[1], b[2], b[3]};
+                    *reinterpret_cast<f32x4*>(outb + c0 + 4) = f32x4{b[4], b[5], b[6], b[7]};
+                }
+            }
         }
     }
 }
@@ -325,17 +453,35 @@ hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+int scatter_blocks(int T) {
+    const int b = (T + kScatterRows - 1) / kScatterRows;
+    return b < 1 ? 1 : b;
+}
+
+template <bool ROUTER>
+hipError_t launch_scatter_ni(const ScatterParams& p, int ni, int rows, size_t lds, hipStream_t s) {
+    const int grid = (p.T + rows - 1) / rows;
+    switch (ni) {
+        case 0: scatter_kernel<ROUTER, 0><<<grid, kThreads, lds, s>>>(p, rows); break;
+        case 1: scatter_kernel<ROUTER, 1><<<grid, kThreads, lds, s>>>(p, rows); break;
+        case 2: scatter_kernel<ROUTER, 2><<<grid, kThreads, lds, s>>>(p, rows); break;
+        case 3: scatter_kernel<ROUTER, 3><<<grid, kThreads, lds, s>>>(p, rows); break;
+        case 4: scatter_kernel<ROUTER, 4><<<grid, kThreads, lds, s>>>(p, rows); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     const bool router = p.dlogits != nullptr && p.E > 1;
-    const int rows_per_block = router ? 64 : 4;
-    const int grid = (p.T + rows_per_block - 1) / rows_per_block;
-    if (router)
-        scatter_kernel<true><<<grid, kThreads, (size_t)p.E * p.d * 2 + (size_t)rows_per_block * p.E * 4, s>>>(
-            p, rows_per_block);
-    else
-        scatter_kernel<false><<<grid, kThreads, 0, s>>>(p, rows_per_block);
-    return hipGetLastError();
+    const bool ln = p.ln_S != nullptr;
+    if (ln && p.d > kLnFusedMaxD) return hipErrorInvalidValue;
+    const int rows = (router || ln) ? kScatterRows : 4;
+    size_t lds = router ? (size_t)p.E * p.d * 2 + (size_t)rows * p.E * 4 : 0;
+    if (ln && !(router && p.E >= kRedOnWrExperts)) lds += (size_t)3 * 2 * p.d * 4;
+    const int ni = ln ? (p.d + 511) / 512 : 0;
+    return router ? launch_scatter_ni<true>(p, ni, rows, lds, s) : launch_scatter_ni<false>(p, ni, rows, lds, s);
 }
 
 }  // namespace tmt

@@ -125,13 +125,15 @@ def check_all(g, r, E, h):
 
 
 @pytest.mark.parametrize("T,d,E,K,h", [
-    (300, 256, 4, 2, 1024),    # one 512-row chunk of the dGamma/dBeta pass
-    (1237, 384, 8, 2, 256),    # three chunks, d not a multiple of the 256-column tile
+    (300, 256, 4, 2, 1024),    # a few 64-row workgroups of the fused dGamma/dBeta partials
+    (1237, 384, 8, 2, 256),    # ragged T, d not a multiple of 512
     (520, 1088, 4, 2, 128),    # d > 512: three row passes per lane, the last partial
     (777, 256, 1, 1, 0),       # reference dense path (experts=1, no router)
     (700, 512, 16, 4, 0),      # reference single-linear experts
     (5, 192, 5, 2, 320),       # decode-sized: fused router, weight-streaming GEMMs
     (64, 1024, 16, 4, 512),    # largest decode batch, c3 width
+    (2100, 2048, 12, 2, 128),  # widest row of the scatter-fused backward (4 passes per lane)
+    (300, 2560, 4, 2, 128),    # d > 2048: separate two-pass LayerNorm backward
 ])
 def test_layernorm_block_against_oracle(orc, T, d, E, K, h):
     say(f"layernorm block T={T} d={d} E={E} K={K} h={h} fwd+bwd")
