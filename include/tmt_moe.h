@@ -184,6 +184,28 @@ int tmt_moe_read_routing(tmt_moe* moe, void* stream, float* logits,
                          int32_t* offsets, int32_t* perm, int32_t* slot_of);
 
 /*
+ * Standalone LayerNorm, no handle: replaces layernorm_fwd / layernorm_bwd
+ * (norm.cu:96-106), e.g. for the LayerNorm in front of the reference's MLA
+ * block (model.cu:521-522, 667-669). Same kernels and summation order as
+ * tmt_moe_forward_ln / tmt_moe_backward_ln (d > 2048 path).
+ *   forward:  H = LayerNorm(S; gamma, beta) (eps 1e-5), mean / rstd [T] out.
+ *   backward: from the bf16 gradient dH at H: dS [T][d] bf16, dGamma, dBeta
+ *             [d] fp32 (overwritten, fixed-order sums over rows).
+ * The backward needs `workspace` of at least tmt_moe_layernorm_workspace_size
+ * bytes (device memory, 256-byte aligned); no call allocates. d must be a
+ * multiple of 64, pointers 16-byte aligned. Calls that share a workspace
+ * must be ordered by the caller.
+ */
+int tmt_moe_layernorm_workspace_size(int32_t T, int32_t d, size_t* bytes);
+int tmt_moe_layernorm_forward(void* stream, int32_t T, int32_t d, const uint16_t* S,
+                              const float* gamma, const float* beta, uint16_t* H,
+                              float* mean, float* rstd);
+int tmt_moe_layernorm_backward(void* stream, int32_t T, int32_t d, const uint16_t* S,
+                               const uint16_t* dH, const float* gamma, const float* mean,
+                               const float* rstd, uint16_t* dS, float* dGamma, float* dBeta,
+                               void* workspace, size_t workspace_bytes);
+
+/*
  * Parity/debug: waits for `stream` and copies what the last
  * tmt_moe_forward_ln kept: H [T][d] bf16, mean and rstd [T] fp32 (the
  * reference's Ly.mean / Ly.rstd, model.cu:510-511). Any pointer may be NULL.

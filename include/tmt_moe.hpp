@@ -13,6 +13,7 @@
  *   moe_forward                         moe.cu:372-466
  *   moe_aux_from                        moe.cu:468-475
  *   moe_backward                        moe.cu:477-545
+ *   layernorm_fwd / layernorm_bwd       norm.cu:96-106
  *
  * Behaviour kept from the reference:
  *   - experts are single d x d linears with SiLU inside combine (hidden = 0);
@@ -184,6 +185,52 @@ inline void moe_backward(const B* dY, B** Wexp, const B* Wrouter, float* dWroute
     using namespace tmt_moe_detail;
     backward(bits(dY), table(Wexp), nullptr, bits(Wrouter), dWrouter, dWexp, nullptr, bits(dX), k,
              aux, zcoef);
+}
+
+namespace tmt_moe_detail {
+// Per-device workspace of layernorm_bwd, grown on demand and kept for the
+// process (like the reference's lazily created cuBLAS handle, util.h:23-31;
+// not thread-safe, as the reference's layer is not).
+inline void* ln_workspace(size_t bytes) {
+    static void* ws[64] = {};
+    static size_t cap[64] = {};
+    int dev = 0;
+    check_hip(hipGetDevice(&dev), "layernorm_bwd");
+    if (dev < 0 || dev >= 64) die("layernorm_bwd", "device index out of range");
+    if (cap[dev] < bytes) {
+        if (ws[dev]) {
+            check_hip(hipDeviceSynchronize(), "layernorm_bwd");
+            check_hip(hipFree(ws[dev]), "layernorm_bwd");
+        }
+        ws[dev] = nullptr;
+        check_hip(hipMalloc(&ws[dev], bytes), "layernorm_bwd");
+        cap[dev] = bytes;
+    }
+    return ws[dev];
+}
+}  // namespace tmt_moe_detail
+
+/* norm.cu:96-100: Y = LayerNorm(X; gamma, beta), eps 1e-5; mean / rstd [N]
+ * saved for the backward. On the null stream, like the reference. */
+template <class B>
+inline void layernorm_fwd(const B* X, const float* gamma, const float* beta, B* Y, float* mean,
+                          float* rstd, int N, int D) {
+    using namespace tmt_moe_detail;
+    check(tmt_moe_layernorm_forward(nullptr, N, D, bits(X), gamma, beta, bits(Y), mean, rstd),
+          "layernorm_fwd");
+}
+
+/* norm.cu:102-106: dX [N][D] bf16 from the bf16 gradient dY; dGamma and
+ * dBeta [D] are overwritten (the reference zeroes them, then accumulates). */
+template <class B>
+inline void layernorm_bwd(const B* X, const B* dY, const float* gamma, const float* mean,
+                          const float* rstd, B* dX, float* dGamma, float* dBeta, int N, int D) {
+    using namespace tmt_moe_detail;
+    size_t bytes = 0;
+    check(tmt_moe_layernorm_workspace_size(N, D, &bytes), "layernorm_bwd");
+    check(tmt_moe_layernorm_backward(nullptr, N, D, bits(X), bits(dY), gamma, mean, rstd, bits(dX),
+                                     dGamma, dBeta, ln_workspace(bytes), bytes),
+          "layernorm_bwd");
 }
 
 /* Up/SiLU/down experts: dW_up[e] [hidden][D], dW_down[e] [D][hidden] fp32. */

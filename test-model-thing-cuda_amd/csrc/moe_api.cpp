@@ -474,6 +474,21 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
     return TMT_MOE_OK;
 }
 
+int check_ln_shape(int32_t T, int32_t d) {
+    if (T < 0) return fail(TMT_MOE_EINVAL, "T=%d must be >= 0", T);
+    if (d < 64 || d % 64 != 0) return fail(TMT_MOE_EINVAL, "d=%d must be a positive multiple of 64", d);
+    return TMT_MOE_OK;
+}
+
+// Workspace of the standalone LayerNorm backward, in floats: chunk partials,
+// then (from *level1_off, 256-byte aligned) the level-1 column sums.
+size_t ln_workspace_floats(int32_t T, int32_t d, size_t* level1_off) {
+    const size_t nch = (size_t)ln_chunks(T);
+    const size_t off = (nch * 2 * d + 63) & ~size_t(63);
+    *level1_off = off;
+    return off + (size_t)colsum_groups((int)nch) * 2 * d;
+}
+
 }  // namespace
 
 extern "C" {
@@ -720,6 +735,56 @@ int tmt_moe_read_routing(tmt_moe* m, void* stream, float* logits, float* probs,
     if (offsets) HIP_TRY(hipMemcpy(offsets, m->offsets, (E + 1) * 4, hipMemcpyDeviceToHost));
     if (perm && T) HIP_TRY(hipMemcpy(perm, m->perm, T * K * 4, hipMemcpyDeviceToHost));
     if (slot_of && T) HIP_TRY(hipMemcpy(slot_of, m->slot_of, T * K * 4, hipMemcpyDeviceToHost));
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_layernorm_workspace_size(int32_t T, int32_t d, size_t* bytes) {
+    int rc = check_ln_shape(T, d);
+    if (rc) return rc;
+    if (!bytes) return fail(TMT_MOE_EINVAL, "bytes is NULL");
+    size_t off;
+    *bytes = ln_workspace_floats(T, d, &off) * 4;
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_layernorm_forward(void* stream, int32_t T, int32_t d, const uint16_t* S, const float* gamma,
+                              const float* beta, uint16_t* H, float* mean, float* rstd) {
+    int rc = check_ln_shape(T, d);
+    if (rc) return rc;
+    if (T > 0 && (!S || !H || !mean || !rstd)) return fail(TMT_MOE_EINVAL, "S, H, mean and rstd must be non-NULL");
+    if (!gamma || !beta) return fail(TMT_MOE_EINVAL, "gamma and beta must be non-NULL");
+    if (!aligned16(S) || !aligned16(H) || !aligned16(gamma) || !aligned16(beta))
+        return fail(TMT_MOE_EINVAL, "S, H, gamma and beta must be 16-byte aligned");
+    LayerNormParams p{};
+    p.S = S; p.gamma = gamma; p.beta = beta; p.T = T; p.d = d; p.H = H; p.mean = mean; p.rstd = rstd;
+    HIP_TRY(launch_ln_fwd(p, (hipStream_t)stream));
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_layernorm_backward(void* stream, int32_t T, int32_t d, const uint16_t* S, const uint16_t* dH,
+                               const float* gamma, const float* mean, const float* rstd, uint16_t* dS,
+                               float* dGamma, float* dBeta, void* workspace, size_t workspace_bytes) {
+    int rc = check_ln_shape(T, d);
+    if (rc) return rc;
+    if (T > 0 && (!S || !dH || !mean || !rstd || !dS))
+        return fail(TMT_MOE_EINVAL, "S, dH, mean, rstd and dS must be non-NULL");
+    if (!gamma || !dGamma || !dBeta) return fail(TMT_MOE_EINVAL, "gamma, dGamma and dBeta must be non-NULL");
+    if (!aligned16(S) || !aligned16(dH) || !aligned16(dS) || !aligned16(gamma) || !aligned16(dGamma) ||
+        !aligned16(dBeta))
+        return fail(TMT_MOE_EINVAL, "S, dH, dS, gamma, dGamma and dBeta must be 16-byte aligned");
+    size_t off;
+    const size_t need = ln_workspace_floats(T, d, &off) * 4;
+    if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+        return fail(TMT_MOE_EINVAL, "workspace must be a 256-byte aligned device pointer");
+    if (workspace_bytes < need)
+        return fail(TMT_MOE_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes needed", workspace_bytes, need);
+    LayerNormParams p{};
+    p.S = S; p.gamma = gamma; p.T = T; p.d = d; p.mean = const_cast<float*>(mean);
+    p.rstd = const_cast<float*>(rstd); p.dH = dH; p.dS = dS;
+    p.partial = static_cast<float*>(workspace);
+    p.partial2 = static_cast<float*>(workspace) + off;
+    p.dgamma = dGamma; p.dbeta = dBeta;
+    HIP_TRY(launch_ln_bwd(p, (hipStream_t)stream));
     return TMT_MOE_OK;
 }
 

@@ -37,6 +37,9 @@ EXPORTED = (
     "tmt_moe_stats_device_ptr",
     "tmt_moe_read_routing",
     "tmt_moe_read_norm",
+    "tmt_moe_layernorm_workspace_size",
+    "tmt_moe_layernorm_forward",
+    "tmt_moe_layernorm_backward",
     "tmt_moe_set_profiling",
     "tmt_moe_read_profile",
     "tmt_moe_phase_name",
@@ -82,6 +85,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.tmt_moe_backward_ln.argtypes = [vp, vp, vp, vp, vp, vp, pp, pp, f32, f32, vp, vp, vp, vp,
                                         pp, pp]
     lib.tmt_moe_read_norm.argtypes = [vp, vp, vp, vp, vp]
+    lib.tmt_moe_layernorm_workspace_size.argtypes = [i32, i32, ctypes.POINTER(ctypes.c_size_t)]
+    lib.tmt_moe_layernorm_forward.argtypes = [vp, i32, i32, vp, vp, vp, vp, vp, vp]
+    lib.tmt_moe_layernorm_backward.argtypes = [vp, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                               ctypes.c_size_t]
     lib.tmt_moe_read_stats.argtypes = [vp, vp, vp, vp, vp]
     lib.tmt_moe_stats_device_ptr.argtypes = [vp, pp]
     lib.tmt_moe_read_routing.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
@@ -145,6 +152,33 @@ def workspace_size(max_tokens: int, d: int, experts: int, topk: int, hidden: int
     out = ctypes.c_size_t(0)
     _check(lib.tmt_moe_workspace_size(ctypes.byref(desc), ctypes.byref(out)))
     return int(out.value)
+
+
+def layernorm_workspace_size(T: int, d: int) -> int:
+    """Bytes of device workspace layernorm_backward needs for [T, d]."""
+    out = ctypes.c_size_t(0)
+    _check(load_library().tmt_moe_layernorm_workspace_size(T, d, ctypes.byref(out)))
+    return int(out.value)
+
+
+def layernorm_forward(S, gamma, beta, H, mean, rstd, stream=None) -> None:
+    """Standalone LayerNorm (the reference's layernorm_fwd): H = LN(S),
+    mean / rstd [T] written. S, H: [T, d] bf16; gamma, beta: [d] fp32."""
+    T, d = int(S.shape[0]), int(S.shape[1])
+    _check(load_library().tmt_moe_layernorm_forward(
+        _stream(stream), T, d, _ptr(S), _ptr(gamma), _ptr(beta), _ptr(H), _ptr(mean), _ptr(rstd)))
+
+
+def layernorm_backward(S, dH, gamma, mean, rstd, dS, dGamma, dBeta, workspace,
+                       stream=None) -> None:
+    """Standalone LayerNorm backward (the reference's layernorm_bwd) from the
+    bf16 gradient dH; workspace is a device buffer of at least
+    layernorm_workspace_size(T, d) bytes."""
+    T, d = int(S.shape[0]), int(S.shape[1])
+    nbytes = workspace.numel() * workspace.element_size()
+    _check(load_library().tmt_moe_layernorm_backward(
+        _stream(stream), T, d, _ptr(S), _ptr(dH), _ptr(gamma), _ptr(mean), _ptr(rstd), _ptr(dS),
+        _ptr(dGamma), _ptr(dBeta), _ptr(workspace), ctypes.c_size_t(nbytes)))
 
 
 class MoE:

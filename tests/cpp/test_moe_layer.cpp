@@ -6,6 +6,7 @@
 //   test_router        tmt-cuda/src/architecture_test.cu:62-87
 //   test_moe_backward  tmt-cuda/src/architecture_test.cu:228-264
 //   experts limit      tmt-cuda/tests/cli.sh:30-32 (the limit here is 64)
+//   test_layernorm     layernorm_fwd / layernorm_bwd (norm.cu:96-106) against fp64
 //
 // Usage: test_moe_layer            all GPU tests
 //        test_moe_layer reject     only the configuration check (no GPU use)
@@ -273,6 +274,73 @@ static void test_deferred_stats() {
     std::puts("PASS deferred router statistics equal the immediate read");
 }
 
+// layernorm_fwd / layernorm_bwd (norm.cu:96-106) against an fp64 host
+// LayerNorm on the same bf16 inputs, and the fused moe path's input side:
+// rows with offsets and scales, ragged D.
+static void test_layernorm() {
+    const int N = 77, D = 320;
+    std::mt19937 g(21);
+    std::normal_distribution<float> nd(0.f, 1.f);
+    std::vector<uint16_t> X(N * D), dY(N * D);
+    std::vector<float> gamma(D), beta(D);
+    for (int r = 0; r < N; ++r) {
+        const float sc = std::exp(nd(g)), sh = nd(g);
+        for (int k = 0; k < D; ++k) X[r * D + k] = f2bf(nd(g) * sc + sh);
+    }
+    for (auto& v : dY) v = f2bf(nd(g));
+    for (int k = 0; k < D; ++k) {
+        gamma[k] = 1.f + 0.2f * nd(g);
+        beta[k] = 0.1f * nd(g);
+    }
+    Device dv;
+    const uint16_t* dX_in = dv.upload(X);
+    const uint16_t* ddY = dv.upload(dY);
+    const float* dg = dv.upload(gamma);
+    const float* db = dv.upload(beta);
+    uint16_t* dYout = dv.alloc<uint16_t>(N * D);
+    uint16_t* dXout = dv.alloc<uint16_t>(N * D);
+    float* mean = dv.alloc<float>(N);
+    float* rstd = dv.alloc<float>(N);
+    float* dG = dv.alloc<float>(D);
+    float* dB = dv.alloc<float>(D);
+    layernorm_fwd(dX_in, dg, db, dYout, mean, rstd, N, D);
+    layernorm_bwd(dX_in, ddY, dg, mean, rstd, dXout, dG, dB, N, D);
+    const auto H = to_f32(download(dYout, N * D));
+    const auto dXg = to_f32(download(dXout, N * D));
+    const auto dGg = download(dG, D), dBg = download(dB, D);
+    std::vector<float> Href(N * D), dXref(N * D), dGref(D, 0.f), dBref(D, 0.f);
+    std::vector<double> acc_g(D, 0.0), acc_b(D, 0.0);
+    for (int r = 0; r < N; ++r) {
+        double s = 0, q = 0;
+        for (int k = 0; k < D; ++k) s += bf2f(X[r * D + k]);
+        const double m = s / D;
+        for (int k = 0; k < D; ++k) q += (bf2f(X[r * D + k]) - m) * (bf2f(X[r * D + k]) - m);
+        const double rs = 1.0 / std::sqrt(q / D + 1e-5);
+        double s1 = 0, s2 = 0;
+        for (int k = 0; k < D; ++k) {
+            const double xh = (bf2f(X[r * D + k]) - m) * rs, gy = bf2f(dY[r * D + k]) * gamma[k];
+            Href[r * D + k] = (float)(xh * gamma[k] + beta[k]);
+            s1 += gy;
+            s2 += gy * xh;
+            acc_g[k] += bf2f(dY[r * D + k]) * xh;
+            acc_b[k] += bf2f(dY[r * D + k]);
+        }
+        for (int k = 0; k < D; ++k) {
+            const double xh = (bf2f(X[r * D + k]) - m) * rs, gy = bf2f(dY[r * D + k]) * gamma[k];
+            dXref[r * D + k] = (float)(rs * (gy - s1 / D - xh * s2 / D));
+        }
+    }
+    for (int k = 0; k < D; ++k) {
+        dGref[k] = (float)acc_g[k];
+        dBref[k] = (float)acc_b[k];
+    }
+    require(rel_l2(H, Href) < 5e-3, "layernorm_fwd output");
+    require(rel_l2(dXg, dXref) < 1e-2, "layernorm_bwd dX");
+    require(rel_l2(dGg, dGref) < 1e-3, "layernorm_bwd dGamma");
+    require(rel_l2(dBg, dBref) < 1e-5, "layernorm_bwd dBeta");
+    std::puts("PASS layernorm_fwd / layernorm_bwd match an fp64 LayerNorm");
+}
+
 int main(int argc, char** argv) {
     if (argc > 1 && std::string(argv[1]) == "reject") {
         MoeKeep k;
@@ -283,6 +351,7 @@ int main(int argc, char** argv) {
     test_router();
     test_moe_backward();
     test_deferred_stats();
+    test_layernorm();
     std::puts("ALL PASS");
     return 0;
 }

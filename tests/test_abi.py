@@ -57,6 +57,26 @@ def test_invalid_descriptors_are_rejected(desc, msg):
     assert msg in str(ei.value)
 
 
+def test_layernorm_workspace_and_argument_checks():
+    # chunk partials (512-row chunks) + level-1 sums (64 chunks per group), fp32
+    nch = 32768 // 512
+    assert tmt_moe.layernorm_workspace_size(32768, 1024) == (nch * 2 * 1024 + 1 * 2 * 1024) * 4
+    assert tmt_moe.layernorm_workspace_size(0, 64) == (2 * 64 + 2 * 64) * 4
+    with pytest.raises(tmt_moe.MoeError, match="multiple of 64"):
+        tmt_moe.layernorm_workspace_size(16, 100)
+    lib = tmt_moe.load_library()
+    f = ctypes.c_void_p
+    # argument checks run before any device work
+    assert lib.tmt_moe_layernorm_forward(None, 4, 96, None, None, None, None, None, None) == -1
+    assert "multiple of 64" in tmt_moe.last_error()
+    assert lib.tmt_moe_layernorm_forward(None, 4, 128, None, None, None, None, None, None) == -1
+    assert "non-NULL" in tmt_moe.last_error()
+    fake = f(256)  # 256-byte aligned, never dereferenced: the size check fails first
+    assert lib.tmt_moe_layernorm_backward(None, 4, 128, fake, fake, fake, fake, fake, fake, fake,
+                                          fake, fake, ctypes.c_size_t(16)) == -1
+    assert "smaller than" in tmt_moe.last_error()
+
+
 def test_mxfp4_requires_hidden():
     with pytest.raises(tmt_moe.MoeError, match="hidden"):
         tmt_moe.workspace_size(16, 128, 4, 2, 0, tmt_moe.WEIGHTS_MXFP4)

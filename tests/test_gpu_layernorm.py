@@ -212,6 +212,45 @@ def test_backward_ln_needs_forward_ln():
         m.close()
 
 
+@pytest.mark.parametrize("T,d", [(1, 64), (777, 384), (4096, 1024), (300, 2560), (0, 128)])
+def test_standalone_layernorm_against_oracle(orc, T, d):
+    """tmt_moe_layernorm_forward / _backward (the reference's layernorm_fwd /
+    layernorm_bwd): H, mean, rstd bit-identical; dS, dGamma, dBeta within
+    1e-2 rel-L2 of the oracle on the same bf16 dH."""
+    say(f"standalone layernorm T={T} d={d}")
+    rng = np.random.default_rng(T + d)
+    X = bf16_bits(rng.standard_normal((max(T, 1), d)).astype(np.float32))[:T]
+    S, gamma, beta = ln_inputs(X, seed=d)
+    dH = bf16_bits(rng.standard_normal((T, d)).astype(np.float32))
+    Sd = dev(S)
+    g_d, b_d = torch.from_numpy(gamma).cuda(), torch.from_numpy(beta).cuda()
+    H = torch.empty(T, d, dtype=torch.bfloat16, device="cuda")
+    mean = torch.empty(T, device="cuda")
+    rstd = torch.empty(T, device="cuda")
+    tmt_moe.layernorm_forward(Sd, g_d, b_d, H, mean, rstd)
+    ws = torch.empty(tmt_moe.layernorm_workspace_size(T, d), dtype=torch.uint8, device="cuda")
+    dS = torch.full((T, d), float("nan"), dtype=torch.bfloat16, device="cuda")
+    dG = torch.full((d,), float("nan"), device="cuda")
+    dB = torch.full((d,), float("nan"), device="cuda")
+    tmt_moe.layernorm_backward(Sd, dev(dH), g_d, mean, rstd, dS, dG, dB, ws)
+    torch.cuda.synchronize()
+    ref = orc.layernorm(S, gamma, beta)
+    Hh = H.view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(Hh, ref["H"]), "H is not bit-identical"
+    assert np.array_equal(mean.cpu().numpy().view(np.uint32), ref["mean"].view(np.uint32))
+    assert np.array_equal(rstd.cpu().numpy().view(np.uint32), ref["rstd"].view(np.uint32))
+    rb = orc.layernorm_bwd(S, bf16_to_f32(dH), gamma, ref["mean"], ref["rstd"])
+    got = {"dS": host_f32(dS), "dgamma": dG.cpu().numpy(), "dbeta": dB.cpu().numpy()}
+    for n in ("dS", "dgamma", "dbeta"):
+        assert np.isfinite(got[n]).all(), n
+        if T == 0:
+            assert not got[n].any(), n
+            continue
+        err = rel_l2(got[n], rb[n])
+        say(f"  {n}: rel-L2 {err:.2e}")
+        assert err <= REL_L2, f"{n} rel-L2 {err:.3e}"
+
+
 def test_c3_full_size_layernorm_block(orc):
     """At the c3 size: H bit-exact against the oracle LayerNorm, routing
     bit-exact against the oracle router on H, and the fused backward equal to
