@@ -231,6 +231,54 @@ int tmt_moe_set_profiling(tmt_moe* moe, int enable);
 int tmt_moe_read_profile(tmt_moe* moe, float* ms, int32_t* launches, int reset);
 const char* tmt_moe_phase_name(int phase);
 
+/*
+ * Multi-tensor AdamW with global-norm gradient clipping over fp32 master
+ * weights, moments and gradients, e.g. the block's router and expert
+ * parameters with the fp32 gradients tmt_moe_backward writes. Replaces the
+ * reference's multi-tensor optimizer (MTParams + mt_sumsq_kernel +
+ * mt_adam_kernel + mt_zero_kernel, adam.cu:37-96; table built once,
+ * model.cu:436-454; optimizer_step, model.cu:716-729).
+ *
+ * tmt_moe_adamw_create copies the parameter list into a device chunk table
+ * (chunks of 8192 elements) and allocates all state; no later call
+ * allocates. Every pointer must be 16-byte aligned device memory; `work`
+ * may be NULL. flags: TMT_MOE_ADAMW_IN_NORM (the gradient counts in the
+ * clipping norm), TMT_MOE_ADAMW_UPDATE (the parameter is updated).
+ *
+ * tmt_moe_adamw_step enqueues, with `step` the 1-based update count
+ * (bias corrections 1 - beta^step, as the reference's powf(b, step + 1) with
+ * its 0-based step):
+ *   s = sum of grad^2 over IN_NORM parameters (double, one fixed order);
+ *   if s is finite, for every UPDATE parameter, elementwise:
+ *     g = grad * scale, scale = clip > 0 ? min(1, clip / max(sqrt(s), 1e-12)) : 1
+ *     m = b1 m + (1 - b1) g;  v = b2 v + (1 - b2) g g
+ *     w = w - lr ((m / bc1) / (sqrt(v / bc2) + eps) + wd w);  work = bf16(w)
+ *   else nothing is updated (the reference refuses the step).
+ * tmt_moe_adamw_read_sumsq waits for `stream` and returns s of the last step
+ * (the reference's one host read per step); the caller refuses non-finite.
+ * tmt_moe_adamw_zero_grads sets every gradient to zero (model.cu:592).
+ * Calls on one optimizer must be ordered by the caller.
+ */
+enum { TMT_MOE_ADAMW_IN_NORM = 1, TMT_MOE_ADAMW_UPDATE = 2 };
+typedef struct tmt_moe_adamw_param {
+    float* master;     /* [n] fp32 master weights */
+    float* m;          /* [n] first moment */
+    float* v;          /* [n] second moment */
+    float* grad;       /* [n] fp32 gradient */
+    uint16_t* work;    /* [n] bf16 working copy, or NULL */
+    int64_t n;
+    int32_t flags;
+} tmt_moe_adamw_param;
+typedef struct tmt_moe_adamw tmt_moe_adamw;
+int tmt_moe_adamw_create(const tmt_moe_adamw_param* params, int32_t count, tmt_moe_adamw** out);
+int tmt_moe_adamw_destroy(tmt_moe_adamw* opt);
+int tmt_moe_adamw_step(tmt_moe_adamw* opt, void* stream, float clip, float lr, float beta1,
+                       float beta2, float eps, float weight_decay, int32_t step);
+int tmt_moe_adamw_read_sumsq(tmt_moe_adamw* opt, void* stream, double* sumsq);
+int tmt_moe_adamw_zero_grads(tmt_moe_adamw* opt, void* stream);
+/* Number of chunks (workgroups per launch) of an optimizer. */
+int tmt_moe_adamw_chunks(tmt_moe_adamw* opt, int32_t* chunks);
+
 /* Thread-local message of the last failing call on this thread. */
 const char* tmt_moe_last_error(void);
 

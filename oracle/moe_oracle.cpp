@@ -817,6 +817,97 @@ int orc_mxfp4_quantize(const float* in, int64_t rows, int64_t n,
     return 0;
 }
 
+}  // extern "C"
+
+namespace {
+
+constexpr int kAdamChunkElems = 8192;  // elements per chunk (one GPU workgroup)
+constexpr int kAdamThreads = 256;      // threads per workgroup (4 waves of 64)
+
+// Fixed-order sum of 256 per-thread values: within each wave of 64 an xor
+// butterfly (offsets 32..1, every lane ends with the same value), then the
+// four wave sums as ((w0 + w1) + w2) + w3.
+double adamw_block_sum(const double* t) {
+    double w[4];
+    for (int wave = 0; wave < 4; ++wave) {
+        double l[64];
+        for (int i = 0; i < 64; ++i) l[i] = t[wave * 64 + i];
+        for (int off = 32; off >= 1; off >>= 1) {
+            double nl[64];
+            for (int i = 0; i < 64; ++i) nl[i] = l[i] + l[i ^ off];
+            std::memcpy(l, nl, sizeof(l));
+        }
+        w[wave] = l[0];
+    }
+    return ((w[0] + w[1]) + w[2]) + w[3];
+}
+
+// Canonical sum of grad^2 of one chunk: thread t owns the 4-element groups
+// t, t+256, t+512, ... (elements in ascending order inside a group) and
+// accumulates (double)g*g from +0; then adamw_block_sum.
+double adamw_chunk_sum(const float* g, int len) {
+    double t[kAdamThreads];
+    for (int th = 0; th < kAdamThreads; ++th) {
+        double acc = 0.0;
+        for (int i0 = th * 4; i0 < len; i0 += 4 * kAdamThreads)
+            for (int k = 0; k < 4 && i0 + k < len; ++k) acc = acc + (double)g[i0 + k] * (double)g[i0 + k];
+        t[th] = acc;
+    }
+    return adamw_block_sum(t);
+}
+
+uint16_t adamw_tobf(float f) {  // round to nearest even (finite values)
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+}  // namespace
+
+extern "C" {
+
+// The reference's per-element update (adam.cu:74-85) with the clipping scale
+// of adam.cu:72-73 and the bias corrections of model.cu:721-722.
+int orc_adamw_step(int32_t count, float* const* master, float* const* m, float* const* v,
+                   const float* const* grad, uint16_t* const* work, const int64_t* n,
+                   const int32_t* flags, float clip, float lr, float b1, float b2, float eps,
+                   float wd, int32_t step, double* sumsq) {
+    if (count < 0 || step < 1 || !sumsq) return -1;
+    // Chunk sums in table order, then the global fixed-order sum.
+    std::vector<double> part;
+    for (int i = 0; i < count; ++i)
+        for (int64_t s = 0; s < n[i]; s += kAdamChunkElems) {
+            const int len = (int)std::min<int64_t>(kAdamChunkElems, n[i] - s);
+            part.push_back((flags[i] & 1) ? adamw_chunk_sum(grad[i] + s, len) : 0.0);
+        }
+    double t[kAdamThreads];
+    for (int th = 0; th < kAdamThreads; ++th) {
+        double acc = 0.0;
+        for (size_t k = th; k < part.size(); k += kAdamThreads) acc = acc + part[k];
+        t[th] = acc;
+    }
+    const double s = adamw_block_sum(t);
+    *sumsq = s;
+    if (!std::isfinite(s)) return 0;  // the step is refused: nothing changes
+    const float scale = clip > 0.f ? std::fmin(1.f, clip / std::fmax((float)std::sqrt(s), 1e-12f)) : 1.f;
+    const float bc1 = 1.0f - powf(b1, (float)step), bc2 = 1.0f - powf(b2, (float)step);
+    for (int i = 0; i < count; ++i) {
+        if (!(flags[i] & 2)) continue;
+        for (int64_t k = 0; k < n[i]; ++k) {
+            const float g = grad[i][k] * scale;
+            const float nm = b1 * m[i][k] + (1.0f - b1) * g;
+            const float nv = b2 * v[i][k] + (1.0f - b2) * g * g;
+            m[i][k] = nm;
+            v[i][k] = nv;
+            const float w = master[i][k] - lr * ((nm / bc1) / (std::sqrt(nv / bc2) + eps) + wd * master[i][k]);
+            master[i][k] = w;
+            if (work && work[i]) work[i][k] = adamw_tobf(w);
+        }
+    }
+    return 0;
+}
+
 int orc_mxfp4_dequantize(const uint8_t* packed, const uint8_t* scales,
                          int64_t rows, int64_t n, float* out) {
     if (!packed || !scales || !out || n % 32 != 0 || rows < 0) return -1;

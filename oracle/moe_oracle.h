@@ -127,6 +127,18 @@ int orc_layernorm_bwd(int32_t T, int32_t d, const uint16_t* S, const float* dH,
                       const float* gamma, const float* mean, const float* rstd,
                       float* dS, float* dgamma, float* dbeta);
 
+/* Multi-tensor AdamW with global-norm clipping (tmt-cuda/src/adam.cu:37-96,
+ * optimizer_step tmt-cuda/src/model.cu:716-729), one step in place over
+ * `count` parameters; flags bit 0: gradient in the norm, bit 1: updated.
+ * `step` is the 1-based update count (bias corrections 1 - b^step). The
+ * squared gradient norm is summed in the canonical order documented at
+ * adamw_chunk_sum() (the GPU kernels' order) and returned in *sumsq; a
+ * non-finite norm leaves every parameter unchanged. */
+int orc_adamw_step(int32_t count, float* const* master, float* const* m, float* const* v,
+                   const float* const* grad, uint16_t* const* work, const int64_t* n,
+                   const int32_t* flags, float clip, float lr, float b1, float b2, float eps,
+                   float wd, int32_t step, double* sumsq);
+
 #ifdef __cplusplus
 }
 #endif

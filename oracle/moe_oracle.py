@@ -209,6 +209,30 @@ def layernorm(S, gamma, beta):
     return {"H": H, "mean": mean, "rstd": rstd}
 
 
+def adamw_step(params, clip, lr, b1, b2, eps, wd, step):
+    """One multi-tensor AdamW step in place. params: list of dicts with fp32
+    arrays master, m, v, grad (C-contiguous, modified in place), optional
+    uint16 work, and int flags (1: in the norm, 2: updated). Returns the
+    squared gradient norm in the canonical order."""
+    cnt = len(params)
+    for q in params:
+        for k in ("master", "m", "v", "grad"):
+            assert q[k].dtype == np.float32 and q[k].flags["C_CONTIGUOUS"], k
+        if q.get("work") is not None:
+            assert q["work"].dtype == np.uint16 and q["work"].flags["C_CONTIGUOUS"]
+    ptrs = lambda key: (ctypes.c_void_p * max(cnt, 1))(
+        *[(q[key].ctypes.data if q.get(key) is not None else None) for q in params])
+    n = np.array([q["master"].size for q in params] or [0], np.int64)
+    flags = np.array([q["flags"] for q in params] or [0], np.int32)
+    s = ctypes.c_double(0)
+    f = ctypes.c_float
+    rc = load().orc_adamw_step(cnt, ptrs("master"), ptrs("m"), ptrs("v"), ptrs("grad"), ptrs("work"),
+                               _p(n), _p(flags), f(clip), f(lr), f(b1), f(b2), f(eps), f(wd),
+                               ctypes.c_int32(step), ctypes.byref(s))
+    assert rc == 0, rc
+    return s.value
+
+
 def layernorm_bwd(S, dH, gamma, mean, rstd):
     """LayerNorm backward from the fp32 gradient dH of its output."""
     S = _c(S, np.uint16)

@@ -9,7 +9,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -798,6 +800,130 @@ int tmt_moe_read_norm(tmt_moe* m, void* stream, uint16_t* H, float* mean, float*
     if (H && T) HIP_TRY(hipMemcpy(H, m->H, T * d * 2, hipMemcpyDeviceToHost));
     if (mean && T) HIP_TRY(hipMemcpy(mean, m->ln_mean, T * 4, hipMemcpyDeviceToHost));
     if (rstd && T) HIP_TRY(hipMemcpy(rstd, m->ln_rstd, T * 4, hipMemcpyDeviceToHost));
+    return TMT_MOE_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------ AdamW --
+
+struct tmt_moe_adamw {
+    int device = 0;
+    char* arena = nullptr;  // chunk table, per-chunk sums, sumsq, ticket
+    AdamwParams p{};
+};
+
+namespace {
+int adamw_check_device(const tmt_moe_adamw* o) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev != o->device)
+        return fail(TMT_MOE_EINVAL, "optimizer was created on device %d but device %d is current", o->device, dev);
+    return TMT_MOE_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int tmt_moe_adamw_create(const tmt_moe_adamw_param* params, int32_t count, tmt_moe_adamw** out) {
+    if (!out) return fail(TMT_MOE_EINVAL, "out is NULL");
+    *out = nullptr;
+    if (count < 0 || (count > 0 && !params)) return fail(TMT_MOE_EINVAL, "bad parameter list (count=%d)", count);
+    std::vector<AdamwChunk> chunks;
+    for (int i = 0; i < count; ++i) {
+        const tmt_moe_adamw_param& q = params[i];
+        if (q.n < 0) return fail(TMT_MOE_EINVAL, "parameter %d: n=%lld < 0", i, (long long)q.n);
+        if (q.flags < 0 || q.flags > 3) return fail(TMT_MOE_EINVAL, "parameter %d: unknown flags %d", i, q.flags);
+        if (q.n > 0 && (!q.master || !q.m || !q.v || !q.grad))
+            return fail(TMT_MOE_EINVAL, "parameter %d: master, m, v and grad must be non-NULL", i);
+        if (!aligned16(q.master) || !aligned16(q.m) || !aligned16(q.v) || !aligned16(q.grad) || !aligned16(q.work))
+            return fail(TMT_MOE_EINVAL, "parameter %d: pointers must be 16-byte aligned", i);
+        for (int64_t s = 0; s < q.n; s += kAdamChunk) {
+            AdamwChunk c{};
+            c.master = q.master + s; c.m = q.m + s; c.v = q.v + s; c.grad = q.grad + s;
+            c.work = q.work ? q.work + s : nullptr;
+            c.len = (int32_t)std::min<int64_t>(kAdamChunk, q.n - s);
+            c.flags = q.flags;
+            chunks.push_back(c);
+        }
+    }
+    if (chunks.size() > (size_t)INT32_MAX) return fail(TMT_MOE_EINVAL, "too many chunks");
+    tmt_moe_adamw* o = new (std::nothrow) tmt_moe_adamw();
+    if (!o) return fail(TMT_MOE_ENOMEM, "host allocation failed");
+    hipError_t err = hipGetDevice(&o->device);
+    const size_t nch = chunks.size();
+    Layout L;
+    const size_t o_tab = L.add(nch * sizeof(AdamwChunk)), o_part = L.add(nch * 8), o_sum = L.add(8),
+                 o_tick = L.add(4);
+    if (err == hipSuccess) err = hipMalloc(&o->arena, L.total);
+    if (err != hipSuccess) {
+        delete o;
+        (void)hipGetLastError();
+        return fail(TMT_MOE_ENOMEM, "optimizer allocation failed: %s", hipGetErrorString(err));
+    }
+    o->p.chunks = reinterpret_cast<AdamwChunk*>(o->arena + o_tab);
+    o->p.nchunks = (int)nch;
+    o->p.partial = reinterpret_cast<double*>(o->arena + o_part);
+    o->p.sumsq = reinterpret_cast<double*>(o->arena + o_sum);
+    o->p.ticket = reinterpret_cast<int*>(o->arena + o_tick);
+    if (nch) err = hipMemcpy(o->arena + o_tab, chunks.data(), nch * sizeof(AdamwChunk), hipMemcpyHostToDevice);
+    if (err == hipSuccess) err = hipMemset(o->arena + o_sum, 0, sizeof(double));
+    if (err == hipSuccess) err = hipMemset(o->arena + o_tick, 0, sizeof(int));  // last-workgroup ticket
+    if (err == hipSuccess) err = hipStreamSynchronize(nullptr);
+    if (err != hipSuccess) {
+        (void)hipFree(o->arena);
+        delete o;
+        (void)hipGetLastError();
+        return fail(TMT_MOE_EDEVICE, "initialising the optimizer failed: %s", hipGetErrorString(err));
+    }
+    *out = o;
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_adamw_destroy(tmt_moe_adamw* o) {
+    if (!o) return TMT_MOE_OK;
+    hipError_t err = o->arena ? hipFree(o->arena) : hipSuccess;
+    delete o;
+    if (err != hipSuccess) return fail(TMT_MOE_EDEVICE, "hipFree failed: %s", hipGetErrorString(err));
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_adamw_step(tmt_moe_adamw* o, void* stream, float clip, float lr, float beta1, float beta2,
+                       float eps, float weight_decay, int32_t step) {
+    if (!o) return fail(TMT_MOE_EINVAL, "optimizer is NULL");
+    if (step < 1) return fail(TMT_MOE_EINVAL, "step=%d must be >= 1 (1-based update count)", step);
+    int rc = adamw_check_device(o);
+    if (rc) return rc;
+    AdamwHyper h{};
+    h.clip = clip; h.lr = lr; h.b1 = beta1; h.b2 = beta2; h.eps = eps; h.wd = weight_decay;
+    h.bc1 = 1.0f - powf(beta1, (float)step);
+    h.bc2 = 1.0f - powf(beta2, (float)step);
+    hipStream_t s = (hipStream_t)stream;
+    HIP_TRY(launch_adamw_sumsq(o->p, s));
+    HIP_TRY(launch_adamw_update(o->p, h, s));
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_adamw_read_sumsq(tmt_moe_adamw* o, void* stream, double* sumsq) {
+    if (!o || !sumsq) return fail(TMT_MOE_EINVAL, "optimizer or sumsq is NULL");
+    int rc = adamw_check_device(o);
+    if (rc) return rc;
+    HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+    HIP_TRY(hipMemcpy(sumsq, o->p.sumsq, 8, hipMemcpyDeviceToHost));
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_adamw_zero_grads(tmt_moe_adamw* o, void* stream) {
+    if (!o) return fail(TMT_MOE_EINVAL, "optimizer is NULL");
+    int rc = adamw_check_device(o);
+    if (rc) return rc;
+    HIP_TRY(launch_adamw_zero(o->p, (hipStream_t)stream));
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_adamw_chunks(tmt_moe_adamw* o, int32_t* chunks) {
+    if (!o || !chunks) return fail(TMT_MOE_EINVAL, "optimizer or chunks is NULL");
+    *chunks = o->p.nchunks;
     return TMT_MOE_OK;
 }
 

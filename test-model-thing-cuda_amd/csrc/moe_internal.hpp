@@ -7,6 +7,7 @@
 //   skinny.hip    weight-streaming expert GEMMs for decode-sized batches
 //   pointwise.hip combine, combine/router backward, router dW, dX scatter
 //   norm.hip      LayerNorm forward / backward in front of the block
+//   adamw.hip     multi-tensor AdamW with global-norm clipping
 // The host orchestration lives in moe_api.cpp.
 #pragma once
 #include <hip/hip_runtime.h>
@@ -199,5 +200,32 @@ hipError_t launch_ln_bwd(const LayerNormParams& p, hipStream_t s);
 int colsum_groups(int nrows);
 hipError_t launch_colsum(const float* in, int nrows, int ncols, float* scratch, int split, float* out_lo,
                          float* out_hi, hipStream_t s);
+
+// ----------------------------------------------------------------- adamw --
+constexpr int kAdamChunk = 8192;      // elements per chunk (one workgroup)
+constexpr int kAdamwInNorm = 1;       // flags bit 0: gradient counts in the clipping norm
+constexpr int kAdamwUpdate = 2;       // flags bit 1: parameter is updated
+struct AdamwChunk {
+    float* master;                    // chunk start in each tensor (16-byte aligned)
+    float* m;
+    float* v;
+    float* grad;
+    uint16_t* work;                   // bf16 working copy or nullptr
+    int32_t len;                      // elements, <= kAdamChunk
+    int32_t flags;
+};
+struct AdamwParams {
+    const AdamwChunk* chunks;         // [nchunks]
+    int nchunks;
+    double* partial;                  // [nchunks] per-chunk sums of grad^2
+    double* sumsq;                    // global sum of grad^2 (written by the last workgroup)
+    int* ticket;                      // zero between launches
+};
+struct AdamwHyper {
+    float clip, lr, b1, b2, eps, wd, bc1, bc2;
+};
+hipError_t launch_adamw_sumsq(const AdamwParams& p, hipStream_t s);
+hipError_t launch_adamw_update(const AdamwParams& p, const AdamwHyper& h, hipStream_t s);
+hipError_t launch_adamw_zero(const AdamwParams& p, hipStream_t s);
 
 }  // namespace tmt

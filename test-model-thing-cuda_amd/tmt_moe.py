@@ -40,6 +40,12 @@ EXPORTED = (
     "tmt_moe_layernorm_workspace_size",
     "tmt_moe_layernorm_forward",
     "tmt_moe_layernorm_backward",
+    "tmt_moe_adamw_create",
+    "tmt_moe_adamw_destroy",
+    "tmt_moe_adamw_step",
+    "tmt_moe_adamw_read_sumsq",
+    "tmt_moe_adamw_zero_grads",
+    "tmt_moe_adamw_chunks",
     "tmt_moe_set_profiling",
     "tmt_moe_read_profile",
     "tmt_moe_phase_name",
@@ -89,6 +95,12 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.tmt_moe_layernorm_forward.argtypes = [vp, i32, i32, vp, vp, vp, vp, vp, vp]
     lib.tmt_moe_layernorm_backward.argtypes = [vp, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                                ctypes.c_size_t]
+    lib.tmt_moe_adamw_create.argtypes = [vp, i32, ctypes.POINTER(vp)]
+    lib.tmt_moe_adamw_destroy.argtypes = [vp]
+    lib.tmt_moe_adamw_step.argtypes = [vp, vp, f32, f32, f32, f32, f32, f32, i32]
+    lib.tmt_moe_adamw_read_sumsq.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_double)]
+    lib.tmt_moe_adamw_zero_grads.argtypes = [vp, vp]
+    lib.tmt_moe_adamw_chunks.argtypes = [vp, ctypes.POINTER(i32)]
     lib.tmt_moe_read_stats.argtypes = [vp, vp, vp, vp, vp]
     lib.tmt_moe_stats_device_ptr.argtypes = [vp, pp]
     lib.tmt_moe_read_routing.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
@@ -307,3 +319,71 @@ class MoE:
                                             ("logits", "probs", "idx", "gate", "offsets",
                                              "perm", "slot_of"))))
         return out
+
+
+ADAMW_IN_NORM = 1
+ADAMW_UPDATE = 2
+
+
+class AdamwParam(ctypes.Structure):
+    _fields_ = [("master", ctypes.c_void_p), ("m", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("grad", ctypes.c_void_p), ("work", ctypes.c_void_p), ("n", ctypes.c_int64),
+                ("flags", ctypes.c_int32)]
+
+
+class AdamW:
+    """Multi-tensor AdamW with global-norm clipping (the reference's MTParams
+    optimizer). params: list of dicts of fp32 CUDA tensors master, m, v, grad
+    (same numel), optional bf16 work, and flags (ADAMW_IN_NORM | ADAMW_UPDATE).
+    The tensors must stay alive while the optimizer exists."""
+
+    def __init__(self, params):
+        self.lib = load_library()
+        self._keep = params
+        arr = (AdamwParam * max(len(params), 1))()
+        for i, q in enumerate(params):
+            n = q["master"].numel()
+            for k in ("m", "v", "grad"):
+                assert q[k].numel() == n, k
+            if q.get("work") is not None:
+                assert q["work"].numel() == n
+            arr[i] = AdamwParam(_ptr(q["master"]), _ptr(q["m"]), _ptr(q["v"]), _ptr(q["grad"]),
+                                _ptr(q.get("work")), n, int(q.get("flags", ADAMW_IN_NORM | ADAMW_UPDATE)))
+        h = ctypes.c_void_p(0)
+        _check(self.lib.tmt_moe_adamw_create(ctypes.cast(arr, ctypes.c_void_p), len(params),
+                                             ctypes.byref(h)))
+        self.handle = h
+
+    def step(self, step: int, lr: float, clip: float = 0.0, beta1: float = 0.9,
+             beta2: float = 0.999, eps: float = 1e-8, weight_decay: float = 0.01,
+             stream=None) -> None:
+        """Enqueue one update; step is the 1-based update count."""
+        f = ctypes.c_float
+        _check(self.lib.tmt_moe_adamw_step(self.handle, _stream(stream), f(clip), f(lr), f(beta1),
+                                           f(beta2), f(eps), f(weight_decay), int(step)))
+
+    def sumsq(self, stream=None) -> float:
+        """Squared gradient norm of the last step (waits for the stream)."""
+        out = ctypes.c_double(0)
+        _check(self.lib.tmt_moe_adamw_read_sumsq(self.handle, _stream(stream), ctypes.byref(out)))
+        return out.value
+
+    def zero_grads(self, stream=None) -> None:
+        _check(self.lib.tmt_moe_adamw_zero_grads(self.handle, _stream(stream)))
+
+    @property
+    def chunks(self) -> int:
+        out = ctypes.c_int32(0)
+        _check(self.lib.tmt_moe_adamw_chunks(self.handle, ctypes.byref(out)))
+        return out.value
+
+    def close(self) -> None:
+        if getattr(self, "handle", None) is not None and self.handle.value:
+            self.lib.tmt_moe_adamw_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -77,6 +77,25 @@ def test_layernorm_workspace_and_argument_checks():
     assert "smaller than" in tmt_moe.last_error()
 
 
+def test_adamw_argument_checks():
+    lib = tmt_moe.load_library()
+    out = ctypes.c_void_p(0)
+    assert lib.tmt_moe_adamw_create(None, -1, ctypes.byref(out)) == -1
+    p = (tmt_moe.AdamwParam * 1)()
+    p[0] = tmt_moe.AdamwParam(256, 512, 768, 1024 + 4, None, 10, 3)  # grad misaligned
+    assert lib.tmt_moe_adamw_create(ctypes.cast(p, ctypes.c_void_p), 1, ctypes.byref(out)) == -1
+    assert "16-byte aligned" in tmt_moe.last_error()
+    p[0] = tmt_moe.AdamwParam(256, 512, 768, 1024, None, 10, 7)
+    assert lib.tmt_moe_adamw_create(ctypes.cast(p, ctypes.c_void_p), 1, ctypes.byref(out)) == -1
+    assert "flags" in tmt_moe.last_error()
+    p[0] = tmt_moe.AdamwParam(256, 0, 768, 1024, None, 10, 3)
+    assert lib.tmt_moe_adamw_create(ctypes.cast(p, ctypes.c_void_p), 1, ctypes.byref(out)) == -1
+    assert "non-NULL" in tmt_moe.last_error()
+    f = ctypes.c_float(0.0)
+    assert lib.tmt_moe_adamw_step(None, None, f, f, f, f, f, f, 1) == -1
+    assert lib.tmt_moe_adamw_zero_grads(None, None) == -1
+
+
 def test_mxfp4_requires_hidden():
     with pytest.raises(tmt_moe.MoeError, match="hidden"):
         tmt_moe.workspace_size(16, 128, 4, 2, 0, tmt_moe.WEIGHTS_MXFP4)
