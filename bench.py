@@ -246,6 +246,47 @@ def bench_layernorm(m, X, Wr, Wu, Wd, dY, T, d, E, K, h, aux_c, z_c, steps, warm
     return out
 
 
+def bench_adamw(d, E, h, steps=10, warmup=2):
+    """Multi-tensor AdamW (tmt_moe_adamw_step: gradient-norm pass + clipped
+    update) over the block's parameters at this config: router [E, d] and
+    E x (W_up [h, d] + W_down [d, h]), fp32 master / m / v / grad and a bf16
+    work copy each. Algorithmic HBM bytes per element: 4 (norm pass reads
+    grad) + 16 read + 14 written (update) = 34."""
+    import torch
+    import tmt_moe
+    sizes = [E * d] + [h * d] * (2 * E)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    params = []
+    for n in sizes:
+        params.append(dict(master=0.02 * torch.randn(n, device="cuda", generator=g),
+                           m=torch.zeros(n, device="cuda"), v=torch.zeros(n, device="cuda"),
+                           grad=1e-3 * torch.randn(n, device="cuda", generator=g),
+                           work=torch.empty(n, dtype=torch.bfloat16, device="cuda"),
+                           flags=tmt_moe.ADAMW_IN_NORM | tmt_moe.ADAMW_UPDATE))
+    opt = tmt_moe.AdamW(params)
+    try:
+        for i in range(warmup):
+            opt.step(i + 1, 1e-4, clip=1.0)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for i in range(steps):
+            opt.step(warmup + i + 1, 1e-4, clip=1.0)
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        ms = ev0.elapsed_time(ev1) / steps
+        n = sum(sizes)
+        gbs = 34 * n / (ms / 1e3) / 1e9
+        return {"params": n, "chunks": opt.chunks, "ms_per_step": round(ms, 4),
+                "gbs": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4),
+                "bytes_per_param": 34, "finite": bool(opt.sumsq() == opt.sumsq())}
+    finally:
+        opt.close()
+        del params
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -257,6 +298,10 @@ def main():
     ap.add_argument("--no-fp4", action="store_true", help="skip the c5 MXFP4 forward measurement")
     ap.add_argument("--no-ln", action="store_true",
                     help="skip the LayerNorm-fronted block measurement")
+    ap.add_argument("--no-adamw", action="store_true",
+                    help="skip the multi-tensor AdamW measurement")
+    ap.add_argument("--adamw-only", action="store_true",
+                    help="only the AdamW step over the config's block parameters")
     ap.add_argument("--no-profile", action="store_true",
                     help="time the step without per-kernel events")
     ap.add_argument("--copy-probe", action="store_true",
@@ -294,6 +339,9 @@ def main():
     dWu = torch.empty(E, hn, d, dtype=torch.float32, device="cuda")
     dWd = torch.empty(E, d, h, dtype=torch.float32, device="cuda") if h > 0 else None
     aux_c, z_c = cfg.get("aux", 0.0), cfg.get("z", 0.0)
+    if args.adamw_only:
+        print(json.dumps({"adamw": bench_adamw(d, E, h if h > 0 else d, args.steps, args.warmup)}))
+        return
     if args.decode_only:
         print(json.dumps({"decode": bench_decode(X, Wr, Wu, Wd, d, E, K, h, torch.cuda.current_stream())}))
         return
@@ -367,6 +415,10 @@ def main():
     if not args.no_decode and args.config == "c3":
         decode = bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream)
 
+    adamw = None
+    if not args.no_adamw:
+        adamw = bench_adamw(d, E, h if h > 0 else d)
+
     fp4 = None
     if not args.no_fp4 and args.config == "c3":
         fp4 = bench_mxfp4(stream)
@@ -400,6 +452,7 @@ def main():
         "cpu_baseline": cpu,
         "kernels": kernels,
         "layernorm_block": ln,
+        "adamw": adamw,
         "decode": decode,
         "mxfp4_forward": fp4,
         "aux": round(aux, 6),

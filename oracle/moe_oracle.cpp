@@ -824,12 +824,14 @@ namespace {
 constexpr int kAdamChunkElems = 8192;  // elements per chunk (one GPU workgroup)
 constexpr int kAdamThreads = 256;      // threads per workgroup (4 waves of 64)
 
-// Fixed-order sum of 256 per-thread values: within each wave of 64 an xor
-// butterfly (offsets 32..1, every lane ends with the same value), then the
-// four wave sums as ((w0 + w1) + w2) + w3.
-double adamw_block_sum(const double* t) {
-    double w[4];
-    for (int wave = 0; wave < 4; ++wave) {
+constexpr int kAdamNormThreads = 1024;  // threads of the final (one-workgroup) sum
+
+// Fixed-order sum of nthreads per-thread values: within each wave of 64 an
+// xor butterfly (offsets 32..1, every lane ends with the same value), then
+// the wave sums added in order, ((w0 + w1) + w2) + ...
+double adamw_block_sum(const double* t, int nthreads) {
+    double tot = 0.0;
+    for (int wave = 0; wave < nthreads / 64; ++wave) {
         double l[64];
         for (int i = 0; i < 64; ++i) l[i] = t[wave * 64 + i];
         for (int off = 32; off >= 1; off >>= 1) {
@@ -837,9 +839,9 @@ double adamw_block_sum(const double* t) {
             for (int i = 0; i < 64; ++i) nl[i] = l[i] + l[i ^ off];
             std::memcpy(l, nl, sizeof(l));
         }
-        w[wave] = l[0];
+        tot = wave == 0 ? l[0] : tot + l[0];
     }
-    return ((w[0] + w[1]) + w[2]) + w[3];
+    return tot;
 }
 
 // Canonical sum of grad^2 of one chunk: thread t owns the 4-element groups
@@ -853,7 +855,7 @@ double adamw_chunk_sum(const float* g, int len) {
             for (int k = 0; k < 4 && i0 + k < len; ++k) acc = acc + (double)g[i0 + k] * (double)g[i0 + k];
         t[th] = acc;
     }
-    return adamw_block_sum(t);
+    return adamw_block_sum(t, kAdamThreads);
 }
 
 uint16_t adamw_tobf(float f) {  // round to nearest even (finite values)
@@ -881,13 +883,13 @@ int orc_adamw_step(int32_t count, float* const* master, float* const* m, float* 
             const int len = (int)std::min<int64_t>(kAdamChunkElems, n[i] - s);
             part.push_back((flags[i] & 1) ? adamw_chunk_sum(grad[i] + s, len) : 0.0);
         }
-    double t[kAdamThreads];
-    for (int th = 0; th < kAdamThreads; ++th) {
+    double t[kAdamNormThreads];
+    for (int th = 0; th < kAdamNormThreads; ++th) {
         double acc = 0.0;
-        for (size_t k = th; k < part.size(); k += kAdamThreads) acc = acc + part[k];
+        for (size_t k = th; k < part.size(); k += kAdamNormThreads) acc = acc + part[k];
         t[th] = acc;
     }
-    const double s = adamw_block_sum(t);
+    const double s = adamw_block_sum(t, kAdamNormThreads);
     *sumsq = s;
     if (!std::isfinite(s)) return 0;  // the step is refused: nothing changes
     const float scale = clip > 0.f ? std::fmin(1.f, clip / std::fmax((float)std::sqrt(s), 1e-12f)) : 1.f;

@@ -15,6 +15,8 @@
  *   backward                           tmt-cuda/src/moe.cu:160-249, 477-545
  *   numerics (silu, silu')             tmt-cuda/src/common.h:15-24
  *   GEMM layouts ([out,in], fp32 acc)  tmt-cuda/src/linalg.cu:1-41
+ *   LayerNorm                          tmt-cuda/src/norm.cu:8-106
+ *   multi-tensor AdamW                 tmt-cuda/src/adam.cu:37-96, model.cu:716-729
  *
  * Conventions shared with the HIP library (include/tmt_moe.h):
  *   bf16 values are raw uint16 bit patterns; fp32 accumulation everywhere.
@@ -132,8 +134,8 @@ int orc_layernorm_bwd(int32_t T, int32_t d, const uint16_t* S, const float* dH,
  * `count` parameters; flags bit 0: gradient in the norm, bit 1: updated.
  * `step` is the 1-based update count (bias corrections 1 - b^step). The
  * squared gradient norm is summed in the canonical order documented at
- * adamw_chunk_sum() (the GPU kernels' order) and returned in *sumsq; a
- * non-finite norm leaves every parameter unchanged. */
+ * adamw_chunk_sum() and orc_adamw_step() (the GPU kernels' order) and
+ * returned in *sumsq; a non-finite norm leaves every parameter unchanged. */
 int orc_adamw_step(int32_t count, float* const* master, float* const* m, float* const* v,
                    const float* const* grad, uint16_t* const* work, const int64_t* n,
                    const int32_t* flags, float clip, float lr, float b1, float b2, float eps,

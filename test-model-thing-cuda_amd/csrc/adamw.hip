@@ -8,13 +8,15 @@
 //   adamw_sumsq_kernel  per chunk: sum of grad^2 in double, in a fixed order
 //                       (thread t owns the float4 groups t, t+256, ... of
 //                       the chunk, x y z w in order; wave xor butterfly
-//                       32..1; the four waves added in order). The last
-//                       workgroup to finish (atomic ticket between
-//                       device-scope fences, re-armed by that workgroup)
-//                       adds the chunk sums in the same fixed order
-//                       (thread t: chunks t, t+256, ...) into *sumsq. The
-//                       reference adds block sums with a double atomicAdd
-//                       (adam.cu:60), which is not reproducible.
+//                       32..1; the four waves added in order).
+//   adamw_norm_kernel   one workgroup of 1024 threads adds the chunk sums in
+//                       the same kind of fixed order (thread t: chunks t,
+//                       t+1024, ...; butterfly; sixteen waves in order) into
+//                       *sumsq. The reference adds block sums with a double
+//                       atomicAdd (adam.cu:60), which is not reproducible; a
+//                       last-workgroup ticket instead of this second launch
+//                       needs a device-scope fence per workgroup, i.e. an L2
+//                       write-back per chunk (measured 7x slower).
 //   adamw_update_kernel per element, the reference's arithmetic
 //                       (adam.cu:74-85): g = grad*scale,
 //                       m = b1*m + (1-b1)*g, v = b2*v + (1-b2)*g*g,
@@ -47,7 +49,8 @@ __device__ __forceinline__ double xor_lane_f64(double v, int off) {
 }
 
 // Sum over the workgroup in the fixed order: xor butterfly inside each wave,
-// then waves 0..3 added in order. Every thread must call it.
+// then the NW waves added in order. Every thread must call it.
+template <int NW>
 __device__ __forceinline__ double block_sum_f64(double v, double* s_w) {
     v = v + xor_lane_f64(v, 32);
     v = v + xor_lane_f64(v, 16);
@@ -58,17 +61,29 @@ __device__ __forceinline__ double block_sum_f64(double v, double* s_w) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     if (lane == 0) s_w[wave] = v;
     __syncthreads();
-    const double t = ((s_w[0] + s_w[1]) + s_w[2]) + s_w[3];
+    double t = s_w[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t = t + s_w[w];
     __syncthreads();
     return t;
 }
 
 __global__ __launch_bounds__(kThreads) void adamw_sumsq_kernel(AdamwParams p) {
     __shared__ double s_w[4];
-    __shared__ int s_last;
     const AdamwChunk c = p.chunks[blockIdx.x];
     double acc = 0.0;
-    if (c.flags & kAdamwInNorm) {
+    if ((c.flags & kAdamwInNorm) && c.len == kAdamChunk) {
+        // Full chunk: all eight of the thread's groups in flight at once.
+        constexpr int G = kAdamChunk / (4 * kThreads);
+        f32x4 a[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u)
+            a[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(c.grad) + threadIdx.x + u * kThreads);
+#pragma unroll
+        for (int u = 0; u < G; ++u)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc = acc + (double)a[u][t] * (double)a[u][t];
+    } else if (c.flags & kAdamwInNorm) {
         const float* g = c.grad;
         for (int i0 = threadIdx.x * 4; i0 < c.len; i0 += 4 * kThreads * 2) {
             const int i1 = i0 + 4 * kThreads;
@@ -87,22 +102,38 @@ __global__ __launch_bounds__(kThreads) void adamw_sumsq_kernel(AdamwParams p) {
             }
         }
     }
-    const double tot = block_sum_f64(acc, s_w);
-    if (threadIdx.x == 0) {
-        p.partial[blockIdx.x] = tot;
-        __threadfence();
-        s_last = atomicAdd(p.ticket, 1) == (int)gridDim.x - 1;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
+    const double tot = block_sum_f64<4>(acc, s_w);
+    if (threadIdx.x == 0) p.partial[blockIdx.x] = tot;
+}
+
+constexpr int kNormThreads = 1024;
+__global__ __launch_bounds__(kNormThreads) void adamw_norm_kernel(AdamwParams p) {
+    __shared__ double s_w[kNormThreads / 64];
     double s = 0.0;
-    for (int k = threadIdx.x; k < p.nchunks; k += kThreads) s = s + p.partial[k];
-    s = block_sum_f64(s, s_w);
-    if (threadIdx.x == 0) {
-        *p.sumsq = s;
-        *p.ticket = 0;  // re-armed for the next step (this is the last workgroup)
+    for (int k0 = threadIdx.x; k0 < p.nchunks; k0 += 8 * kNormThreads) {
+        double v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int k = k0 + u * kNormThreads;
+            v[u] = k < p.nchunks ? p.partial[k] : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (k0 + u * kNormThreads < p.nchunks) s = s + v[u];
     }
+    s = block_sum_f64<kNormThreads / 64>(s, s_w);
+    if (threadIdx.x == 0) *p.sumsq = s;
+}
+
+// One element of the update (adam.cu:78-84); w, m, v in place.
+__device__ __forceinline__ void adam_elem(float g, float& m, float& v, float& w, float scale,
+                                          const AdamwHyper& h, float ob1, float ob2) {
+    const float gg = g * scale;
+    const float nm = h.b1 * m + ob1 * gg;
+    const float nv = h.b2 * v + ob2 * gg * gg;
+    m = nm;
+    v = nv;
+    w = w - h.lr * ((nm / h.bc1) / (sqrtf(nv / h.bc2) + h.eps) + h.wd * w);
 }
 
 __global__ __launch_bounds__(kThreads) void adamw_update_kernel(AdamwParams p, AdamwHyper h) {
@@ -111,45 +142,59 @@ __global__ __launch_bounds__(kThreads) void adamw_update_kernel(AdamwParams p, A
     const double s = *p.sumsq;
     if (!isfinite(s)) return;
     const float scale = h.clip > 0.f ? fminf(1.f, h.clip / fmaxf((float)sqrt(s), 1e-12f)) : 1.f;
-    const float b1 = h.b1, b2 = h.b2, ob1 = 1.0f - h.b1, ob2 = 1.0f - h.b2;
-    for (int i0 = threadIdx.x * 4; i0 < c.len; i0 += 4 * kThreads) {
-        if (i0 + 4 <= c.len) {
-            f32x4 g = *reinterpret_cast<const f32x4*>(c.grad + i0);
-            f32x4 m = *reinterpret_cast<const f32x4*>(c.m + i0);
-            f32x4 v = *reinterpret_cast<const f32x4*>(c.v + i0);
-            f32x4 w = *reinterpret_cast<const f32x4*>(c.master + i0);
-            float wf[4];
+    const float ob1 = 1.0f - h.b1, ob2 = 1.0f - h.b2;
+    const f32x4* __restrict__ gp = reinterpret_cast<const f32x4*>(c.grad);
+    f32x4* __restrict__ mp = reinterpret_cast<f32x4*>(c.m);
+    f32x4* __restrict__ vp = reinterpret_cast<f32x4*>(c.v);
+    f32x4* __restrict__ wp = reinterpret_cast<f32x4*>(c.master);
+    uint2* __restrict__ op = reinterpret_cast<uint2*>(c.work);
+    const int nvec = c.len / 4;
+    // Two 4-element groups per thread and iteration, all eight loads first.
+    for (int j0 = threadIdx.x; j0 < nvec; j0 += 2 * kThreads) {
+        const int j1 = j0 + kThreads;
+        const bool two = j1 < nvec;
+        f32x4 g[2], m[2], v[2], w[2];
+        g[0] = __builtin_nontemporal_load(gp + j0);
+        m[0] = mp[j0];
+        v[0] = vp[j0];
+        w[0] = wp[j0];
+        if (two) {
+            g[1] = __builtin_nontemporal_load(gp + j1);
+            m[1] = mp[j1];
+            v[1] = vp[j1];
+            w[1] = wp[j1];
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            if (u == 1 && !two) break;
+            const int j = u == 0 ? j0 : j1;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const float gg = g[t] * scale;
-                const float nm = b1 * m[t] + ob1 * gg;
-                const float nv = b2 * v[t] + ob2 * gg * gg;
-                m[t] = nm;
-                v[t] = nv;
-                w[t] = w[t] - h.lr * ((nm / h.bc1) / (sqrtf(nv / h.bc2) + h.eps) + h.wd * w[t]);
-                wf[t] = w[t];
+                float mm = m[u][t], vv = v[u][t], ww = w[u][t];
+                adam_elem(g[u][t], mm, vv, ww, scale, h, ob1, ob2);
+                m[u][t] = mm;
+                v[u][t] = vv;
+                w[u][t] = ww;
             }
-            *reinterpret_cast<f32x4*>(c.m + i0) = m;
-            *reinterpret_cast<f32x4*>(c.v + i0) = v;
-            *reinterpret_cast<f32x4*>(c.master + i0) = w;
-            if (c.work) {
+            mp[j] = m[u];
+            vp[j] = v[u];
+            wp[j] = w[u];
+            if (op) {
                 uint2 o;
-                o.x = pack_bf2(wf[0], wf[1]);
-                o.y = pack_bf2(wf[2], wf[3]);
-                *reinterpret_cast<uint2*>(c.work + i0) = o;
-            }
-        } else {
-            for (int i = i0; i < c.len; ++i) {
-                const float gg = c.grad[i] * scale;
-                const float nm = b1 * c.m[i] + ob1 * gg;
-                const float nv = b2 * c.v[i] + ob2 * gg * gg;
-                c.m[i] = nm;
-                c.v[i] = nv;
-                const float w = c.master[i] - h.lr * ((nm / h.bc1) / (sqrtf(nv / h.bc2) + h.eps) + h.wd * c.master[i]);
-                c.master[i] = w;
-                if (c.work) c.work[i] = f2bf(w);
+                o.x = pack_bf2(w[u][0], w[u][1]);
+                o.y = pack_bf2(w[u][2], w[u][3]);
+                op[j] = o;
             }
         }
+    }
+    // Tail of a parameter whose size is not a multiple of 4.
+    for (int i = nvec * 4 + threadIdx.x; i < c.len; i += kThreads) {
+        float mm = c.m[i], vv = c.v[i], ww = c.master[i];
+        adam_elem(c.grad[i], mm, vv, ww, scale, h, ob1, ob2);
+        c.m[i] = mm;
+        c.v[i] = vv;
+        c.master[i] = ww;
+        if (c.work) c.work[i] = f2bf(ww);
     }
 }
 
@@ -167,6 +212,7 @@ __global__ __launch_bounds__(kThreads) void adamw_zero_kernel(AdamwParams p) {
 hipError_t launch_adamw_sumsq(const AdamwParams& p, hipStream_t s) {
     if (p.nchunks <= 0) return hipSuccess;
     adamw_sumsq_kernel<<<p.nchunks, kThreads, 0, s>>>(p);
+    adamw_norm_kernel<<<1, kNormThreads, 0, s>>>(p);
     return hipGetLastError();
 }
 

@@ -809,7 +809,7 @@ int tmt_moe_read_norm(tmt_moe* m, void* stream, uint16_t* H, float* mean, float*
 
 struct tmt_moe_adamw {
     int device = 0;
-    char* arena = nullptr;  // chunk table, per-chunk sums, sumsq, ticket
+    char* arena = nullptr;  // chunk table, per-chunk sums, sumsq
     AdamwParams p{};
 };
 
@@ -853,8 +853,7 @@ int tmt_moe_adamw_create(const tmt_moe_adamw_param* params, int32_t count, tmt_m
     hipError_t err = hipGetDevice(&o->device);
     const size_t nch = chunks.size();
     Layout L;
-    const size_t o_tab = L.add(nch * sizeof(AdamwChunk)), o_part = L.add(nch * 8), o_sum = L.add(8),
-                 o_tick = L.add(4);
+    const size_t o_tab = L.add(nch * sizeof(AdamwChunk)), o_part = L.add(nch * 8), o_sum = L.add(8);
     if (err == hipSuccess) err = hipMalloc(&o->arena, L.total);
     if (err != hipSuccess) {
         delete o;
@@ -865,10 +864,8 @@ int tmt_moe_adamw_create(const tmt_moe_adamw_param* params, int32_t count, tmt_m
     o->p.nchunks = (int)nch;
     o->p.partial = reinterpret_cast<double*>(o->arena + o_part);
     o->p.sumsq = reinterpret_cast<double*>(o->arena + o_sum);
-    o->p.ticket = reinterpret_cast<int*>(o->arena + o_tick);
     if (nch) err = hipMemcpy(o->arena + o_tab, chunks.data(), nch * sizeof(AdamwChunk), hipMemcpyHostToDevice);
     if (err == hipSuccess) err = hipMemset(o->arena + o_sum, 0, sizeof(double));
-    if (err == hipSuccess) err = hipMemset(o->arena + o_tick, 0, sizeof(int));  // last-workgroup ticket
     if (err == hipSuccess) err = hipStreamSynchronize(nullptr);
     if (err != hipSuccess) {
         (void)hipFree(o->arena);

@@ -218,8 +218,7 @@ struct AdamwParams {
     const AdamwChunk* chunks;         // [nchunks]
     int nchunks;
     double* partial;                  // [nchunks] per-chunk sums of grad^2
-    double* sumsq;                    // global sum of grad^2 (written by the last workgroup)
-    int* ticket;                      // zero between launches
+    double* sumsq;                    // global sum of grad^2
 };
 struct AdamwHyper {
     float clip, lr, b1, b2, eps, wd, bc1, bc2;

@@ -86,20 +86,24 @@ def numpy_canonical_sumsq(ps, waves_reversed=False):
     """Independent restatement of the GPU kernels' order: 8192-element
     chunks; thread t of 256 accumulates its 4-element groups t, t+256, ...
     in ascending element order; xor butterfly 32..1 per wave; waves added in
-    order; then the chunk sums by the same scheme. waves_reversed plants a
-    plausible mistake (the four wave sums added from the last)."""
+    order; then the chunk sums by the same scheme on 1024 threads (sixteen
+    waves). waves_reversed plants a plausible mistake (the wave sums added
+    from the last)."""
     lanes = np.arange(64)
 
     def block(t):
         w = []
-        for wave in range(4):
+        for wave in range(t.size // 64):
             l = t[wave * 64:(wave + 1) * 64].copy()
             for off in (32, 16, 8, 4, 2, 1):
                 l = l + l[lanes ^ off]
             w.append(l[0])
         if waves_reversed:
-            return ((w[3] + w[2]) + w[1]) + w[0]
-        return ((w[0] + w[1]) + w[2]) + w[3]
+            w = w[::-1]
+        tot = w[0]
+        for x in w[1:]:
+            tot = tot + x
+        return tot
 
     parts = []
     for q in ps:
@@ -118,9 +122,9 @@ def numpy_canonical_sumsq(ps, waves_reversed=False):
                     acc = np.where(ok, acc + np.where(ok, c[np.minimum(idx, c.size - 1)], 0.0) ** 2, acc)
             parts.append(block(acc))
     parts = np.array(parts)
-    t = np.zeros(256)
-    for k0 in range(0, parts.size, 256):
-        chunk = parts[k0:k0 + 256]
+    t = np.zeros(1024)  # the final sum runs on one workgroup of 1024 threads
+    for k0 in range(0, parts.size, 1024):
+        chunk = parts[k0:k0 + 1024]
         t[:chunk.size] = t[:chunk.size] + chunk
     return block(t)
 
