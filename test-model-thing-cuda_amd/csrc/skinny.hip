@@ -5,18 +5,19 @@
 // cuBLAS calls, tmt-cuda/src/moe.cu:414-436, tmt-cuda/src/generate.h:19-44).
 // The 256 x 256 tiles of gemm.hip would leave most CUs idle and read each
 // weight tile through a deep LDS pipeline for one useful row. Here a
-// workgroup owns 16 output columns of one expert and all of its rows:
-//   * the 4 waves split the reduction (K) into contiguous quarters;
-//   * each lane streams one weight row (output column) straight from HBM
-//     into registers, 128 contiguous bytes per 256-element chunk, and the
-//     matching activation row of each 16-row block (rows past the expert's
-//     count are zero and not loaded);
+// workgroup owns one or two tiles of 16 output columns of one expert and all
+// of its rows:
+//   * the waves split the reduction (K) into contiguous chunks;
+//   * each lane streams weight rows (output columns) straight from HBM into
+//     registers, and the matching activation row of each 16-row block (rows
+//     past the expert's count are zero and not loaded);
 //   * v_mfma_f32_16x16x32_bf16 multiplies them. A and B use the same
-//     lane/k assignment (lane group g holds k = base + 64g + 8i .. +7 for
-//     MFMA i), which is a permutation of the reduction, so the product is
-//     the plain dot product;
+//     lane/k assignment, which is a permutation of the reduction, so the
+//     product is the plain dot product;
 //   * the wave partials are summed in LDS in a fixed order and written with
 //     the same epilogue semantics as gemm.hip (U, SiLU(U) from the fp32 sum).
+// skinny_chunk_kernel is the main path; skinny_gemm_kernel covers reduction
+// lengths that do not split into one chunk per wave.
 // Experts are visited in descending-count order (the scan's LPT order), so
 // the grid only spans min(E, T*K) expert ranks.
 #include "device_util.hpp"
@@ -133,37 +134,50 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(GemmParams p, int
     }
 }
 
+// Output column tiles of 16 per workgroup in the chunk kernel (CT): with
+// two, both tiles' weight loads are in flight together and each activation
+// chunk is loaded once for both (measured with d = 1024, h = 4096, E = 16,
+// top-4: T = 64 UP 40.6 -> 30.6 us, DOWN 42.0 -> 31.1 us, T = 8 about 10%
+// faster; four tiles are slower again). Below kSkinnyTwoTileTokens tokens
+// the step is latency-bound and the larger grid of one tile wins (T = 1:
+// 29.6 us per step with one tile, 34.0 with two).
+constexpr int kSkinnyTwoTileTokens = 4;
+
 // Variant for reduction lengths K = NW * 32J (J = 8: K a multiple of 256
 // up to 4096; J = 2: a multiple of 64 up to 1024): the workgroup has NW
 // waves and wave w owns one K-chunk, [32Jw, 32J(w+1)); lane group g holds
-// k = 32Jw + 8Jg + 8i .. +7 for MFMA i. Every weight load of the tile is
+// k = 32Jw + 32i + 8g .. +7 for MFMA i, so the four lane groups of one load
+// instruction read 64 contiguous bytes of each of the 16 rows (16 cache
+// lines per instruction instead of 64: the address unit, not HBM, bounded
+// the first layout). Every weight load of the tile is
 // issued at once (J per lane), then each 16-row block of the expert loads
 // its activation chunk and multiplies; blocks past the expert's count are
 // skipped as a whole (uniform branch). No load sits under a divergent
 // branch, so the compiler's wait counts stay exact.
-template <int KIND, bool DUAL, int J, int RB>
+template <int KIND, bool DUAL, int J, int RB, int CT>
 __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int nexp) {
     static_assert(KIND == GEMM_UP || KIND == GEMM_DOWN, "forward GEMMs only");
     constexpr bool kGather = KIND == GEMM_UP;
-    extern __shared__ f32x4 red[];  // [RB][nw][64] wave partials
+    extern __shared__ f32x4 red[];  // [RB][CT][nw][64] wave partials
 
     const int nw = (int)blockDim.x >> 6;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rank = (int)blockIdx.x % nexp, tile = (int)blockIdx.x / nexp;
+    const int rank = (int)blockIdx.x % nexp, tile0 = ((int)blockIdx.x / nexp) * CT;
     const int e = p.order[rank];
     const int row0 = p.offsets[e];
     const int rows = min(p.offsets[e + 1] - row0, 16 * RB);
     if (rows <= 0) return;
     const int nrb = (rows + 15) >> 4;
     const int g = lane >> 4, li = lane & 15;
-    const int kw = wave * (32 * J) + g * (8 * J);
+    const int kw = wave * (32 * J) + g * 8;
 
-    uint4 wv[J];
-    {
-        const uint16_t* src = p.w[e] + (int64_t)(tile * 16 + li) * p.ldb + kw;
+    uint4 wv[CT][J];
 #pragma unroll
-        for (int i = 0; i < J; ++i) wv[i] = ld16(src + 8 * i);
+    for (int c = 0; c < CT; ++c) {
+        const uint16_t* src = p.w[e] + (int64_t)((tile0 + c) * 16 + li) * p.ldb + kw;
+#pragma unroll
+        for (int i = 0; i < J; ++i) wv[c][i] = ld16(src + 32 * i);
     }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -175,29 +189,33 @@ __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int ne
         const uint16_t* ar = p.a + (int64_t)srow * p.lda + kw;
         uint4 av[J];
 #pragma unroll
-        for (int i = 0; i < J; ++i) av[i] = ld16(ar + 8 * i);
+        for (int i = 0; i < J; ++i) av[i] = ld16(ar + 32 * i);
         if (!ok) {
 #pragma unroll
             for (int i = 0; i < J; ++i) av[i] = make_uint4(0, 0, 0, 0);
         }
-        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < J; ++i) acc = mfma16(wv[i], av[i], acc);
-        red[(rb * nw + wave) * 64 + lane] = acc;
+        for (int c = 0; c < CT; ++c) {
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < J; ++i) acc = mfma16(wv[c][i], av[i], acc);
+            red[((rb * CT + c) * nw + wave) * 64 + lane] = acc;
+        }
     }
     __syncthreads();
 
-    // Output (m, n) of a row block = lane (n/4)*16 + m, element n%4; the wave
-    // partials are added in wave order.
+    // Output (m, n) of a row block and column tile = lane (n/4)*16 + m,
+    // element n%4; the wave partials are added in wave order.
     uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
-    for (int o = tid; o < nrb * 256; o += (int)blockDim.x) {
-        const int rb = o >> 8, m = (o >> 4) & 15, n = o & 15;
+    for (int o = tid; o < nrb * CT * 256; o += (int)blockDim.x) {
+        const int rbc = o >> 8, m = (o >> 4) & 15, n = o & 15;
+        const int rb = rbc / CT, c = rbc % CT;
         const int row = rb * 16 + m;
         if (row >= rows) continue;
         const int sl = (n >> 2) * 16 + m, r = n & 3;
-        float v = red[(rb * nw) * 64 + sl][r];
-        for (int w2 = 1; w2 < nw; ++w2) v += red[(rb * nw + w2) * 64 + sl][r];
-        const int64_t off = (int64_t)(row0 + row) * p.ldc + tile * 16 + n;
+        float v = red[(rbc * nw) * 64 + sl][r];
+        for (int w2 = 1; w2 < nw; ++w2) v += red[(rbc * nw + w2) * 64 + sl][r];
+        const int64_t off = (int64_t)(row0 + row) * p.ldc + (tile0 + c) * 16 + n;
         C[off] = f2bf(v);
         if constexpr (DUAL) p.c2[off] = f2bf(silu_fast(v));
     }
@@ -214,23 +232,26 @@ hipError_t launch_rb(int rb, const GemmParams& p, int nexp, unsigned grid, hipSt
     return hipGetLastError();
 }
 
-template <int KIND, bool DUAL, int J>
+template <int KIND, bool DUAL, int J, int CT>
 hipError_t launch_chunk_rb(int rb, int nw, const GemmParams& p, int nexp, hipStream_t s) {
-    const unsigned grid = (unsigned)(p.N / 16) * (unsigned)nexp;
+    const unsigned grid = (unsigned)(p.N / (16 * CT)) * (unsigned)nexp;
     const dim3 block(64 * nw);
-    const size_t lds = (size_t)rb * nw * 64 * sizeof(f32x4);
+    const size_t lds = (size_t)rb * CT * nw * 64 * sizeof(f32x4);
     switch (rb) {
-        case 1: skinny_chunk_kernel<KIND, DUAL, J, 1><<<grid, block, lds, s>>>(p, nexp); break;
-        case 2: skinny_chunk_kernel<KIND, DUAL, J, 2><<<grid, block, lds, s>>>(p, nexp); break;
-        case 4: skinny_chunk_kernel<KIND, DUAL, J, 4><<<grid, block, lds, s>>>(p, nexp); break;
+        case 1: skinny_chunk_kernel<KIND, DUAL, J, 1, CT><<<grid, block, lds, s>>>(p, nexp); break;
+        case 2: skinny_chunk_kernel<KIND, DUAL, J, 2, CT><<<grid, block, lds, s>>>(p, nexp); break;
+        case 4: skinny_chunk_kernel<KIND, DUAL, J, 4, CT><<<grid, block, lds, s>>>(p, nexp); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 template <int KIND, bool DUAL>
-hipError_t launch_chunk(int J, int rb, int nw, const GemmParams& p, int nexp, hipStream_t s) {
-    return J == 8 ? launch_chunk_rb<KIND, DUAL, 8>(rb, nw, p, nexp, s)
-                  : launch_chunk_rb<KIND, DUAL, 2>(rb, nw, p, nexp, s);
+hipError_t launch_chunk(int J, int ct, int rb, int nw, const GemmParams& p, int nexp, hipStream_t s) {
+    if (ct == 2)
+        return J == 8 ? launch_chunk_rb<KIND, DUAL, 8, 2>(rb, nw, p, nexp, s)
+                      : launch_chunk_rb<KIND, DUAL, 2, 2>(rb, nw, p, nexp, s);
+    return J == 8 ? launch_chunk_rb<KIND, DUAL, 8, 1>(rb, nw, p, nexp, s)
+                  : launch_chunk_rb<KIND, DUAL, 2, 1>(rb, nw, p, nexp, s);
 }
 
 }  // namespace
@@ -251,10 +272,11 @@ hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int
     }
     const int rb = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
     if (J > 0) {
+        const int ct = (T >= kSkinnyTwoTileTokens && p.N % 32 == 0) ? 2 : 1;
         if (kind == GEMM_UP)
-            return dual ? launch_chunk<GEMM_UP, true>(J, rb, nw, p, nexp, s)
-                        : launch_chunk<GEMM_UP, false>(J, rb, nw, p, nexp, s);
-        return launch_chunk<GEMM_DOWN, false>(J, rb, nw, p, nexp, s);
+            return dual ? launch_chunk<GEMM_UP, true>(J, ct, rb, nw, p, nexp, s)
+                        : launch_chunk<GEMM_UP, false>(J, ct, rb, nw, p, nexp, s);
+        return launch_chunk<GEMM_DOWN, false>(J, ct, rb, nw, p, nexp, s);
     }
     // General reduction lengths: K split over 4 waves in 64-element units.
     const unsigned grid = (unsigned)(p.N / 16) * (unsigned)nexp;
