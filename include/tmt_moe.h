@@ -110,7 +110,8 @@ int tmt_moe_forward_mxfp4(tmt_moe* moe, void* stream, int32_t T,
  * (aux_coef / z_coef already divided by the layer count, model.cu:677).
  * X is the forward input (the reference keeps a copy in MoeKeep::H,
  * moe.cu:396; here the caller passes it again). Outputs are overwritten:
- *   dX [T][d] bf16, dWr [E][d] fp32 (may be NULL when E == 1),
+ *   dX [T][d] bf16, dWr [E][d] fp32 (may be NULL when E == 1; when E == 1
+ *   and non-NULL, its d floats are zeroed, as moe.cu:486-487 does),
  *   dW_up[E] -> [h][d] fp32 (or [d][d] when hidden == 0),
  *   dW_down[E] -> [d][h] fp32 (hidden > 0).
  * Experts that received no tokens get all-zero gradients (the reference

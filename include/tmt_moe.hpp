@@ -14,6 +14,8 @@
  *   moe_aux_from                        moe.cu:468-475
  *   moe_backward                        moe.cu:477-545
  *   layernorm_fwd / layernorm_bwd       norm.cu:96-106
+ *   moe_expert_counts                   capi.cu:131-136 (tmt_model_expert_counts)
+ *   moe_router_balance                  train_main.cu:232-248 (router balance log)
  *
  * Behaviour kept from the reference:
  *   - experts are single d x d linears with SiLU inside combine (hidden = 0);
@@ -115,10 +117,9 @@ inline void backward(const uint16_t* dY, const uint16_t* const* Wup, const uint1
                      uint16_t* dX, MoeKeep& k, float aux, float zcoef) {
     const char* where = "moe_backward";
     if (!k.handle) die(where, "moe_keep_alloc was not called");
-    if (k.E == 1 && dWr)  // the reference zeroes the unused router gradient too (moe.cu:487)
-        check_hip(hipMemsetAsync(dWr, 0, (size_t)k.D * 4, k.stream), where);
-    check(tmt_moe_backward(k.handle, k.stream, dY, k.H, Wr, Wup, Wdown, aux, zcoef, dX,
-                           k.E > 1 ? dWr : nullptr, dWup, dWdown), where);
+    // With E == 1 the library zeroes dWr, as the reference does (moe.cu:487).
+    check(tmt_moe_backward(k.handle, k.stream, dY, k.H, Wr, Wup, Wdown, aux, zcoef, dX, dWr, dWup,
+                           dWdown), where);
 }
 }  // namespace tmt_moe_detail
 
@@ -242,4 +243,35 @@ inline void moe_backward(const B* dY, B** W_up, B** W_down, const B* Wrouter, fl
     using namespace tmt_moe_detail;
     backward(bits(dY), table(W_up), table(W_down), bits(Wrouter), dWrouter, dW_up, dW_down,
              bits(dX), k, aux, zcoef);
+}
+
+/* capi.cu:131-136 (tmt_model_expert_counts): the token count of every expert
+ * of every layer in the last forward, out[l * E + e], from each layer's
+ * MoeKeep::hcnt (filled when that layer's statistics were read). */
+inline void moe_expert_counts(const MoeKeep* layers, int L, int64_t* out) {
+    for (int l = 0; l < L; ++l)
+        for (int e = 0; e < layers[l].E; ++e) out[(int64_t)l * layers[l].E + e] = layers[l].hcnt[e];
+}
+
+/* train_main.cu:232-248: the router-balance line over token counts `use`
+ * [L][E] accumulated across steps. Each (layer, expert) pair's share is
+ * use / total * L * E (1.0 = uniform); min starts at 1 and max at 0, as in
+ * the reference, and a pair with share < 0.01 counts as dead. */
+struct MoeBalance {
+    double min = 1, max = 0;
+    long dead = 0;
+    int pairs = 0;
+};
+inline MoeBalance moe_router_balance(const int64_t* use, int L, int E) {
+    MoeBalance b;
+    b.pairs = L * E;
+    long double tot = 0;
+    for (int i = 0; i < L * E; ++i) tot += (long double)use[i];
+    for (int i = 0; i < L * E; ++i) {
+        const double s = tot > 0 ? (double)((long double)use[i] / tot * L * E) : 0.0;
+        if (s < b.min) b.min = s;
+        if (s > b.max) b.max = s;
+        if (s < 0.01) ++b.dead;
+    }
+    return b;
 }

@@ -374,6 +374,7 @@ int check_backward(tmt_moe* m, const uint16_t* dY, const uint16_t* X, const uint
         return fail(TMT_MOE_EINVAL, "dY, X and dX must be 16-byte aligned");
     if (E > 1 && (!Wr || !dWr || !aligned16(Wr) || !aligned16(dWr)))
         return fail(TMT_MOE_EINVAL, "Wr and dWr must be 16-byte aligned pointers when experts > 1");
+    if (!aligned16(dWr)) return fail(TMT_MOE_EINVAL, "dWr must be 16-byte aligned");
     int rc = check_ptrs((const void* const*)W_up, E, "W_up");
     if (rc) return rc;
     if ((rc = check_ptrs((const void* const*)dW_up, E, "dW_up"))) return rc;
@@ -444,6 +445,11 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
         for (int e = 0; e < E; ++e) dx.w[e] = W_up[e];
         dx.ldb = d;
         LAUNCH(TMT_MOE_PH_GEMM_DX, launch_gemm(GEMM_DX, false, dx, s));
+    }
+    if (E == 1 && dWr) {
+        // The dense path has no router; its gradient slot is zeroed like the
+        // reference's (moe.cu:486-487).
+        LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_zero_f32(dWr, d, s));
     }
     if (E > 1) {
         // With T == 0 the partial pass sums no rows and writes zeros.

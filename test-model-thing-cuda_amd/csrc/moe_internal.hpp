@@ -175,6 +175,9 @@ constexpr int kScatterRows = 64;  // rows per scatter workgroup (router or Layer
 int scatter_blocks(int T);
 hipError_t launch_scatter(const ScatterParams& p, hipStream_t s);
 
+// p[0, n) = 0 with a kernel (no memset node, so the call can be captured).
+hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t s);
+
 // ------------------------------------------------------------------ norm --
 struct LayerNormParams {
     const uint16_t* S;       // [T][d] bf16 LayerNorm input

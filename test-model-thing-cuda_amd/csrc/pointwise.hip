@@ -12,6 +12,8 @@
 //                and the router input gradient moe.cu:522-531, fused)
 // Rows are processed by one 64-lane wave with 16-byte vectors; every sum runs
 // in a fixed order, so results are run-to-run deterministic.
+#include <algorithm>
+
 #include "device_util.hpp"
 #include "moe_internal.hpp"
 
@@ -469,6 +471,20 @@ hipError_t launch_scatter_ni(const ScatterParams& p, int ni, int rows, size_t ld
         case 4: scatter_kernel<ROUTER, 4><<<grid, kThreads, lds, s>>>(p, rows); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+namespace {
+__global__ __launch_bounds__(kThreads) void zero_f32_kernel(float* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+        p[i] = 0.0f;
+}
+}  // namespace
+
+hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + kThreads - 1) / kThreads, 1024);
+    zero_f32_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(p, n);
     return hipGetLastError();
 }
 

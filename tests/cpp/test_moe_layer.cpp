@@ -7,6 +7,8 @@
 //   test_moe_backward  tmt-cuda/src/architecture_test.cu:228-264
 //   experts limit      tmt-cuda/tests/cli.sh:30-32 (the limit here is 64)
 //   test_layernorm     layernorm_fwd / layernorm_bwd (norm.cu:96-106) against fp64
+//   test_model_flow    the model's multi-layer use: model.cu:252-258, 512-514,
+//                      542-549, 672-677; capi.cu:131-136; train_main.cu:232-248
 //
 // Usage: test_moe_layer            all GPU tests
 //        test_moe_layer reject     only the configuration check (no GPU use)
@@ -274,6 +276,100 @@ static void test_deferred_stats() {
     std::puts("PASS deferred router statistics equal the immediate read");
 }
 
+// The recurrent model's use of the layer (model.cu:252-258, 512-514,
+// 542-549, 672-677; capi.cu:131-136; train_main.cu:232-248): three layers
+// with E = 32 (above the reference's old limit of 16), one shared MoeWs,
+// residual add through beta = 1, statistics deferred into per-layer slots
+// with a stride of 17 floats and read with one copy, expert counts, the
+// router balance line, and the backward in reverse layer order with the
+// coefficients divided by L.
+static void test_model_flow() {
+    constexpr int L = 3, N = 96, E = 32, K = 4, D = 64;
+    const float aux_c = 0.1f, z_c = 1e-3f;
+    std::mt19937 g(11);
+    Device dev;
+    MoeWs ws;
+    moe_ws_alloc(ws, N, E, K, D);
+    std::vector<MoeKeep> layers(L), immediate(L);
+    std::vector<uint16_t*> Wr(L);
+    std::vector<std::vector<uint16_t*>> Wx(L, std::vector<uint16_t*>(E));
+    std::vector<std::vector<float*>> dWx(L, std::vector<float*>(E));
+    std::vector<float*> dWr(L);
+    float* stats = dev.alloc<float>((size_t)L * 17);
+    for (int l = 0; l < L; ++l) {
+        Wr[l] = dev.upload(normal_bf16(g, (size_t)E * D, 0.2f));
+        for (int e = 0; e < E; ++e) {
+            Wx[l][e] = dev.upload(uniform_bf16(g, (size_t)D * D, std::sqrt(1.f / D)));
+            dWx[l][e] = dev.alloc<float>((size_t)D * D);
+        }
+        dWr[l] = dev.alloc<float>((size_t)E * D);
+        moe_keep_alloc(layers[l], N, E, K, D);
+        moe_keep_alloc(immediate[l], N, E, K, D);
+        layers[l].stat = stats + (size_t)l * 17;
+    }
+    // forward: X_{l+1} = X_l + MoE_l(X_l)
+    std::vector<uint16_t*> X(L + 1);
+    X[0] = dev.upload(normal_bf16(g, (size_t)N * D, 1.f));
+    for (int l = 0; l < L; ++l) {
+        X[l + 1] = dev.alloc<uint16_t>((size_t)N * D);
+        tmt_moe_detail::check_hip(hipMemcpy(X[l + 1], X[l], (size_t)N * D * 2, hipMemcpyDeviceToDevice), "copy");
+        const float r = moe_forward(X[l], Wr[l], Wx[l].data(), X[l + 1], layers[l], ws, N, E, K, D, 1.0f);
+        require(r == 0.f, "deferred moe_forward returns 0");
+    }
+    auto hs = download(stats, (size_t)L * 17);  // the one host read of the step
+    float aux_acc = 0, z_acc = 0;
+    for (int l = 0; l < L; ++l) {
+        aux_acc += moe_aux_from(layers[l], &hs[(size_t)l * 17]);
+        z_acc += layers[l].zloss;
+        // the same layer read immediately gives the same statistics
+        uint16_t* Yi = dev.alloc<uint16_t>((size_t)N * D);
+        const float ai = moe_forward(X[l], Wr[l], Wx[l].data(), Yi, immediate[l], ws, N, E, K, D, 0.f);
+        require(ai == hs[(size_t)l * 17] && immediate[l].zloss == layers[l].zloss,
+                "deferred statistics differ from the immediate read");
+    }
+    require(std::isfinite(aux_acc) && std::isfinite(z_acc) && aux_acc > 0.f, "accumulated aux / z");
+    // expert counts (tmt_model_expert_counts) and the router balance line
+    std::vector<int64_t> counts((size_t)L * E);
+    moe_expert_counts(layers.data(), L, counts.data());
+    int zeros = 0;
+    for (int l = 0; l < L; ++l) {
+        int64_t tot = 0;
+        for (int e = 0; e < E; ++e) {
+            tot += counts[(size_t)l * E + e];
+            zeros += counts[(size_t)l * E + e] == 0;
+        }
+        require(tot == (int64_t)N * K, "expert counts of a layer do not sum to N*K");
+    }
+    const MoeBalance b = moe_router_balance(counts.data(), L, E);
+    require(b.pairs == L * E && b.min <= 1.0 && b.max >= 1.0, "balance shares around 1");
+    require(b.dead == zeros, "dead experts are the ones with no tokens (mean count 12, threshold 0.12)");
+    std::vector<int64_t> flat((size_t)L * E, 5);
+    MoeBalance u = moe_router_balance(flat.data(), L, E);
+    require(u.min == 1.0 && u.max == 1.0 && u.dead == 0, "uniform counts give shares of exactly 1");
+    flat[7] = 0;
+    u = moe_router_balance(flat.data(), L, E);
+    require(u.min == 0.0 && u.dead == 1, "a silent expert is dead");
+    // backward, last layer first, coefficients / L
+    uint16_t* dY = dev.upload(normal_bf16(g, (size_t)N * D, 1.f));
+    uint16_t* dXl = dev.alloc<uint16_t>((size_t)N * D);
+    for (int l = L - 1; l >= 0; --l) {
+        moe_backward(dY, Wx[l].data(), Wr[l], dWr[l], dWx[l].data(), dXl, layers[l], ws, aux_c / L, z_c / L);
+        auto gx = to_f32(download(dXl, (size_t)N * D));
+        auto gr = download(dWr[l], (size_t)E * D);
+        for (float v : gx) require(std::isfinite(v), "dX finite");
+        double nr = 0;
+        for (float v : gr) nr += (double)v * v;
+        require(nr > 0 && std::isfinite(nr), "router gradient written");
+    }
+    for (int l = 0; l < L; ++l) {
+        moe_keep_free(layers[l]);
+        moe_keep_free(immediate[l]);
+    }
+    moe_ws_free(ws);
+    std::printf("PASS model flow: %d layers, E=%d, deferred statistics, counts, balance min %.3f max %.3f dead %ld/%d\n",
+                L, E, b.min, b.max, b.dead, b.pairs);
+}
+
 // layernorm_fwd / layernorm_bwd (norm.cu:96-106) against an fp64 host
 // LayerNorm on the same bf16 inputs, and the fused moe path's input side:
 // rows with offsets and scales, ragged D.
@@ -352,6 +448,7 @@ int main(int argc, char** argv) {
     test_moe_backward();
     test_deferred_stats();
     test_layernorm();
+    test_model_flow();
     std::puts("ALL PASS");
     return 0;
 }
