@@ -280,6 +280,12 @@ int tmt_moe_adamw_zero_grads(tmt_moe_adamw* opt, void* stream);
 /* Number of chunks (workgroups per launch) of an optimizer. */
 int tmt_moe_adamw_chunks(tmt_moe_adamw* opt, int32_t* chunks);
 
+/* out[i] = bf16(in[i]) (round to nearest even) for n fp32 values: the bf16
+ * work copy of fp32 master weights, replacing copy_bf16_kernel
+ * (tmt-cuda/src/model.cu:54; used after initialisation and loads,
+ * model.cu:219, checkpoint.h:149). */
+int tmt_moe_f32_to_bf16(void* stream, const float* in, uint16_t* out, int64_t n);
+
 /* Thread-local message of the last failing call on this thread. */
 const char* tmt_moe_last_error(void);
 

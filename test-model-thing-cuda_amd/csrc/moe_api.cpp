@@ -796,6 +796,13 @@ int tmt_moe_layernorm_backward(void* stream, int32_t T, int32_t d, const uint16_
     return TMT_MOE_OK;
 }
 
+int tmt_moe_f32_to_bf16(void* stream, const float* in, uint16_t* out, int64_t n) {
+    if (n < 0) return fail(TMT_MOE_EINVAL, "n=%lld < 0", (long long)n);
+    if (n > 0 && (!in || !out)) return fail(TMT_MOE_EINVAL, "in and out must be non-NULL");
+    HIP_TRY(launch_f32_to_bf16(in, out, n, (hipStream_t)stream));
+    return TMT_MOE_OK;
+}
+
 int tmt_moe_read_norm(tmt_moe* m, void* stream, uint16_t* H, float* mean, float* rstd) {
     if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
     if (m->last_T < 0 || !m->last_ln) return fail(TMT_MOE_ESTATE, "the last forward was not tmt_moe_forward_ln");

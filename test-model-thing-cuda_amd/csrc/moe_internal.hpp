@@ -177,6 +177,8 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s);
 
 // p[0, n) = 0 with a kernel (no memset node, so the call can be captured).
 hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t s);
+// out = bf16(in), round to nearest even.
+hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t s);
 
 // ------------------------------------------------------------------ norm --
 struct LayerNormParams {

@@ -481,6 +481,20 @@ __global__ __launch_bounds__(kThreads) void zero_f32_kernel(float* p, int64_t n)
 }
 }  // namespace
 
+namespace {
+__global__ __launch_bounds__(kThreads) void f32_to_bf16_kernel(const float* in, uint16_t* out, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads)
+        out[i] = f2bf(in[i]);
+}
+}  // namespace
+
+hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    const int64_t blocks = std::min<int64_t>((n + kThreads - 1) / kThreads, 4096);
+    f32_to_bf16_kernel<<<(unsigned)blocks, kThreads, 0, s>>>(in, out, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     const int64_t blocks = std::min<int64_t>((n + kThreads - 1) / kThreads, 1024);

@@ -46,6 +46,7 @@ EXPORTED = (
     "tmt_moe_adamw_read_sumsq",
     "tmt_moe_adamw_zero_grads",
     "tmt_moe_adamw_chunks",
+    "tmt_moe_f32_to_bf16",
     "tmt_moe_set_profiling",
     "tmt_moe_read_profile",
     "tmt_moe_phase_name",
@@ -101,6 +102,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.tmt_moe_adamw_read_sumsq.argtypes = [vp, vp, ctypes.POINTER(ctypes.c_double)]
     lib.tmt_moe_adamw_zero_grads.argtypes = [vp, vp]
     lib.tmt_moe_adamw_chunks.argtypes = [vp, ctypes.POINTER(i32)]
+    lib.tmt_moe_f32_to_bf16.argtypes = [vp, vp, vp, ctypes.c_int64]
     lib.tmt_moe_read_stats.argtypes = [vp, vp, vp, vp, vp]
     lib.tmt_moe_stats_device_ptr.argtypes = [vp, pp]
     lib.tmt_moe_read_routing.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
