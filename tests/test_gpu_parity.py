@@ -151,6 +151,8 @@ def test_c1_backward_against_oracle(orc):
     (500, 1024, 32, 4, 256),   # the c5 router shape
     (129, 128, 3, 3, 128),     # E == K, odd expert count
     (333, 192, 5, 2, 320),     # d and h not multiples of the 256-wide GEMM tile
+    (6, 256, 8, 2, 512),       # decode-sized: fused down+combine, then the backward reads O
+    (8, 1024, 16, 4, 4096),    # c3 weights at T = 8 (fused), forward + backward
 ])
 def test_shapes_against_oracle(orc, T, d, E, K, h):
     say(f"shape T={T} d={d} E={E} K={K} h={h} fwd+bwd")
@@ -278,6 +280,9 @@ def test_decode_steps_against_oracle(orc, T):
     (65, 192, 5, 2, 320),    # first token count on the tiled path
     (9, 128, 4, 2, 1088),    # down-projection K of 17 x 64: one tile per workgroup
     (33, 256, 8, 2, 2048),   # three 16-row blocks, 8 waves of 256-element chunks
+    (2, 128, 64, 8, 256),    # fused down+combine: 16 experts of one chunk, one unit per wave
+    (7, 320, 6, 3, 768),     # fused: 20 column tiles, a wave's units span two experts
+    (1, 64, 2, 1, 256),      # fused: a single token and expert
 ])
 def test_decode_shapes_against_oracle(orc, T, d, E, K, h):
     """Decode-sized batches (T <= 64 use the weight-streaming expert GEMMs);
