@@ -185,11 +185,31 @@ def bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream, reps=100):
         e1.record(stream)
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) / reps * 1000
+        # The same step captured once in a HIP graph and replayed: no host
+        # launch cost between steps (how a serving loop would run it).
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph):
+            md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+        for _ in range(10):
+            graph.replay()
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us_graph = e0.elapsed_time(e1) / reps * 1000
         routed = md.routing()
         distinct = int(np.unique(routed["idx"]).size)
         wbytes = distinct * 2 * d * h * 2 + E * d * 2
-        out[f"T{td}"] = {"us_per_step": round(us, 2), "distinct_experts": distinct,
-                         "weight_bytes": wbytes,
+        out[f"T{td}"] = {"us_per_step": round(us, 2), "us_per_step_graph": round(us_graph, 2),
+                         "distinct_experts": distinct, "weight_bytes": wbytes,
                          "hbm_gbs": round(wbytes / (us * 1e-6) / 1e9, 1)}
     md.close()
     return out

@@ -331,6 +331,7 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
     if (T > 0) {
         GemmParams up{};
         up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
+        up.idx = E > 1 ? m->idx : nullptr; up.topk = K;
         up.N = hn; up.K = d; up.slots = T * K;
         up.a = X; up.lda = d; up.c = m->U; up.ldc = hn; up.c2 = m->Aact;
         for (int e = 0; e < E; ++e) up.w[e] = W_up[e];

@@ -60,9 +60,10 @@ struct PermuteParams {
 hipError_t launch_permute(const PermuteParams& p, int nblk, hipStream_t s);
 
 // T <= kSmallRouteTokens: router + scan + permute in one launch, one block
-// per token row; the last block to finish (atomic *ticket, zero between
-// calls and re-armed by that block) completes the dispatch. Uses
-// sp.counts/offsets/order/stats and pp.perm/slot_of; no block tables.
+// per token row; with several rows the last block to finish (atomic
+// *ticket, zero between calls and re-armed by that block) completes the
+// dispatch. Uses sp.counts/offsets/order/stats and pp.perm/slot_of; no
+// block tables.
 constexpr int kSmallRouteTokens = 64;
 hipError_t launch_route_small(const RouterParams& p, const ScanParams& sp, const PermuteParams& pp,
                               int* ticket, hipStream_t s);
@@ -88,6 +89,8 @@ struct GemmParams {
     const int32_t* offsets;  // [E+1] expert segment starts (slot space)
     const int32_t* order;    // [E] processing order for weight-gradient GEMMs
     const int32_t* perm;     // [TK] slot -> token (gather table)
+    const int32_t* idx;      // decode UP: [T][topk] expert picks (nullptr: slot == token)
+    int topk;
     int E;
     int M;                   // weight-gradient GEMMs: rows of C
     int N;                   // columns of C

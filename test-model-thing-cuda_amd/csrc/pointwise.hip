@@ -20,42 +20,57 @@
 namespace tmt {
 namespace {
 
-template <bool SILU>
+// K is a template argument so that every load of a pass is issued
+// unconditionally, in one batch: with a runtime K the compiler places the
+// loads under per-pick branches and waits between them.
+template <bool SILU, int K>
 __global__ __launch_bounds__(kThreads) void combine_kernel(CombineParams p) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= p.T) return;
-    const int d = p.d, K = p.K;
-    int pos[kMaxTopK];
-    float g[kMaxTopK];
+    const int d = p.d;
+    int pos[K];
+    float g[K];
 #pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < K) {
-            pos[j] = p.slot_of[(int64_t)r * K + j];
-            g[j] = p.gate[(int64_t)r * K + j];
-        }
+    for (int j = 0; j < K; ++j) {
+        pos[j] = p.slot_of[(int64_t)r * K + j];
+        g[j] = p.gate[(int64_t)r * K + j];
     }
-    for (int c0 = lane * 8; c0 < d; c0 += 512) {
-        float acc[8];
-        uint4* yp = reinterpret_cast<uint4*>(p.Y + (int64_t)r * d + c0);
-        if (p.beta != 0.0f) {
-            unpack8(*yp, acc);
+    const bool resid = p.beta != 0.0f;
+    // Two 512-column chunks per pass with all their loads in flight together
+    // (a decode row waits for one round trip after the slot table, not one
+    // per chunk). A lane whose second chunk lies past d reloads its first
+    // and stores it once.
+    for (int cb = lane * 8; cb < d; cb += 1024) {
+        const bool two = cb + 512 < d;
+        const int cc[2] = {cb, two ? cb + 512 : cb};
+        uint4 yv[2], ov[2][K];
 #pragma unroll
-            for (int t = 0; t < 8; ++t) acc[t] *= p.beta;
-        } else {
+        for (int h = 0; h < 2; ++h) {
+            yv[h] = resid ? *reinterpret_cast<const uint4*>(p.Y + (int64_t)r * d + cc[h]) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-            for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
+            for (int j = 0; j < K; ++j) ov[h][j] = *reinterpret_cast<const uint4*>(p.O + (int64_t)pos[j] * d + cc[h]);
         }
 #pragma unroll
-        for (int j = 0; j < kMaxTopK; ++j) {
-            if (j < K) {
+        for (int h = 0; h < 2; ++h) {
+            float acc[8];
+            if (resid) {
+                unpack8(yv[h], acc);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[t] *= p.beta;
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < K; ++j) {
                 float o[8];
-                unpack8(*reinterpret_cast<const uint4*>(p.O + (int64_t)pos[j] * d + c0), o);
+                unpack8(ov[h][j], o);
 #pragma unroll
                 for (int t = 0; t < 8; ++t) acc[t] += g[j] * (SILU ? silu_fast(o[t]) : o[t]);
             }
+            if (h == 0 || two) *reinterpret_cast<uint4*>(p.Y + (int64_t)r * d + cc[h]) = pack8(acc);
         }
-        *yp = pack8(acc);
     }
 }
 
@@ -428,8 +443,21 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterParams p, int 
 hipError_t launch_combine(const CombineParams& p, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     const int grid = (p.T + 3) / 4;
-    if (p.silu) combine_kernel<true><<<grid, kThreads, 0, s>>>(p);
-    else combine_kernel<false><<<grid, kThreads, 0, s>>>(p);
+    switch (p.K * 2 + (p.silu ? 1 : 0)) {
+#define TMT_COMBINE(KK)                                                       \
+    case 2 * KK: combine_kernel<false, KK><<<grid, kThreads, 0, s>>>(p); break; \
+    case 2 * KK + 1: combine_kernel<true, KK><<<grid, kThreads, 0, s>>>(p); break;
+        TMT_COMBINE(1)
+        TMT_COMBINE(2)
+        TMT_COMBINE(3)
+        TMT_COMBINE(4)
+        TMT_COMBINE(5)
+        TMT_COMBINE(6)
+        TMT_COMBINE(7)
+        TMT_COMBINE(8)
+#undef TMT_COMBINE
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

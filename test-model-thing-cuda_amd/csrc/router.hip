@@ -107,19 +107,23 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 // One arg-max step at offset OFF over (logit desc, expert asc).
 template <int OFF>
-__device__ __forceinline__ void argmax_step(float& bv, float& bp, int& be, bool& has) {
+__device__ __forceinline__ void argmax_step(float& bv, int& be) {
     const float ov = xor_lane<OFF>(bv);
-    const float op = xor_lane<OFF>(bp);
     const int oe = xor_lane<OFF>(be);
-    const int oh = xor_lane<OFF>((int)has);
-    const bool take = oh && (!has || ov > bv || (ov == bv && oe < be));
-    if (take) { bv = ov; bp = op; be = oe; has = true; }
+    if (ov > bv || (ov == bv && oe < be)) {
+        bv = ov;
+        be = oe;
+    }
 }
 
 // Softmax and top-k of one row held by EP lanes (lane e_mine = expert):
 // softmax over the row (moe.cu:41-49); K rounds of a butterfly arg-max over
 // (logit desc, expert asc), i.e. strict '>' with ties to the lower index
 // (moe.cu:52-63); renormalised gate of pick j on lane j (moe.cu:64-66).
+// Lanes out of a round (invalid or already picked) enter it as
+// (-inf, e + 64), which every candidate beats. The winner's probability is
+// recomputed from its logit with the operations its own lane used, so it
+// equals that lane's value bit for bit without another exchange.
 struct RowPick {
     float prob, lse, gate;
     int idx;
@@ -137,22 +141,23 @@ __device__ __forceinline__ RowPick softmax_topk(float logit, bool e_valid, int e
     bool sel = false;
     int out_e = 0;
     float out_p = 0.0f, zsum = 0.0f;
-#pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < K) {
-            bool has = e_valid && !sel;
-            float bv = logit, bp = o.prob;
-            int be = e_mine;
-            if constexpr (EP >= 64) argmax_step<32>(bv, bp, be, has);
-            if constexpr (EP >= 32) argmax_step<16>(bv, bp, be, has);
-            if constexpr (EP >= 16) argmax_step<8>(bv, bp, be, has);
-            argmax_step<4>(bv, bp, be, has);
-            argmax_step<2>(bv, bp, be, has);
-            argmax_step<1>(bv, bp, be, has);
-            if (e_mine == be) sel = true;
-            if (e_mine == j) { out_e = be; out_p = bp; }
-            zsum += bp;
+    for (int j = 0; j < K; ++j) {
+        const bool in = e_valid && !sel;
+        float bv = in ? logit : -INFINITY;
+        int be = in ? e_mine : e_mine + 64;
+        if constexpr (EP >= 64) argmax_step<32>(bv, be);
+        if constexpr (EP >= 32) argmax_step<16>(bv, be);
+        if constexpr (EP >= 16) argmax_step<8>(bv, be);
+        argmax_step<4>(bv, be);
+        argmax_step<2>(bv, be);
+        argmax_step<1>(bv, be);
+        const float bp = __expf(bv - mx) / se;
+        if (e_mine == be) sel = true;
+        if (e_mine == j) {
+            out_e = be;
+            out_p = bp;
         }
+        zsum += bp;
     }
     o.sel = sel;
     o.idx = out_e;
@@ -464,11 +469,59 @@ hipError_t launch_permute(const PermuteParams& p, int nblk, hipStream_t s) {
 //     canonical lane partials and the full xor butterfly (32 .. 1), which adds
 //     the same partial trees as router_kernel's reduce-scatter (bit-identical);
 //  2. softmax / top-k / gates of the row on EP lanes (router_kernel's code);
-//  3. the last block to finish (an atomic ticket, device-scope fences on both
-//     sides) reads every row's picks back and computes counts, offsets, aux /
-//     z, the expert order and the stable permutation, then re-arms the ticket.
+//     a single token's dispatch follows from wave 0's registers directly;
+//  3. with more than one row, the last block to finish (an atomic ticket,
+//     device-scope fences on both sides) reads every row's picks back and
+//     computes counts, offsets, aux / z, the expert order and the stable
+//     permutation, and re-arms the ticket.
+// Decode steps are latency-bound and one wave issues one instruction every
+// few cycles, so the serial parts are short and spread over the waves, and
+// the last block issues its stores after its last barrier (a barrier waits
+// for the block's outstanding global stores).
 constexpr int kSmallGroups = 8;  // ceil(T / floor(64 / K)) for T <= 64, K <= 8
 constexpr int kPairBatch = 4;    // expert dot products per wave with loads in flight
+
+// T == 1: the whole dispatch from wave 0's registers after the softmax. A
+// single token's K picks are distinct experts with one slot each, taken in
+// ascending expert order, so counts, offsets, slots and the expert order
+// are ballots over the picked lanes.
+template <int EP>
+__device__ __forceinline__ void one_token_dispatch(const RouterParams& p, const ScanParams& sp,
+                                                   const PermuteParams& pp, float logit, bool ev,
+                                                   const RowPick& pk, int lane) {
+    const int E = p.E, K = p.K;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    const bool picked = ev && pk.sel;
+    const uint64_t selm = __ballot(picked);
+    const uint64_t valm = __ballot(ev);
+    const int off = __popcll(selm & below);
+    const int ord = picked ? off : K + __popcll(valm & ~selm & below);
+    const int pj = pk.idx;  // pick j on lane j < K
+    const int slot = __popcll(selm & (pj == 0 ? 0ull : (~0ull >> (64 - pj))));
+    // Switch aux (moe.cu:456-465) with T = 1: E * sum_e p_e * (c_e / K).
+    const float inv_tk = 1.0f / (float)K;
+    const float aux = group_sum<EP>(picked ? pk.prob * inv_tk : 0.0f) * (float)E;
+    if (lane < E) {
+        p.logits[lane] = logit;
+        p.probs[lane] = pk.prob;
+        sp.offsets[lane] = off;
+        sp.counts[lane] = picked ? 1 : 0;
+        reinterpret_cast<int32_t*>(sp.stats + 2)[lane] = picked ? 1 : 0;
+        sp.order[ord] = lane;
+    }
+    if (lane < K) {
+        p.idx[lane] = pj;
+        p.gate[lane] = pk.gate;
+        pp.perm[lane] = 0;
+        pp.slot_of[lane] = slot;
+    }
+    if (lane == 0) {
+        p.lse[0] = pk.lse;
+        sp.offsets[E] = K;
+        sp.stats[0] = aux;
+        sp.stats[1] = pk.lse * pk.lse;  // z-loss mean (moe.cu:268-278)
+    }
+}
 
 template <int EP>
 __global__ __launch_bounds__(kThreads) void route_small_kernel(RouterParams p, ScanParams sp,
@@ -486,30 +539,51 @@ __global__ __launch_bounds__(kThreads) void route_small_kernel(RouterParams p, S
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = p.E, K = p.K, T = p.T, d = p.d;
     const int row = blockIdx.x;
-    const int nch = (d + 511) / 512;  // 1 or 2 chunks of 512 (d <= 1024 for E = 32; any d works)
+    const bool single = gridDim.x == 1;
+    const int nch = (d + 511) / 512;
 
-    // 1. logits of this row
+    // 1. logits of this row. Two 512-element chunks per pass, with every
+    // load of the pass (and the bias) in flight together: a decode step
+    // waits for one memory round trip here instead of one per chunk. Each
+    // lane still adds its chunks in ascending order.
     for (int e0 = wave; e0 < E; e0 += 4 * kPairBatch) {
-        float acc[kPairBatch];
+        float acc[kPairBatch], bias[kPairBatch];
 #pragma unroll
-        for (int u = 0; u < kPairBatch; ++u) acc[u] = 0.0f;
-        for (int c = 0; c < nch; ++c) {
-            const int k0 = c * 512 + lane * 8;
-            if (k0 >= d) continue;
-            uint4 wv[kPairBatch];
+        for (int u = 0; u < kPairBatch; ++u) {
+            acc[u] = 0.0f;
+            bias[u] = (p.bias != nullptr && e0 + 4 * u < E) ? p.bias[e0 + 4 * u] : 0.0f;
+        }
+        for (int c = 0; c < nch; c += 2) {
+            int k[2];
+            bool ok[2];
+            uint4 wv[2][kPairBatch], xv[2];
 #pragma unroll
-            for (int u = 0; u < kPairBatch; ++u) {
-                const int e = min(e0 + 4 * u, E - 1);  // clamped: extra pairs are discarded
-                wv[u] = *reinterpret_cast<const uint4*>(p.Wr + (int64_t)e * d + k0);
+            for (int h = 0; h < 2; ++h) {
+                k[h] = (c + h) * 512 + lane * 8;
+                ok[h] = k[h] < d;
+                const int kk = ok[h] ? k[h] : 0;  // clamped: unused lanes load a valid address
+#pragma unroll
+                for (int u = 0; u < kPairBatch; ++u) {
+                    const int e = min(e0 + 4 * u, E - 1);  // clamped: extra pairs are discarded
+                    wv[h][u] = *reinterpret_cast<const uint4*>(p.Wr + (int64_t)e * d + kk);
+                }
+                xv[h] = *reinterpret_cast<const uint4*>(p.X + (int64_t)row * d + kk);
             }
-            float xf[8];
-            unpack8(*reinterpret_cast<const uint4*>(p.X + (int64_t)row * d + k0), xf);
+            // Branch-free (a lane past d keeps its partial by a select): loads
+            // under a branch would be sunk there and waited for separately.
 #pragma unroll
-            for (int u = 0; u < kPairBatch; ++u) {
-                float wf[8];
-                unpack8(wv[u], wf);
+            for (int h = 0; h < 2; ++h) {
+                float xf[8];
+                unpack8(xv[h], xf);
 #pragma unroll
-                for (int t = 0; t < 8; ++t) acc[u] = __builtin_fmaf(xf[t], wf[t], acc[u]);
+                for (int u = 0; u < kPairBatch; ++u) {
+                    float wf[8];
+                    unpack8(wv[h][u], wf);
+                    float a = acc[u];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) a = __builtin_fmaf(xf[t], wf[t], a);
+                    acc[u] = ok[h] ? a : acc[u];
+                }
             }
         }
 #pragma unroll
@@ -522,92 +596,97 @@ __global__ __launch_bounds__(kThreads) void route_small_kernel(RouterParams p, S
             v += xor_lane<2>(v);
             v += xor_lane<1>(v);
             const int e = e0 + 4 * u;
-            if (lane == 0 && e < E) s_logit[e] = p.bias != nullptr ? v + p.bias[e] : v;
+            if (lane == 0 && e < E) s_logit[e] = p.bias != nullptr ? v + bias[u] : v;
         }
     }
     __syncthreads();
 
-    // 2. softmax, top-k, gates on EP lanes of wave 0
+    // 2. softmax, top-k, gates on EP lanes of wave 0; one token finishes
+    // here, several publish their row for the last block.
     if (wave == 0) {
         const int e = lane % EP;
         const bool ev = lane < EP && e < E;
         const float logit = ev ? s_logit[e] : 0.0f;
         const RowPick pk = softmax_topk<EP>(logit, ev, e, K);
-        if (lane < EP) {
+        if (single) {
+            one_token_dispatch<EP>(p, sp, pp, logit, ev, pk, lane);
+        } else if (lane < EP) {
             if (ev) {
                 p.logits[(int64_t)row * E + e] = logit;
                 p.probs[(int64_t)row * E + e] = pk.prob;
-                s_prob[e] = pk.prob;  // used directly when this is the only block
             }
             if (e < K) {
                 p.idx[(int64_t)row * K + e] = pk.idx;
                 p.gate[(int64_t)row * K + e] = pk.gate;
-                s_idx[e] = pk.idx;
             }
-            if (e == 0) {
-                p.lse[row] = pk.lse;
-                s_lse[0] = pk.lse;
-            }
+            if (e == 0) p.lse[row] = pk.lse;
         }
     }
+    if (single) return;
 
-    // 3. the last block finishes the dispatch (a single block already holds
-    // everything in LDS; otherwise every row is read back in one batch)
-    if (gridDim.x > 1) {
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) s_last = atomicAdd(ticket, 1) == T - 1;
-        __syncthreads();
-        if (!s_last) return;
-        __threadfence();
-        const int ni = T * K, np = T * E;
-        for (int i = tid; i < ni + np + T; i += kThreads) {
-            if (i < ni) s_idx[i] = p.idx[i];
-            else if (i < ni + np) s_prob[i - ni] = p.probs[i - ni];
-            else s_lse[i - ni - np] = p.lse[i - ni - np];
+    // 3. the last block finishes the dispatch (every row read back in one batch)
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(ticket, 1) == T - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    {
+        // All of a thread's loads are issued before any LDS store.
+        const int ni = T * K, np = T * E, n = ni + np + T;
+        const uint32_t* gidx = reinterpret_cast<const uint32_t*>(p.idx);
+        const uint32_t* gprob = reinterpret_cast<const uint32_t*>(p.probs);
+        const uint32_t* glse = reinterpret_cast<const uint32_t*>(p.lse);
+        for (int base = tid; base < n; base += 8 * kThreads) {
+            uint32_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = min(base + u * kThreads, n - 1);
+                v[u] = i < ni ? gidx[i] : (i < ni + np ? gprob[i - ni] : glse[i - ni - np]);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = base + u * kThreads;
+                if (i >= n) break;
+                if (i < ni) s_idx[i] = (int)v[u];
+                else if (i < ni + np) s_prob[i - ni] = __uint_as_float(v[u]);
+                else s_lse[i - ni - np] = __uint_as_float(v[u]);
+            }
         }
     }
-    if (tid < kMaxExperts) s_cnt[tid] = 0;
     __syncthreads();
-    for (int i = tid; i < T * K; i += kThreads) atomicAdd(&s_cnt[s_idx[i]], 1);
-    if (tid < E) {
+
+    // Per-expert probability sums over the rows in order (wave 3), the sum
+    // of lse^2 (wave 2) and the per-group pick counts of the stable
+    // permutation (groups of floor(64/K) tokens, a ballot per expert, waves
+    // g < G). Loops over experts and groups run to the compile-time bounds
+    // EP and kSmallGroups, so their LDS reads are issued together.
+    if (wave == 3 && lane < E) {
         float sum = 0.0f;
-        for (int r = 0; r < T; ++r) sum += s_prob[r * E + tid];
-        s_sum[tid] = sum;
-    } else if (tid == E) {
-        float l2 = 0.0f;
-        for (int r = 0; r < T; ++r) l2 += s_lse[r] * s_lse[r];
-        s_sum[E] = l2;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        int run = 0;
-        for (int e = 0; e < E; ++e) {
-            s_off[e] = run;
-            run += s_cnt[e];
+        for (int r0 = 0; r0 < T; r0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = s_prob[min(r0 + i, T - 1) * E + lane];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (r0 + i < T) sum += v[i];
         }
-        s_off[E] = run;
-        // Switch aux (moe.cu:456-465) and z-loss mean (moe.cu:268-278).
-        const float inv_t = 1.0f / (float)T;
-        const float inv_tk = 1.0f / ((float)T * (float)K);
-        float aux = 0.0f;
-        for (int e = 0; e < E; ++e) aux += (s_sum[e] * inv_t) * ((float)s_cnt[e] * inv_tk);
-        sp.stats[0] = aux * (float)E;
-        sp.stats[1] = s_sum[E] * inv_t;
-        if (gridDim.x > 1) *ticket = 0;  // re-armed for the next call (stream order keeps calls apart)
+        s_sum[lane] = sum;
+    } else if (wave == 2 && lane == 0) {
+        float sum = 0.0f;
+        for (int r0 = 0; r0 < T; r0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float l = s_lse[min(r0 + i, T - 1)];
+                v[i] = l * l;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                if (r0 + i < T) sum += v[i];
+        }
+        s_sum[E] = sum;
     }
-    __syncthreads();
-    if (tid <= E) sp.offsets[tid] = s_off[tid];
-    if (tid < E) {
-        sp.counts[tid] = s_cnt[tid];
-        reinterpret_cast<int32_t*>(sp.stats + 2)[tid] = s_cnt[tid];
-        int rank = 0;
-        for (int e = 0; e < E; ++e)
-            rank += (s_cnt[e] > s_cnt[tid]) || (s_cnt[e] == s_cnt[tid] && e < tid);
-        sp.order[rank] = tid;
-    }
-
-    // Stable permutation: groups of floor(64/K) tokens, a ballot per expert.
     const int RG = 64 / K, pairs = RG * K;
     const int G = (T + RG - 1) / RG;
     const int rr = lane / K, j = lane % K;
@@ -616,35 +695,112 @@ __global__ __launch_bounds__(kThreads) void route_small_kernel(RouterParams p, S
         const int r = g * RG + rr;
         const bool valid = lane < pairs && r < T;
         const int e = valid ? s_idx[r * K + j] : -1;
-        for (int ee = 0; ee < E; ++ee) {
+#pragma unroll
+        for (int ee = 0; ee < EP; ++ee) {
             const uint64_t m = __ballot(e == ee);
             if (lane == ee) s_g[g][ee] = __popcll(m);
         }
     }
     __syncthreads();
-    if (tid < E) {
-        int run = s_off[tid];
-        for (int g = 0; g < G; ++g) {
-            const int c = s_g[g][tid];
-            s_g[g][tid] = run;
-            run += c;
+
+    // Counts (the groups' counts added), offsets (an exclusive scan over the
+    // expert lanes) and the group bases of each expert's segment, on wave 0.
+    if (wave == 0) {
+        int c[kSmallGroups], cnt = 0;
+#pragma unroll
+        for (int g = 0; g < kSmallGroups; ++g) {
+            c[g] = (g < G && lane < E) ? s_g[g][lane] : 0;
+            cnt += c[g];
         }
+        int incl = cnt;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        int run = incl - cnt;
+        if (lane < E) {
+            s_cnt[lane] = cnt;
+            s_off[lane] = run;
+#pragma unroll
+            for (int g = 0; g < kSmallGroups; ++g) {
+                if (g < G) s_g[g][lane] = run;
+                run += c[g];
+            }
+        }
+        if (lane == 0) s_off[E] = T * K;
     }
     __syncthreads();
-    for (int g = wave; g < G; g += 4) {
+
+    // Everything that is stored is computed first: a register that still
+    // feeds an outstanding store cannot be overwritten without a wait.
+    int pos[2], prow[2];
+    bool pvalid[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {  // G <= kSmallGroups = 8 groups over 4 waves
+        const int g = wave + 4 * q;
         const int r = g * RG + rr;
-        const bool valid = lane < pairs && r < T;
-        const int e = valid ? s_idx[r * K + j] : -1;
+        pvalid[q] = g < G && lane < pairs && r < T;
+        pos[q] = 0;
+        prow[q] = r;
+        if (g >= G) continue;  // uniform
+        const int e = pvalid[q] ? s_idx[r * K + j] : -1;
         int rank = 0;
-        for (int ee = 0; ee < E; ++ee) {
+#pragma unroll
+        for (int ee = 0; ee < EP; ++ee) {
             const uint64_t m = __ballot(e == ee);
             if (e == ee) rank = __popcll(m & lt_mask);
         }
-        if (valid) {
-            const int pos = s_g[g][e] + rank;
-            pp.perm[pos] = r;
-            pp.slot_of[(int64_t)r * K + j] = pos;
+        if (pvalid[q]) pos[q] = s_g[g][e] + rank;
+    }
+    // Expert order on wave 1, aux / z on wave 2.
+    int ord = 0, cnt = 0, off = 0;
+    if (tid <= E) off = s_off[tid];
+    const bool order_lane = wave == 1 && lane < E;
+    if (order_lane) {
+        cnt = s_cnt[lane];
+#pragma unroll
+        for (int e = 0; e < EP; ++e) {
+            const int ce = s_cnt[e];
+            ord += e < E && ((ce > cnt) || (ce == cnt && e < lane));
         }
+    }
+    float aux = 0.0f, zl = 0.0f;
+    const bool stat_lane = wave == 2 && lane == 0;
+    if (stat_lane) {
+        // Switch aux (moe.cu:456-465) and z-loss mean (moe.cu:268-278).
+        const float inv_t = 1.0f / (float)T;
+        const float inv_tk = 1.0f / ((float)T * (float)K);
+        float fs[EP], fc[EP];
+#pragma unroll
+        for (int e = 0; e < EP; ++e) {
+            fs[e] = s_sum[min(e, E - 1)];
+            fc[e] = (float)s_cnt[e];
+        }
+#pragma unroll
+        for (int e = 0; e < EP; ++e)
+            if (e < E) aux += (fs[e] * inv_t) * (fc[e] * inv_tk);
+        aux *= (float)E;
+        zl = s_sum[E] * inv_t;
+    }
+    // Stores only from here on.
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        if (pvalid[q]) {
+            pp.perm[pos[q]] = prow[q];
+            pp.slot_of[(int64_t)prow[q] * K + j] = pos[q];
+        }
+    }
+    if (tid <= E) sp.offsets[tid] = off;
+    if (order_lane) {
+        sp.counts[lane] = cnt;
+        reinterpret_cast<int32_t*>(sp.stats + 2)[lane] = cnt;
+        sp.order[ord] = lane;
+    }
+    if (stat_lane) {
+        sp.stats[0] = aux;
+        sp.stats[1] = zl;
+        *ticket = 0;  // re-armed for the next call (stream order keeps calls apart)
     }
 }
 

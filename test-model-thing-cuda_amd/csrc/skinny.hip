@@ -20,6 +20,14 @@
 // lengths that do not split into one chunk per wave.
 // Experts are visited in descending-count order (the scan's LPT order), so
 // the grid only spans min(E, T*K) expert ranks.
+//
+// Decode steps are latency-bound, so a workgroup's first memory round trip
+// fetches everything its loads depend on: the rank's expert, the whole
+// offset table and the per-expert weight pointers (lane e holds expert e's
+// entries, the rank's expert is then picked from registers) and, for UP,
+// the [T][K] pick table, from which each wave finds the tokens of its
+// expert's rows itself instead of reading the permutation (a second round
+// trip before the activation loads).
 #include "device_util.hpp"
 #include "moe_internal.hpp"
 
@@ -33,32 +41,120 @@ __device__ __forceinline__ f32x4 mfma16(const uint4& w, const uint4& a, const f3
                                                    __builtin_bit_cast(bf16x8, a), c, 0, 0, 0);
 }
 
+// Weight streams go through a buffer resource: a pointer picked from
+// registers is no longer known to be global memory, so plain loads through
+// it would become flat loads, which also count on the LDS/scalar counter and
+// so hold up every later LDS or scalar wait; buffer loads count on the
+// vector-memory counter only. Word 3 is the gfx9 raw-buffer format.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const uint16_t* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 ld16_buf(__amdgpu_buffer_rsrc_t r, int off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
+// Kernel arguments are brought into registers before the first data load:
+// a scalar argument load that the compiler sinks below the table loads
+// would add a round trip to the workgroup's critical path.
+__device__ __forceinline__ void in_sgpr(int v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void in_sgpr(int64_t v) { asm volatile("" ::"s"(v)); }
+__device__ __forceinline__ void in_sgpr(const void* v) { asm volatile("" ::"s"(v)); }
+template <class... T>
+__device__ __forceinline__ void args_in_sgprs(const T&... v) {
+    (in_sgpr(v), ...);
+}
+
+// The expert of one rank: its first slot, row count and weights.
+struct SkinnyExpert {
+    int e, row0, rows;
+    const uint16_t* w;
+};
+
+// All four tables are read with vector loads: a scalar load of order[rank]
+// would share its wait counter with the kernel-argument loads that the
+// compiler places between the table loads, and so serialise them.
+__device__ __forceinline__ SkinnyExpert skinny_expert(const GemmParams& p, int rank, int lane) {
+    const bool in = lane < p.E;
+    const int ov = in ? p.order[lane] : 0;
+    const int o0 = in ? p.offsets[lane] : 0;
+    const int o1 = in ? p.offsets[lane + 1] : 0;
+    const uint64_t wl = in ? reinterpret_cast<uint64_t>(p.w[lane]) : 0;
+    SkinnyExpert x;
+    x.e = __builtin_amdgcn_readlane(ov, rank);
+    x.row0 = __builtin_amdgcn_readlane(o0, x.e);
+    x.rows = __builtin_amdgcn_readlane(o1, x.e) - x.row0;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)wl, x.e);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(wl >> 32), x.e);
+    x.w = reinterpret_cast<const uint16_t*>(((uint64_t)hi << 32) | lo);
+    return x;
+}
+
+// UP: entries q * 64 + lane of the [T][K] pick table (-1 past T*K, or
+// without a table: E == 1, where slot == token).
+constexpr int kPickGroups = kSkinnyMaxTokens * kMaxTopK / 64;
+__device__ __forceinline__ void load_picks(const GemmParams& p, int lane, int (&ent)[kPickGroups]) {
+#pragma unroll
+    for (int q = 0; q < kPickGroups; ++q) {
+        const int i = q * 64 + lane;
+        ent[q] = (p.idx != nullptr && i < p.slots) ? p.idx[i] : -1;
+    }
+}
+
+// tok[m] = token of row m of expert e, for the first 16 * RB rows. The
+// dispatch is stable (an expert's slots follow ascending token order) and a
+// token picks an expert at most once, so row m is the m-th pick of e in
+// table order. The list is the wave's own: LDS accesses of one wave complete
+// in order, so no barrier is needed before the wave reads it back.
+__device__ __forceinline__ void expert_tokens(const int (&ent)[kPickGroups], int slots, int K, int e,
+                                              int lane, int maxrows, int* tok) {
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int base = 0;
+#pragma unroll
+    for (int q = 0; q < kPickGroups; ++q) {
+        if (q * 64 >= slots) break;  // uniform
+        const bool hit = ent[q] == e;
+        const uint64_t mk = __ballot(hit);
+        const int r = base + __popcll(mk & lt);
+        if (hit && r < maxrows) tok[r] = (q * 64 + lane) / K;
+        base += __popcll(mk);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <int KIND, bool DUAL, int RB>
 __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(GemmParams p, int nexp) {
     static_assert(KIND == GEMM_UP || KIND == GEMM_DOWN, "forward GEMMs only");
     constexpr bool kGather = KIND == GEMM_UP;
     __shared__ f32x4 red[4][RB][64];
+    __shared__ int s_tok[4][16 * RB];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rank = (int)blockIdx.x % nexp, tile = (int)blockIdx.x / nexp;
-    const int e = p.order[rank];
-    const int row0 = p.offsets[e];
-    const int rows = min(p.offsets[e + 1] - row0, 16 * RB);
+    int ent[kPickGroups];
+    if constexpr (kGather) load_picks(p, lane, ent);
+    const SkinnyExpert x = skinny_expert(p, rank, lane);
+    const int row0 = x.row0;
+    const int rows = min(x.rows, 16 * RB);
     if (rows <= 0) return;
     const int n0 = tile * 16;
     const int g = lane >> 4, li = lane & 15;
+    if constexpr (kGather) {
+        if (p.idx != nullptr) expert_tokens(ent, p.slots, p.topk, x.e, lane, 16 * RB, s_tok[wave]);
+    }
 
     // This lane's weight row (output column n0 + li) and activation rows.
-    const uint16_t* wrow = p.w[e] + (int64_t)(n0 + li) * p.ldb;
+    const uint16_t* wrow = p.w[x.e] + (int64_t)(n0 + li) * p.ldb;  // kernarg pointer: global loads
     const uint16_t* arow[RB];
     bool aok[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         const int m = rb * 16 + li;
         aok[rb] = m < rows;
-        const int slot = row0 + (aok[rb] ? m : 0);
-        const int src = kGather ? p.perm[slot] : slot;
+        const int mm = aok[rb] ? m : 0;
+        const int src = (kGather && p.idx != nullptr) ? s_tok[wave][mm] : row0 + mm;
         arow[rb] = p.a + (int64_t)src * p.lda;
     }
 
@@ -159,33 +255,42 @@ __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int ne
     static_assert(KIND == GEMM_UP || KIND == GEMM_DOWN, "forward GEMMs only");
     constexpr bool kGather = KIND == GEMM_UP;
     extern __shared__ f32x4 red[];  // [RB][CT][nw][64] wave partials
+    __shared__ int s_tok[16][16 * RB];
 
     const int nw = (int)blockDim.x >> 6;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rank = (int)blockIdx.x % nexp, tile0 = ((int)blockIdx.x / nexp) * CT;
-    const int e = p.order[rank];
-    const int row0 = p.offsets[e];
-    const int rows = min(p.offsets[e + 1] - row0, 16 * RB);
+    args_in_sgprs(p.order, p.offsets, p.idx, p.a, p.c, p.c2, p.E, p.slots, p.topk, p.lda, p.ldb, p.ldc);
+    int ent[kPickGroups];
+    if constexpr (kGather) load_picks(p, lane, ent);
+    const SkinnyExpert x = skinny_expert(p, rank, lane);
+    const int row0 = x.row0;
+    const int rows = min(x.rows, 16 * RB);
     if (rows <= 0) return;
     const int nrb = (rows + 15) >> 4;
     const int g = lane >> 4, li = lane & 15;
     const int kw = wave * (32 * J) + g * 8;
 
+    // The workgroup's CT * 16 weight rows (K <= 4096 on this path: at most
+    // 256 KiB, so 32-bit offsets).
+    const __amdgpu_buffer_rsrc_t wr = weight_rsrc(x.w + (int64_t)tile0 * 16 * p.ldb, CT * 16 * (int)p.ldb * 2);
     uint4 wv[CT][J];
 #pragma unroll
     for (int c = 0; c < CT; ++c) {
-        const uint16_t* src = p.w[e] + (int64_t)((tile0 + c) * 16 + li) * p.ldb + kw;
+        const int off = ((c * 16 + li) * (int)p.ldb + kw) * 2;
 #pragma unroll
-        for (int i = 0; i < J; ++i) wv[c][i] = ld16(src + 32 * i);
+        for (int i = 0; i < J; ++i) wv[c][i] = ld16_buf(wr, off + 64 * i);
     }
+    const bool by_pick = kGather && p.idx != nullptr;
+    if (by_pick) expert_tokens(ent, p.slots, p.topk, x.e, lane, 16 * RB, s_tok[wave]);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
         if (rb >= nrb) break;  // uniform
         const int m = rb * 16 + li;
         const bool ok = m < rows;
-        const int slot = row0 + (ok ? m : 0);
-        const int srow = kGather ? p.perm[slot] : slot;
+        const int mm = ok ? m : 0;
+        const int srow = by_pick ? s_tok[wave][mm] : row0 + mm;
         const uint16_t* ar = p.a + (int64_t)srow * p.lda + kw;
         uint4 av[J];
 #pragma unroll

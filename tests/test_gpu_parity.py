@@ -280,9 +280,9 @@ def test_decode_steps_against_oracle(orc, T):
     (65, 192, 5, 2, 320),    # first token count on the tiled path
     (9, 128, 4, 2, 1088),    # down-projection K of 17 x 64: one tile per workgroup
     (33, 256, 8, 2, 2048),   # three 16-row blocks, 8 waves of 256-element chunks
-    (2, 128, 64, 8, 256),    # fused down+combine: 16 experts of one chunk, one unit per wave
-    (7, 320, 6, 3, 768),     # fused: 20 column tiles, a wave's units span two experts
-    (1, 64, 2, 1, 256),      # fused: a single token and expert
+    (2, 128, 64, 8, 256),    # 64 experts, 16 ranks of one row, one 64-element unit per wave
+    (7, 320, 6, 3, 768),     # 20 column tiles of DOWN, a single row block per expert
+    (1, 64, 2, 1, 256),      # a single token and expert, d of one unit
 ])
 def test_decode_shapes_against_oracle(orc, T, d, E, K, h):
     """Decode-sized batches (T <= 64 use the weight-streaming expert GEMMs);
