@@ -238,6 +238,9 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(GemmParams p, int
 // the step is latency-bound and the larger grid of one tile wins (T = 1:
 // 29.6 us per step with one tile, 34.0 with two).
 constexpr int kSkinnyTwoTileTokens = 4;
+// From this many tokens the persistent kernel (skinny_stream_kernel) runs
+// where it applies.
+constexpr int kSkinnyStreamTokens = 4;
 
 // Variant for reduction lengths K = NW * 32J (J = 8: K a multiple of 256
 // up to 4096; J = 2: a multiple of 64 up to 1024): the workgroup has NW
@@ -326,6 +329,108 @@ __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int ne
     }
 }
 
+// Persistent variant of the chunk kernel (J = 8) for T >= kSkinnyStreamTokens.
+// Workgroup (rank, s) visits the column tiles s, s + split, ... of its
+// expert. The activation chunks of the expert's rows do not depend on the
+// column, so they are loaded once and stay in registers; the weights of the
+// next tile are requested before the current tile is multiplied, reduced and
+// stored, so a workgroup's weight stream does not pause between tiles (two
+// register sets alternate: a copy between them would wait for the loads).
+// Lane/k assignment, MFMA order and wave order of the sums are the chunk
+// kernel's, so the results are bit-identical to it. A past-the-end tile reads
+// zeros from the buffer resource without touching memory.
+template <int KIND, bool DUAL, int RB, int NWMAX>
+__global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p, int nexp, int split) {
+    static_assert(KIND == GEMM_UP || KIND == GEMM_DOWN, "forward GEMMs only");
+    constexpr bool kGather = KIND == GEMM_UP;
+    constexpr int J = 8;
+    extern __shared__ f32x4 red[];  // [RB][nw][64] wave partials
+    __shared__ int s_tok[NWMAX][16 * RB];
+
+    const int nw = (int)blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int rank = (int)blockIdx.x % nexp, s0 = (int)blockIdx.x / nexp;
+    args_in_sgprs(p.order, p.offsets, p.idx, p.a, p.c, p.c2, p.E, p.N, p.slots, p.topk, p.lda, p.ldb, p.ldc);
+    int ent[kPickGroups];
+    if constexpr (kGather) load_picks(p, lane, ent);
+    const SkinnyExpert x = skinny_expert(p, rank, lane);
+    const int row0 = x.row0;
+    const int rows = min(x.rows, 16 * RB);
+    const int ntile = p.N >> 4;
+    if (rows <= 0 || s0 >= ntile) return;
+    const int nrb = (rows + 15) >> 4;
+    const int g = lane >> 4, li = lane & 15;
+    const int kw = wave * (32 * J) + g * 8;
+
+    // The expert's weights [N][K] as one buffer (below 2 GiB: checked by the host).
+    const int wbytes = p.N * (int)p.ldb * 2;
+    const __amdgpu_buffer_rsrc_t wr = weight_rsrc(x.w, wbytes);
+    const int lane_off = (li * (int)p.ldb + kw) * 2;
+    const int tile_bytes = 16 * (int)p.ldb * 2;
+    auto wload = [&](int tile, uint4 (&w)[J]) {
+        const int off = tile < ntile ? tile * tile_bytes + lane_off : wbytes;
+#pragma unroll
+        for (int i = 0; i < J; ++i) w[i] = ld16_buf(wr, off + 64 * i);
+    };
+    uint4 w0[J], w1[J];
+    wload(s0, w0);
+
+    const bool by_pick = kGather && p.idx != nullptr;
+    if (by_pick) expert_tokens(ent, p.slots, p.topk, x.e, lane, 16 * RB, s_tok[wave]);
+    uint4 av[RB][J];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int m = rb * 16 + li;
+        const bool ok = m < rows;
+        const int mm = ok ? m : 0;
+        const int srow = by_pick ? s_tok[wave][mm] : row0 + mm;
+        const uint16_t* ar = p.a + (int64_t)srow * p.lda + kw;
+#pragma unroll
+        for (int i = 0; i < J; ++i) av[rb][i] = (rb < nrb) ? ld16(ar + 32 * i) : make_uint4(0, 0, 0, 0);
+        if (!ok) {
+#pragma unroll
+            for (int i = 0; i < J; ++i) av[rb][i] = make_uint4(0, 0, 0, 0);
+        }
+    }
+
+    uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
+    auto step = [&](int tile, const uint4 (&w)[J]) {
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            if (rb >= nrb) break;  // uniform
+            f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < J; ++i) acc = mfma16(w[i], av[rb][i], acc);
+            red[(rb * nw + wave) * 64 + lane] = acc;
+        }
+        __syncthreads();
+        for (int o = tid; o < nrb * 256; o += (int)blockDim.x) {
+            const int rb = o >> 8, m = (o >> 4) & 15, n = o & 15;
+            const int row = rb * 16 + m;
+            if (row >= rows) continue;
+            const int sl = (n >> 2) * 16 + m, r = n & 3;
+            float v = red[(rb * nw) * 64 + sl][r];
+            for (int w2 = 1; w2 < nw; ++w2) v += red[(rb * nw + w2) * 64 + sl][r];
+            const int64_t off = (int64_t)(row0 + row) * p.ldc + tile * 16 + n;
+            C[off] = f2bf(v);
+            if constexpr (DUAL) p.c2[off] = f2bf(silu_fast(v));
+        }
+        __syncthreads();
+    };
+    // The scheduling barriers keep the next tile's loads ahead of the
+    // current tile's multiplies (the scheduler would otherwise sink them).
+    for (int tile = s0; tile < ntile; tile += 2 * split) {
+        wload(tile + split, w1);
+        __builtin_amdgcn_sched_barrier(0);
+        step(tile, w0);
+        if (tile + split >= ntile) break;
+        wload(tile + 2 * split, w0);
+        __builtin_amdgcn_sched_barrier(0);
+        step(tile + split, w1);
+    }
+}
+
 template <int KIND, bool DUAL>
 hipError_t launch_rb(int rb, const GemmParams& p, int nexp, unsigned grid, hipStream_t s) {
     switch (rb) {
@@ -359,6 +464,38 @@ hipError_t launch_chunk(int J, int ct, int rb, int nw, const GemmParams& p, int 
                   : launch_chunk_rb<KIND, DUAL, 2, 1>(rb, nw, p, nexp, s);
 }
 
+template <int KIND, bool DUAL>
+hipError_t launch_stream(int rb, int nw, const GemmParams& p, int nexp, int split, hipStream_t s) {
+    const unsigned grid = (unsigned)split * (unsigned)nexp;
+    const dim3 block(64 * nw);
+    const size_t lds = (size_t)rb * nw * 64 * sizeof(f32x4);
+    if (nw > 8) {
+        if (rb != 1) return hipErrorInvalidValue;
+        skinny_stream_kernel<KIND, DUAL, 1, 16><<<grid, block, lds, s>>>(p, nexp, split);
+        return hipGetLastError();
+    }
+    switch (rb) {
+        case 1: skinny_stream_kernel<KIND, DUAL, 1, 8><<<grid, block, lds, s>>>(p, nexp, split); break;
+        case 2: skinny_stream_kernel<KIND, DUAL, 2, 8><<<grid, block, lds, s>>>(p, nexp, split); break;
+        case 4: skinny_stream_kernel<KIND, DUAL, 4, 8><<<grid, block, lds, s>>>(p, nexp, split); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// Compute units of the current device (cached per device).
+int cu_count() {
+    static int cached[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
 }  // namespace
 
 hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s) {
@@ -376,6 +513,19 @@ hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int
         nw = p.K / 64;
     }
     const int rb = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
+    // Persistent workgroups where the activation chunks fit in registers next
+    // to two weight sets: up to 8 waves for any row count, 16 waves for one
+    // row block.
+    if (J == 8 && T >= kSkinnyStreamTokens && (nw <= 8 || rb == 1) && (int64_t)p.N * p.ldb * 2 < (1ll << 31)) {
+        const int ntile = p.N / 16;
+        const int per_cu = nw > 8 ? 1 : (rb == 4 ? 2 : (rb == 2 ? 3 : 4)) * 4 / nw;
+        int split = (cu_count() * (per_cu > 0 ? per_cu : 1) + nexp - 1) / nexp;
+        split = split < 1 ? 1 : (split > ntile ? ntile : split);
+        if (kind == GEMM_UP)
+            return dual ? launch_stream<GEMM_UP, true>(rb, nw, p, nexp, split, s)
+                        : launch_stream<GEMM_UP, false>(rb, nw, p, nexp, split, s);
+        return launch_stream<GEMM_DOWN, false>(rb, nw, p, nexp, split, s);
+    }
     if (J > 0) {
         const int ct = (T >= kSkinnyTwoTileTokens && p.N % 32 == 0) ? 2 : 1;
         if (kind == GEMM_UP)

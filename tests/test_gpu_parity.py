@@ -283,6 +283,8 @@ def test_decode_steps_against_oracle(orc, T):
     (2, 128, 64, 8, 256),    # 64 experts, 16 ranks of one row, one 64-element unit per wave
     (7, 320, 6, 3, 768),     # 20 column tiles of DOWN, a single row block per expert
     (1, 64, 2, 1, 256),      # a single token and expert, d of one unit
+    (24, 1024, 8, 2, 4096),  # persistent UP, two resident row blocks, 2-3 tiles per workgroup
+    (12, 512, 3, 2, 2048),   # persistent DOWN over 8 waves, one tile and a past-the-end prefetch
 ])
 def test_decode_shapes_against_oracle(orc, T, d, E, K, h):
     """Decode-sized batches (T <= 64 use the weight-streaming expert GEMMs);
