@@ -192,7 +192,7 @@ def test_dead_experts_get_zero_gradients(orc):
     check_grads(g, r, h, E)
 
 
-@pytest.mark.parametrize("T", [256, 8])  # tiled router and the single-workgroup decode router
+@pytest.mark.parametrize("T", [256, 8, 1])  # tiled router, decode router, single-token dispatch
 def test_router_ties_go_to_lower_index(orc, T):
     say(f"router ties (T={T}): experts 2 and 4 have identical rows")
     d, E, K, h = 256, 6, 2, 128
@@ -299,6 +299,25 @@ def test_decode_shapes_against_oracle(orc, T, d, E, K, h):
     err = rel_l2(g["Y"], r["Y"])
     say(f"  Y rel-L2 {err:.2e}")
     assert err <= REL_L2
+    check_grads(g, r, h, E)
+
+
+@pytest.mark.parametrize("E,K", [(64, 8), (16, 4), (3, 3)])
+def test_single_token_dispatch_with_bias(orc, E, K):
+    """T = 1 finishes the dispatch in the router's registers (ballots over
+    the picked lanes); a Zipf logit bias, every expert count from 1 to 64
+    lanes, K up to E."""
+    say(f"single token E={E} K={K} with a Zipf logit bias, fwd+bwd")
+    d, h = 256, 256
+    case = make_case(1, d, E, K, h, seed=100 + E, zipf=1.1)
+    Y0 = bf16_bits(np.random.default_rng(E).standard_normal((1, d)).astype(np.float32))
+    g = run_gpu(case, K, h, beta=1.0, Y0=Y0, backward=True, aux=0.1, z=1e-3, max_tokens=4)
+    r = oracle_case(orc, case, K, h, Y0=Y0, beta=1.0, backward=True, aux=0.1, z=1e-3)
+    check_routing(g, r, E)
+    near(g["aux"], r["aux"], 1e-6, 1e-4, "aux")
+    near(g["z"], r["z"], 1e-6, 1e-4, "z")
+    assert list(g["counts"]) == [int(e in r["idx"][0]) for e in range(E)]
+    assert rel_l2(g["Y"], r["Y"]) <= REL_L2
     check_grads(g, r, h, E)
 
 
