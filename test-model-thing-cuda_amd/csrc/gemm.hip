@@ -38,7 +38,7 @@
 namespace tmt {
 namespace {
 
-constexpr int BM = 256;
+constexpr int BM = kGemmTileRows;
 
 // Tile geometry. BK_ is the K depth of one LDS stage (32 or 64), NST the
 // number of stages in the ring, BN_ the tile width and NWM_ the waves along
@@ -172,6 +172,60 @@ __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
 }
 
+// Split-K of the last round (GEMM_DOWN / GEMM_DX, tiles 256 x BN, one
+// workgroup per CU). The activation tiles are numbered expert segment by
+// segment, M tile mt of all ntn column tiles; with ntn <= 8 and W resident
+// workgroups, the tiles with mt < cut (cut * ntn a multiple of W) fill whole
+// rounds. The R = (MT - cut) * ntn tiles left would otherwise run as one
+// short round on R CUs while the rest idle, so each is cut into S parts
+// along K (S = W / R, at least 8 k tiles a part). Part q of tail tile j is
+// workgroup F + j*S + q (F = cut * ntn, after the whole rounds in launch
+// order); it writes an fp32 partial tile, and split_fixup_kernel adds a
+// tile's S partials in part order and stores the bf16 result.
+struct SplitPlan {
+    int cut = 0, F = 0, R = 0, S = 1, chunk = 0;  // chunk: reduction length of a part
+};
+__device__ __forceinline__ int act_mtiles(const GemmParams& p) {
+    int mt = 0;
+    for (int ee = 0; ee < p.E; ++ee) mt += (p.offsets[ee + 1] - p.offsets[ee] + BM - 1) / BM;
+    return mt;
+}
+template <int BK>
+__device__ __forceinline__ SplitPlan split_plan(const GemmParams& p, int ntn, int mtiles) {
+    SplitPlan sp;
+    const int W = p.resident;
+    // W a multiple of 256: the launch-order permutation of workgroups stays
+    // inside aligned blocks of 256, so the first F workgroups are the rounds' tiles.
+    if (p.part == nullptr || ntn > 8 || W <= 0 || W % 256 != 0 || W % ntn != 0) return sp;
+    const int per = W / ntn;  // M tiles per round
+    sp.cut = (mtiles / per) * per;
+    sp.F = sp.cut * ntn;
+    sp.R = (mtiles - sp.cut) * ntn;
+    const int nk = p.K / BK;
+    int S = sp.R > 0 ? W / sp.R : 1;
+    S = min(S, nk / 8);
+    if (S < 2) return SplitPlan{};
+    sp.S = S;
+    sp.chunk = ((nk + S - 1) / S) * BK;
+    return sp;
+}
+// Expert segment of activation M tile mt: expert, first slot, rows (e < 0: none).
+__device__ __forceinline__ void act_tile(const GemmParams& p, int mt, int& e, int& row0, int& rows) {
+    e = -1;
+    int t0 = 0;
+    for (int ee = 0; ee < p.E; ++ee) {
+        const int beg = p.offsets[ee], end = p.offsets[ee + 1];
+        const int tiles = (end - beg + BM - 1) / BM;
+        if (mt < t0 + tiles) {
+            e = ee;
+            row0 = beg + (mt - t0) * BM;
+            rows = min(BM, end - row0);
+            return;
+        }
+        t0 += tiles;
+    }
+}
+
 template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2>
 __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
     using Tr = Traits<KIND>;
@@ -209,32 +263,39 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     const int G = lid >> 5, gi = lid & 31;
     const int gn = min(ntn, 8), gm = 32 / gn;
     const int ngn = (ntn + gn - 1) / gn;
-    if (gi >= gm * gn) return;
     int e = -1, mt = 0, nt = 0;
     int row0 = 0, rows = 0;   // activation GEMMs: slot range of this tile
     int kbeg = 0, kend = 0;   // reduction range (slots for dW GEMMs)
     int mlim = 0;             // valid output rows in this tile
+    constexpr bool kSplitK = KIND == GEMM_DOWN || KIND == GEMM_DX;
+    int part_unit = -1;  // split-K tail: index of this workgroup's partial tile
     if constexpr (!Tr::group_k) {
-        mt = (G / ngn) * gm + gi % gm;
-        nt = (G % ngn) * gn + gi / gm;
-        if (nt >= ntn) return;
-        int t0 = 0;
-        for (int ee = 0; ee < p.E; ++ee) {
-            const int beg = p.offsets[ee], end = p.offsets[ee + 1];
-            const int tiles = (end - beg + BM - 1) / BM;
-            if (mt < t0 + tiles) {
-                e = ee;
-                row0 = beg + (mt - t0) * BM;
-                rows = min(BM, end - row0);
-                break;
-            }
-            t0 += tiles;
-        }
-        if (e < 0) return;  // beyond the last tile of the last expert
         kbeg = 0;
         kend = p.K;
+        SplitPlan sp;
+        if constexpr (kSplitK) {
+            if (p.part != nullptr) sp = split_plan<BK>(p, ntn, act_mtiles(p));
+        }
+        if (sp.S >= 2 && (int)blockIdx.x >= sp.F) {
+            const int u = (int)blockIdx.x - sp.F;
+            if (u >= sp.R * sp.S) return;
+            const int j = u / sp.S, q = u - j * sp.S;
+            mt = sp.cut + j / ntn;
+            nt = j % ntn;
+            kbeg = q * sp.chunk;
+            kend = min(p.K, kbeg + sp.chunk);
+            part_unit = u;
+        } else {
+            if (gi >= gm * gn) return;
+            mt = (G / ngn) * gm + gi % gm;
+            nt = (G % ngn) * gn + gi / gm;
+            if (nt >= ntn) return;
+        }
+        act_tile(p, mt, e, row0, rows);
+        if (e < 0) return;  // beyond the last tile of the last expert
         mlim = rows;
     } else {
+        if (gi >= gm * gn) return;
         const int ntm = (p.M + BM - 1) / BM;
         const int gpe = ((ntm + gm - 1) / gm) * ngn;  // groups per expert
         const int ei = G / gpe, g = G - ei * gpe;
@@ -507,7 +568,19 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
                 }
         }
         __syncthreads();
-        if constexpr (!Tr::group_k) {
+        if (kSplitK && part_unit >= 0) {
+            // split-K part: the fp32 partial tile [BM][BN], rows < mlim
+            float* C = p.part + (int64_t)part_unit * BM * BN;
+            const int cl = lane % FLPR;
+#pragma unroll 4
+            for (int rr = lane / FLPR; rr < EPR; rr += FRPI) {
+                const int m = mbase + pass * EPR + rr;
+                const int n = nbase + cl * 4;
+                if (m >= mlim || n >= nlim) continue;
+                const f32x4 v = *reinterpret_cast<const f32x4*>(stage_f + rr * WTN + ((cl ^ (rr & (CH - 1))) * 4));
+                st16_nt(C + (int64_t)m * BN + n, v);
+            }
+        } else if constexpr (!Tr::group_k) {
             // LPR lanes per row (8 bf16 each), RPI rows per instruction
             uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
             const int cl = lane % LPR;
@@ -562,6 +635,37 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     }
 }
 
+// The split-K tail's second pass: tail tile j is the sum of its S partials
+// in part order, rounded once to bf16. Work items are (tile, 8-row slab);
+// thread t adds 8 columns of one row.
+template <int BK, int BN>
+__global__ __launch_bounds__(256) void split_fixup_kernel(GemmParams p) {
+    const int ntn = (p.N + BN - 1) / BN;
+    const SplitPlan sp = split_plan<BK>(p, ntn, act_mtiles(p));
+    if (sp.S < 2) return;
+    constexpr int kSlabs = BM / 8;
+    const int tid = threadIdx.x;
+    const int rr = tid / (BN / 8), col = (tid % (BN / 8)) * 8;  // BN = 256: 8 rows x 32 lanes of 8 columns
+    uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
+    for (int w = blockIdx.x; w < sp.R * kSlabs; w += gridDim.x) {
+        const int j = w / kSlabs, slab = w % kSlabs;
+        const int mt = sp.cut + j / ntn, nt = j % ntn;
+        int e, row0 = 0, rows = 0;
+        act_tile(p, mt, e, row0, rows);
+        const int row = slab * 8 + rr;
+        if (e < 0 || row >= rows || nt * BN + col >= p.N) continue;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        const float* src = p.part + (int64_t)j * sp.S * BM * BN + (int64_t)row * BN + col;
+        for (int q = 0; q < sp.S; ++q) {
+            const f32x4 a = *reinterpret_cast<const f32x4*>(src + (int64_t)q * BM * BN);
+            const f32x4 b = *reinterpret_cast<const f32x4*>(src + (int64_t)q * BM * BN + 4);
+            acc[0] += a[0]; acc[1] += a[1]; acc[2] += a[2]; acc[3] += a[3];
+            acc[4] += b[0]; acc[5] += b[1]; acc[6] += b[2]; acc[7] += b[3];
+        }
+        *reinterpret_cast<uint4*>(C + (int64_t)(row0 + row) * p.ldc + nt * BN + col) = pack8(acc);
+    }
+}
+
 }  // namespace
 
 constexpr int kBK = 32, kNST = 4;  // fastest of BK 32/64 x 2-4 stages on the c3 shapes
@@ -609,12 +713,25 @@ hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn,
         groups = ((mtiles + gm - 1) / gm) * ngn;
     }
     // whole rounds of 8 XCDs x 32 workgroups keep the block -> tile map a bijection
-    const int64_t grid = (groups * 32 + 255) / 256 * 256;
+    int64_t grid = (groups * 32 + 255) / 256 * 256;
+    // split-K tail (GEMM_DOWN / GEMM_DX on 256-column tiles): its parts are
+    // the workgroups after the whole rounds, at most `resident` of them.
+    const bool split = (kind == GEMM_DOWN || kind == GEMM_DX) && bn == 256 && p.part != nullptr &&
+                       p.resident > 0 && p.resident % 256 == 0;
+    if (split) grid += p.resident;
     if (grid <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     const unsigned g = (unsigned)grid;
 #define TMT_BN(KIND_, DUAL_) \
     (bn == 256 ? launch_kind<KIND_, DUAL_, 256>(p, g, s) : launch_kind<KIND_, DUAL_, 128>(p, g, s))
+    if (split) {
+        // bn == 256 here, so launch_kind runs the 256-column kernel
+        hipError_t err = kind == GEMM_DOWN ? launch_kind<GEMM_DOWN, false, 256>(p, g, s)
+                                           : launch_kind<GEMM_DX, false, 256>(p, g, s);
+        if (err != hipSuccess) return err;
+        split_fixup_kernel<kBK, 256><<<p.resident, 256, 0, s>>>(p);
+        return hipGetLastError();
+    }
     switch (kind) {
         case GEMM_UP: return dual ? TMT_BN(GEMM_UP, true) : TMT_BN(GEMM_UP, false);
         case GEMM_DOWN: return TMT_BN(GEMM_DOWN, false);

@@ -66,6 +66,8 @@ struct tmt_moe {
     // routing state (kept from forward for backward; the reference's MoeKeep)
     float *logits, *probs, *lse, *gate, *blkstat, *stats;
     int32_t* ticket = nullptr;  // decode router's completion counter (zero between calls)
+    float* split = nullptr;     // split-K partial tiles of GEMM_DOWN / GEMM_DX (nullptr: none)
+    int resident = 0;           // workgroups the GPU runs at once (one per CU)
     int32_t *idx, *blkcnt, *blkbase, *counts, *offsets, *order, *perm, *slot_of;
     // activations
     uint16_t *U, *Aact, *O, *dO, *dU, *dXg, *Xg;
@@ -149,6 +151,10 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
     size_t o_dwr = bwd ? L.add((size_t)router_dw_chunks((int)T) * E * D * 4) : 0;
     size_t o_H = L.add(T * D * 2), o_mean = L.add(T * 4), o_rstd = L.add(T * 4);
     size_t o_dH = bwd ? L.add(T * D * 2) : 0;
+    // Split-K tail of the tiled GEMM_DOWN / GEMM_DX (decode-sized handles never tile).
+    const bool split = d->weight_format == TMT_MOE_WEIGHTS_BF16 && T > kSkinnyMaxTokens;
+    const int resident = cu_count();
+    size_t o_split = split ? L.add(gemm_split_floats(resident) * 4) : 0;
     const int64_t ln_rows = std::max(scatter_blocks((int)T), ln_chunks((int)T));
     size_t o_lnp = bwd ? L.add((size_t)ln_rows * 2 * D * 4) : 0;
     size_t o_lnp2 = bwd ? L.add((size_t)colsum_groups((int)ln_rows) * 2 * D * 4) : 0;
@@ -167,6 +173,8 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->order = (int32_t*)(a + o_order);
         m->stats = (float*)(a + o_stats);
         m->ticket = (int32_t*)(a + o_ticket);
+        m->split = split ? (float*)(a + o_split) : nullptr;
+        m->resident = resident;
         m->perm = (int32_t*)(a + o_perm);
         m->slot_of = (int32_t*)(a + o_slot);
         m->U = (uint16_t*)(a + o_U);
@@ -347,6 +355,7 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
             dn.a = m->Aact; dn.lda = h; dn.c = m->O; dn.ldc = d;
             for (int e = 0; e < E; ++e) dn.w[e] = W_down[e];
             dn.ldb = h;
+            dn.part = m->split; dn.resident = m->resident;
             LAUNCH(TMT_MOE_PH_GEMM_DOWN, skinny ? launch_skinny_gemm(GEMM_DOWN, false, dn, T, s)
                                                 : launch_gemm(GEMM_DOWN, false, dn, s));
         }
@@ -445,6 +454,7 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
         dx.a = m->dU; dx.lda = hn; dx.c = m->dXg; dx.ldc = d;
         for (int e = 0; e < E; ++e) dx.w[e] = W_up[e];
         dx.ldb = d;
+        dx.part = m->split; dx.resident = m->resident;
         LAUNCH(TMT_MOE_PH_GEMM_DX, launch_gemm(GEMM_DX, false, dx, s));
     }
     if (E == 1 && dWr) {

@@ -105,8 +105,18 @@ struct GemmParams {
     float* dw[kMaxExperts];           // per-expert fp32 outputs (dW GEMMs)
     const uint8_t* wq[kMaxExperts];   // MXFP4 weights: packed e2m1 [N][K/2] (low nibble = even k)
     const uint8_t* wsc[kMaxExperts];  // MXFP4 scales: e8m0 [K/32][N]
+    // GEMM_DOWN / GEMM_DX: split-K of the last round's tiles. part holds
+    // resident * BM * BN fp32 partial tiles (nullptr: no split); resident is
+    // the number of workgroups the GPU runs at once (one per CU).
+    float* part;
+    int resident;
 };
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s);
+// Rows of an activation-GEMM tile, and the fp32 partial buffer the split-K
+// tail needs (floats) for `resident` workgroups.
+constexpr int kGemmTileRows = 256;
+inline size_t gemm_split_floats(int resident) { return (size_t)resident * kGemmTileRows * 256; }
+int cu_count();  // compute units of the current device (cached per device)
 // Same with an explicit tile width (256, or 128 = two workgroups per CU).
 hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn, hipStream_t s);
 

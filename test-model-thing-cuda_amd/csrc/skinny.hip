@@ -483,6 +483,9 @@ hipError_t launch_stream(int rb, int nw, const GemmParams& p, int nexp, int spli
     return hipGetLastError();
 }
 
+
+}  // namespace
+
 // Compute units of the current device (cached per device).
 int cu_count() {
     static int cached[64] = {};
@@ -495,8 +498,6 @@ int cu_count() {
     }
     return cached[dev];
 }
-
-}  // namespace
 
 hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s) {
     if (T <= 0) return hipSuccess;
