@@ -152,7 +152,7 @@ __global__ __launch_bounds__(kThreads) void combine_bwd_kernel(CombineBwdParams 
 constexpr int kDwExperts = 16;
 constexpr int kDwCols = 256;
 constexpr int kDwUnroll = 8;
-constexpr int kDwRows = 512;  // most rows of one chunk (router_dw_chunks)
+constexpr int kDwRows = 256;  // most rows of one chunk (router_dw_chunks); 512 workgroups at c3
 __global__ __launch_bounds__(kThreads) void router_dw_partial_kernel(RouterDwParams p) {
     __shared__ f32x4 s_part[3][kDwExperts][64];
     __shared__ f32x4 s_dl[kDwRows][kDwExperts / 4];  // the chunk's dlogits, experts e0 .. e0+15
@@ -228,22 +228,22 @@ __global__ __launch_bounds__(kThreads) void router_dw_partial_kernel(RouterDwPar
 }
 
 // Pass 2: dWr[e][k] = sum over chunks in ascending order; each thread owns
-// 4 consecutive outputs and keeps 8 chunk loads in flight.
+// one output and keeps 16 chunk loads in flight.
 __global__ __launch_bounds__(kThreads) void router_dw_reduce_kernel(RouterDwParams p) {
-    const int64_t n = (int64_t)p.E * p.d;  // a multiple of 64
-    const int64_t i = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+    const int64_t n = (int64_t)p.E * p.d;
+    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+    float s = 0.0f;
     int c = 0;
-    for (; c + 8 <= p.nchunks; c += 8) {
-        f32x4 v[8];
+    for (; c + 16 <= p.nchunks; c += 16) {
+        float v[16];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const f32x4*>(p.partial + (int64_t)(c + u) * n + i);
+        for (int u = 0; u < 16; ++u) v[u] = p.partial[(int64_t)(c + u) * n + i];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) s += v[u];
+        for (int u = 0; u < 16; ++u) s += v[u];
     }
-    for (; c < p.nchunks; ++c) s += *reinterpret_cast<const f32x4*>(p.partial + (int64_t)c * n + i);
-    *reinterpret_cast<f32x4*>(p.dWr + i) = s;
+    for (; c < p.nchunks; ++c) s += p.partial[(int64_t)c * n + i];
+    p.dWr[i] = s;
 }
 
 // Gradient of one token row over the lane's 8 columns at c0: the K expert
@@ -479,7 +479,7 @@ hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s) {
     dim3 grid1(p.nchunks, (p.d + kDwCols - 1) / kDwCols, (p.E + kDwExperts - 1) / kDwExperts);
     router_dw_partial_kernel<<<grid1, kThreads, 0, s>>>(p);
     const int64_t n = (int64_t)p.E * p.d;
-    router_dw_reduce_kernel<<<(unsigned)((n / 4 + kThreads - 1) / kThreads), kThreads, 0, s>>>(p);
+    router_dw_reduce_kernel<<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, s>>>(p);
     return hipGetLastError();
 }
 
