@@ -217,12 +217,15 @@ __global__ __launch_bounds__(kThreads) void router_dw_partial_kernel(RouterDwPar
     }
     __syncthreads();
     if (wave == 0 && cok) {
-        for (int q = 0; q < ne; ++q) {
-            f32x4 v = acc[q];
-            v += s_part[0][q][lane];
-            v += s_part[1][q][lane];
-            v += s_part[2][q][lane];
-            *reinterpret_cast<f32x4*>(p.partial + ((int64_t)chunk * E + e0 + q) * d + col) = v;
+#pragma unroll
+        for (int q = 0; q < kDwExperts; ++q) {  // fixed trip count: acc stays in registers
+            if (q < ne) {
+                f32x4 v = acc[q];
+                v += s_part[0][q][lane];
+                v += s_part[1][q][lane];
+                v += s_part[2][q][lane];
+                *reinterpret_cast<f32x4*>(p.partial + ((int64_t)chunk * E + e0 + q) * d + col) = v;
+            }
         }
     }
 }
