@@ -296,9 +296,17 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
         mlim = rows;
     } else {
         if (gi >= gm * gn) return;
+        // A group's work is proportional to its expert's count, and groups
+        // come in descending-count order. With G % 8 as the XCD, an expert
+        // whose groups fill half of the XCDs sends every following expert to
+        // the same halves in turn (c3: 74K against 57K slots per XCD). Round r
+        // hands its 8 groups to the XCDs in snake order instead (reversed on
+        // odd rounds), which keeps every XCD's sum of counts near the mean.
+        const int rnd = (int)blockIdx.x >> 8, xcd = (int)blockIdx.x & 7;
+        const int Gs = 8 * rnd + ((rnd & 1) ? 7 - xcd : xcd);
         const int ntm = (p.M + BM - 1) / BM;
         const int gpe = ((ntm + gm - 1) / gm) * ngn;  // groups per expert
-        const int ei = G / gpe, g = G - ei * gpe;
+        const int ei = Gs / gpe, g = Gs - ei * gpe;
         if (ei >= p.E) return;
         mt = (g / ngn) * gm + gi % gm;
         nt = (g % ngn) * gn + gi / gm;
