@@ -610,6 +610,23 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     constexpr int FPP = EPR / 32, PASSES = MI / FPP;  // row fragments per pass, passes
     float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (EPR * WTN);
     const int mbase = wm * WTM, nbase = wn * WTN;
+    // GEMM_DACT: the pre-activations of every pass are requested here, in one
+    // batch, so the tile waits for one memory round trip instead of one per
+    // pass (the mainloop's operand fragments are dead, which leaves room).
+    constexpr int UPP = KIND == GEMM_DACT ? EPR / RPI : 1;  // U loads per lane and pass
+    uint4 uin[KIND == GEMM_DACT ? PASSES : 1][UPP];
+    if constexpr (KIND == GEMM_DACT && !Tr::group_k) {
+        const int n = nbase + (lane % LPR) * 8;
+#pragma unroll
+        for (int pass = 0; pass < PASSES; ++pass)
+#pragma unroll
+            for (int k = 0; k < UPP; ++k) {
+                const int m = mbase + pass * EPR + lane / LPR + RPI * k;
+                const bool ok = m < mlim && n < nlim;
+                const int64_t off = (int64_t)(row0 + (ok ? m : 0)) * p.ldc + nt * BN + (ok ? n : 0);
+                uin[pass][k] = ld16_nt(p.u + off);
+            }
+    }
 #pragma unroll
     for (int pass = 0; pass < PASSES; ++pass) {
 #pragma unroll
@@ -644,16 +661,6 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
             uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
             const int cl = lane % LPR;
             const int n = nbase + cl * 8;
-            uint4 uin[EPR / RPI];  // GEMM_DACT: pre-activations, all loads issued first
-            if constexpr (KIND == GEMM_DACT) {
-#pragma unroll
-                for (int k = 0; k < EPR / RPI; ++k) {
-                    const int m = mbase + pass * EPR + lane / LPR + RPI * k;
-                    const bool ok = m < mlim && n < nlim;
-                    const int64_t off = (int64_t)(row0 + (ok ? m : 0)) * p.ldc + nt * BN + (ok ? n : 0);
-                    uin[k] = ld16_nt(p.u + off);
-                }
-            }
 #pragma unroll
             for (int k = 0; k < EPR / RPI; ++k) {
                 const int rr = lane / LPR + RPI * k;
@@ -666,7 +673,7 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
                 const int64_t off = (int64_t)(row0 + m) * p.ldc + nt * BN + n;
                 if constexpr (KIND == GEMM_DACT) {
                     float u[8];
-                    unpack8(uin[k], u);
+                    unpack8(uin[pass][k], u);
 #pragma unroll
                     for (int t = 0; t < 8; ++t) v[t] *= dsilu_fast(u[t]);
                 }
