@@ -74,42 +74,55 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(CombineParams p) {
     }
 }
 
-template <bool SILU>
+// One pass over the row's 512-column chunks: each chunk of dY and X is loaded
+// once for all K picks (re-reading them per pick missed in L2 behind the
+// dO / Xg stores), with the K gathered O chunks in flight together. Each
+// pick's partial dot product still runs over the chunks in ascending order.
+template <bool SILU, int K>
 __global__ __launch_bounds__(kThreads) void combine_bwd_kernel(CombineBwdParams p) {
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= p.T) return;
-    const int d = p.d, K = p.K, E = p.E;
-    float s[kMaxTopK];
+    const int d = p.d, E = p.E;
+    int64_t pos[K];
+    float gj[K], part[K];
 #pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < K) {
-            const int64_t pos = p.slot_of[(int64_t)r * K + j];
-            const float g = p.gate[(int64_t)r * K + j];
-            float part = 0.0f;
-            for (int c0 = lane * 8; c0 < d; c0 += 512) {
-                float dy[8], o[8], out[8];
-                unpack8(*reinterpret_cast<const uint4*>(p.dY + (int64_t)r * d + c0), dy);
-                unpack8(*reinterpret_cast<const uint4*>(p.O + pos * d + c0), o);
+    for (int j = 0; j < K; ++j) {
+        pos[j] = p.slot_of[(int64_t)r * K + j];
+        gj[j] = p.gate[(int64_t)r * K + j];
+        part[j] = 0.0f;
+    }
+    for (int c0 = lane * 8; c0 < d; c0 += 512) {
+        const uint4 dyv = *reinterpret_cast<const uint4*>(p.dY + (int64_t)r * d + c0);
+        const uint4 xv = *reinterpret_cast<const uint4*>(p.X + (int64_t)r * d + c0);
+        uint4 ov[K];
 #pragma unroll
-                for (int t = 0; t < 8; ++t) {
-                    if (SILU) {
-                        // Reference experts: gradient through the SiLU applied in
-                        // combine (combine_bwd_kernel, moe.cu:162-176).
-                        part += dy[t] * silu_fast(o[t]);
-                        out[t] = g * dy[t] * dsilu_fast(o[t]);
-                    } else {
-                        part += dy[t] * o[t];
-                        out[t] = g * dy[t];
-                    }
+        for (int j = 0; j < K; ++j) ov[j] = *reinterpret_cast<const uint4*>(p.O + pos[j] * d + c0);
+        float dy[8];
+        unpack8(dyv, dy);
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            float o[8], out[8];
+            unpack8(ov[j], o);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                if (SILU) {
+                    // Reference experts: gradient through the SiLU applied in
+                    // combine (combine_bwd_kernel, moe.cu:162-176).
+                    part[j] += dy[t] * silu_fast(o[t]);
+                    out[t] = gj[j] * dy[t] * dsilu_fast(o[t]);
+                } else {
+                    part[j] += dy[t] * o[t];
+                    out[t] = gj[j] * dy[t];
                 }
-                *reinterpret_cast<uint4*>(p.dO + pos * d + c0) = pack8(out);
-                *reinterpret_cast<uint4*>(p.Xg + pos * d + c0) =
-                    *reinterpret_cast<const uint4*>(p.X + (int64_t)r * d + c0);
             }
-            s[j] = wave_sum(part);
+            *reinterpret_cast<uint4*>(p.dO + pos[j] * d + c0) = pack8(out);
+            *reinterpret_cast<uint4*>(p.Xg + pos[j] * d + c0) = xv;
         }
     }
+    float s[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) s[j] = wave_sum(part[j]);
     if (E <= 1) return;
 
     // Router backward for row r, lane e (router_bwd_kernel, moe.cu:199-234).
@@ -117,19 +130,19 @@ __global__ __launch_bounds__(kThreads) void combine_bwd_kernel(CombineBwdParams 
     const bool ev = e < E;
     const float pe = ev ? p.probs[(int64_t)r * E + e] : 0.0f;
     float Z = 0.0f, sp = 0.0f, g = 0.0f;
+    int ej[K];
 #pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < K) {
-            const int ej = p.idx[(int64_t)r * K + j];
-            const float pj = p.probs[(int64_t)r * E + ej];
-            Z += pj;
-            sp += s[j] * pj;
-        }
+    for (int j = 0; j < K; ++j) ej[j] = p.idx[(int64_t)r * K + j];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        const float pj = p.probs[(int64_t)r * E + ej[j]];
+        Z += pj;
+        sp += s[j] * pj;
     }
     const float Z2 = Z * Z + 1e-12f;
 #pragma unroll
-    for (int j = 0; j < kMaxTopK; ++j) {
-        if (j < K && p.idx[(int64_t)r * K + j] == e) g = (s[j] * Z - sp) / Z2;
+    for (int j = 0; j < K; ++j) {
+        if (ej[j] == e) g = (s[j] * Z - sp) / Z2;
     }
     const float inv_tk = 1.0f / ((float)p.T * (float)K);
     const float frac = ev ? (float)p.counts[e] * inv_tk : 0.0f;
@@ -467,8 +480,21 @@ hipError_t launch_combine(const CombineParams& p, hipStream_t s) {
 hipError_t launch_combine_bwd(const CombineBwdParams& p, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     const int grid = (p.T + 3) / 4;
-    if (p.silu) combine_bwd_kernel<true><<<grid, kThreads, 0, s>>>(p);
-    else combine_bwd_kernel<false><<<grid, kThreads, 0, s>>>(p);
+    switch (p.K * 2 + (p.silu ? 1 : 0)) {
+#define TMT_COMBINE_BWD(KK)                                                       \
+    case 2 * KK: combine_bwd_kernel<false, KK><<<grid, kThreads, 0, s>>>(p); break; \
+    case 2 * KK + 1: combine_bwd_kernel<true, KK><<<grid, kThreads, 0, s>>>(p); break;
+        TMT_COMBINE_BWD(1)
+        TMT_COMBINE_BWD(2)
+        TMT_COMBINE_BWD(3)
+        TMT_COMBINE_BWD(4)
+        TMT_COMBINE_BWD(5)
+        TMT_COMBINE_BWD(6)
+        TMT_COMBINE_BWD(7)
+        TMT_COMBINE_BWD(8)
+#undef TMT_COMBINE_BWD
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
