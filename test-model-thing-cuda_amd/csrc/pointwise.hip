@@ -512,6 +512,88 @@ hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Variant without the LayerNorm: each wave keeps RPW rows in flight (rows
+// w, w + 4, ..., of the workgroup's slice in groups of RPW): the K gathered
+// dXg chunks of all RPW rows are loaded together, and each staged Wr chunk is
+// unpacked once for the RPW rows. K is a template argument so that every
+// load is issued unconditionally. Per row the sum runs in the same order as
+// scatter_chunk (picks j ascending, then experts e ascending).
+namespace {
+constexpr int kScatterRowsPerWave = 4;
+template <bool ROUTER, int K>
+__global__ __launch_bounds__(kThreads) void scatter_rows_kernel(ScatterParams p, int rows_per_block) {
+    extern __shared__ uint4 smem_w[];
+    constexpr int RPW = kScatterRowsPerWave;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d = p.d, E = p.E;
+    const int rbeg = blockIdx.x * rows_per_block;
+    const int rend = min(p.T, rbeg + rows_per_block);
+    float* s_dl = reinterpret_cast<float*>(smem_w + (ROUTER ? E * d / 8 : 0));  // [rows_per_block][E]
+    if (ROUTER) {
+        const uint4* src = reinterpret_cast<const uint4*>(p.Wr);
+        const int nvec = E * d / 8;
+        for (int i0 = threadIdx.x; i0 < nvec; i0 += 8 * kThreads) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = src[min(i0 + u * kThreads, nvec - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (i0 + u * kThreads < nvec) smem_w[i0 + u * kThreads] = v[u];
+        }
+        const int ndl = (rend - rbeg) * E;
+        for (int i = threadIdx.x; i < ndl; i += kThreads) s_dl[i] = p.dlogits[(int64_t)rbeg * E + i];
+        __syncthreads();
+    }
+    const uint16_t* wl = reinterpret_cast<const uint16_t*>(smem_w);
+    for (int r = rbeg + wave; r < rend; r += 4 * RPW) {
+        int row[RPW], pos[RPW][K];
+        bool ok[RPW];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+            ok[i] = r + 4 * i < rend;
+            row[i] = ok[i] ? r + 4 * i : r;  // clamped: a row past the slice is loaded, not stored
+#pragma unroll
+            for (int j = 0; j < K; ++j) pos[i][j] = p.slot_of[(int64_t)row[i] * K + j];
+        }
+        for (int c0 = lane * 8; c0 < d; c0 += 512) {
+            uint4 xv[RPW][K];
+#pragma unroll
+            for (int i = 0; i < RPW; ++i)
+#pragma unroll
+                for (int j = 0; j < K; ++j) xv[i][j] = *reinterpret_cast<const uint4*>(p.dXg + (int64_t)pos[i][j] * d + c0);
+            float acc[RPW][8];
+#pragma unroll
+            for (int i = 0; i < RPW; ++i) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) acc[i][t] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < K; ++j) {
+                    float v[8];
+                    unpack8(xv[i][j], v);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) acc[i][t] += v[t];
+                }
+            }
+            if (ROUTER) {
+                for (int e = 0; e < E; ++e) {
+                    float w[8];
+                    unpack8(*reinterpret_cast<const uint4*>(wl + e * d + c0), w);
+#pragma unroll
+                    for (int i = 0; i < RPW; ++i) {
+                        const float g = s_dl[(row[i] - rbeg) * E + e];
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) acc[i][t] += g * w[t];
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < RPW; ++i)
+                if (ok[i]) *reinterpret_cast<uint4*>(p.dX + (int64_t)row[i] * d + c0) = pack8(acc[i]);
+        }
+    }
+}
+}  // namespace
+
 int scatter_blocks(int T) {
     const int b = (T + kScatterRows - 1) / kScatterRows;
     return b < 1 ? 1 : b;
@@ -568,6 +650,26 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
     size_t lds = router ? (size_t)p.E * p.d * 2 + (size_t)rows * p.E * 4 : 0;
     if (ln && !(router && p.E >= kRedOnWrExperts)) lds += (size_t)3 * 2 * p.d * 4;
     const int ni = ln ? (p.d + 511) / 512 : 0;
+    if (ni == 0) {
+        const int rrows = router ? kScatterRows : 4 * kScatterRowsPerWave;
+        const int grid = (p.T + rrows - 1) / rrows;
+        switch (p.K * 2 + (router ? 1 : 0)) {
+#define TMT_SCATTER_ROWS(KK)                                                                   \
+    case 2 * KK: scatter_rows_kernel<false, KK><<<grid, kThreads, 0, s>>>(p, rrows); break;      \
+    case 2 * KK + 1: scatter_rows_kernel<true, KK><<<grid, kThreads, lds, s>>>(p, rrows); break;
+            TMT_SCATTER_ROWS(1)
+            TMT_SCATTER_ROWS(2)
+            TMT_SCATTER_ROWS(3)
+            TMT_SCATTER_ROWS(4)
+            TMT_SCATTER_ROWS(5)
+            TMT_SCATTER_ROWS(6)
+            TMT_SCATTER_ROWS(7)
+            TMT_SCATTER_ROWS(8)
+#undef TMT_SCATTER_ROWS
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     return router ? launch_scatter_ni<true>(p, ni, rows, lds, s) : launch_scatter_ni<false>(p, ni, rows, lds, s);
 }
 
