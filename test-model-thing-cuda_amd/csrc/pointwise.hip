@@ -520,6 +520,9 @@ hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s) {
 // scatter_chunk (picks j ascending, then experts e ascending).
 namespace {
 constexpr int kScatterRowsPerWave = 4;
+// Rows per workgroup of the router variant: 32 gives 1024 workgroups at
+// T = 32768, four per CU (LDS: E*d*2 bytes of Wr + 32*E*4 of dlogits).
+constexpr int kScatterRowsRouter = 32;
 template <bool ROUTER, int K>
 __global__ __launch_bounds__(kThreads) void scatter_rows_kernel(ScatterParams p, int rows_per_block) {
     extern __shared__ uint4 smem_w[];
@@ -651,12 +654,13 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
     if (ln && !(router && p.E >= kRedOnWrExperts)) lds += (size_t)3 * 2 * p.d * 4;
     const int ni = ln ? (p.d + 511) / 512 : 0;
     if (ni == 0) {
-        const int rrows = router ? kScatterRows : 4 * kScatterRowsPerWave;
+        const int rrows = router ? kScatterRowsRouter : 4 * kScatterRowsPerWave;
         const int grid = (p.T + rrows - 1) / rrows;
+        const size_t rlds = router ? (size_t)p.E * p.d * 2 + (size_t)rrows * p.E * 4 : 0;
         switch (p.K * 2 + (router ? 1 : 0)) {
 #define TMT_SCATTER_ROWS(KK)                                                                   \
     case 2 * KK: scatter_rows_kernel<false, KK><<<grid, kThreads, 0, s>>>(p, rrows); break;      \
-    case 2 * KK + 1: scatter_rows_kernel<true, KK><<<grid, kThreads, lds, s>>>(p, rrows); break;
+    case 2 * KK + 1: scatter_rows_kernel<true, KK><<<grid, kThreads, rlds, s>>>(p, rrows); break;
             TMT_SCATTER_ROWS(1)
             TMT_SCATTER_ROWS(2)
             TMT_SCATTER_ROWS(3)
