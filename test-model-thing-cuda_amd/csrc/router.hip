@@ -319,11 +319,19 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanParams p) {
     // 1) per (segment, expert) sums of the block histograms
     const int S = 1024 / E;
     const int chunk = (nblk + S - 1) / S;
+    // (Loads in batches of 8 at clamped addresses, added in ascending order:
+    // one memory round trip per batch instead of one per block.)
     if (tid < S * E) {
         const int e = tid % E, seg = tid / E;
         const int b0 = seg * chunk, b1 = min(nblk, b0 + chunk);
         int sum = 0;
-        for (int b = b0; b < b1; ++b) sum += p.blkcnt[(int64_t)b * E + e];
+        for (int b = b0; b < b1; b += 8) {
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p.blkcnt[(int64_t)min(b + u, b1 - 1) * E + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) sum += b + u < b1 ? v[u] : 0;
+        }
         s_seg[seg * E + e] = sum;
     }
     // 1b) per (segment, statistic) sums of the block statistics
@@ -334,23 +342,44 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanParams p) {
         const int q = tid % E1, seg = tid / E1;
         const int b0 = seg * chunk2, b1 = min(nblk, b0 + chunk2);
         float sum = 0.0f;
-        for (int b = b0; b < b1; ++b) sum += p.blkstat[(int64_t)b * E1 + q];
+        for (int b = b0; b < b1; b += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p.blkstat[(int64_t)min(b + u, b1 - 1) * E1 + q];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (b + u < b1) sum += v[u];
+        }
         s_fseg[seg * E1 + q] = sum;
     }
     __syncthreads();
     // 2) exclusive scan over segments, per expert
     if (tid < E) {
         int run = 0;
-        for (int seg = 0; seg < S; ++seg) {
-            const int c = s_seg[seg * E + tid];
-            s_seg[seg * E + tid] = run;
-            run += c;
+        for (int seg0 = 0; seg0 < S; seg0 += 8) {
+            int c[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c[u] = s_seg[min(seg0 + u, S - 1) * E + tid];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (seg0 + u < S) {
+                    s_seg[(seg0 + u) * E + tid] = run;
+                    run += c[u];
+                }
+            }
         }
         s_cnt[tid] = run;
     }
     if (tid < E1) {
         float run = 0.0f;
-        for (int seg = 0; seg < S2; ++seg) run += s_fseg[seg * E1 + tid];
+        for (int seg0 = 0; seg0 < S2; seg0 += 8) {
+            float c[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) c[u] = s_fseg[min(seg0 + u, S2 - 1) * E1 + tid];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (seg0 + u < S2) run += c[u];
+        }
         s_fsum[tid] = run;
     }
     __syncthreads();
@@ -388,9 +417,17 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanParams p) {
         const int e = tid % E, seg = tid / E;
         const int b0 = seg * chunk, b1 = min(nblk, b0 + chunk);
         int run = s_off[e] + s_seg[seg * E + e];
-        for (int b = b0; b < b1; ++b) {
-            p.blkbase[(int64_t)b * E + e] = run;
-            run += p.blkcnt[(int64_t)b * E + e];
+        for (int b = b0; b < b1; b += 8) {
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = p.blkcnt[(int64_t)min(b + u, b1 - 1) * E + e];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (b + u < b1) {
+                    p.blkbase[(int64_t)(b + u) * E + e] = run;
+                    run += v[u];
+                }
+            }
         }
     }
 }

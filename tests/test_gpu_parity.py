@@ -151,8 +151,8 @@ def test_c1_backward_against_oracle(orc):
     (500, 1024, 32, 4, 256),   # the c5 router shape
     (129, 128, 3, 3, 128),     # E == K, odd expert count
     (333, 192, 5, 2, 320),     # d and h not multiples of the 256-wide GEMM tile
-    (6, 256, 8, 2, 512),       # decode-sized: fused down+combine, then the backward reads O
-    (8, 1024, 16, 4, 4096),    # c3 weights at T = 8 (fused), forward + backward
+    (6, 256, 8, 2, 512),       # decode-sized: skinny expert GEMMs forward, tiled GEMMs backward
+    (8, 1024, 16, 4, 4096),    # c3 weights at T = 8 (persistent skinny forward), forward + backward
 ])
 def test_shapes_against_oracle(orc, T, d, E, K, h):
     say(f"shape T={T} d={d} E={E} K={K} h={h} fwd+bwd")
