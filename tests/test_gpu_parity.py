@@ -153,6 +153,8 @@ def test_c1_backward_against_oracle(orc):
     (333, 192, 5, 2, 320),     # d and h not multiples of the 256-wide GEMM tile
     (6, 256, 8, 2, 512),       # decode-sized: skinny expert GEMMs forward, tiled GEMMs backward
     (8, 1024, 16, 4, 4096),    # c3 weights at T = 8 (persistent skinny forward), forward + backward
+    (211, 256, 12, 6, 256),    # top-6: the K = 6 combine / combine_bwd / scatter instantiations
+    (97, 128, 7, 5, 128),      # top-5 over 7 experts, T below one router block
 ])
 def test_shapes_against_oracle(orc, T, d, E, K, h):
     say(f"shape T={T} d={d} E={E} K={K} h={h} fwd+bwd")
