@@ -67,6 +67,7 @@ struct tmt_moe {
     float *logits, *probs, *lse, *gate, *blkstat, *stats;
     int32_t* ticket = nullptr;  // decode router's completion counter (zero between calls)
     float* split = nullptr;     // split-K partial tiles of GEMM_DOWN / GEMM_DX (nullptr: none)
+    float* dpart = nullptr;     // decode GEMM_DOWN: fp32 rows of the two K halves (nullptr: none)
     int resident = 0;           // workgroups the GPU runs at once (one per CU)
     int32_t *idx, *blkcnt, *blkbase, *counts, *offsets, *order, *perm, *slot_of;
     // activations
@@ -155,6 +156,9 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
     const bool split = d->weight_format == TMT_MOE_WEIGHTS_BF16 && T > kSkinnyMaxTokens;
     const int resident = cu_count();
     size_t o_split = split ? L.add(gemm_split_floats(resident) * 4) : 0;
+    // Decode GEMM_DOWN in K halves: [2][min(T, 64) * K][d] fp32.
+    const bool dsplit = d->weight_format == TMT_MOE_WEIGHTS_BF16 && h > 0;
+    size_t o_dpart = dsplit ? L.add((size_t)2 * std::min<int64_t>(T, kSkinnyMaxTokens) * K * D * 4) : 0;
     const int64_t ln_rows = std::max(scatter_blocks((int)T), ln_chunks((int)T));
     size_t o_lnp = bwd ? L.add((size_t)ln_rows * 2 * D * 4) : 0;
     size_t o_lnp2 = bwd ? L.add((size_t)colsum_groups((int)ln_rows) * 2 * D * 4) : 0;
@@ -174,6 +178,7 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->stats = (float*)(a + o_stats);
         m->ticket = (int32_t*)(a + o_ticket);
         m->split = split ? (float*)(a + o_split) : nullptr;
+        m->dpart = dsplit ? (float*)(a + o_dpart) : nullptr;
         m->resident = resident;
         m->perm = (int32_t*)(a + o_perm);
         m->slot_of = (int32_t*)(a + o_slot);
@@ -346,6 +351,7 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
         up.ldb = d;
         // Decode-sized batches stream the weights with the skinny kernel.
         const bool skinny = T <= kSkinnyMaxTokens;
+        bool halves = false;  // decode GEMM_DOWN wrote fp32 K halves instead of O
         LAUNCH(TMT_MOE_PH_GEMM_UP, skinny ? launch_skinny_gemm(GEMM_UP, h > 0, up, T, s)
                                           : launch_gemm(GEMM_UP, h > 0, up, s));
         if (h > 0) {
@@ -356,12 +362,16 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
             for (int e = 0; e < E; ++e) dn.w[e] = W_down[e];
             dn.ldb = h;
             dn.part = m->split; dn.resident = m->resident;
-            LAUNCH(TMT_MOE_PH_GEMM_DOWN, skinny ? launch_skinny_gemm(GEMM_DOWN, false, dn, T, s)
+            dn.dpart = skinny ? m->dpart : nullptr;
+            LAUNCH(TMT_MOE_PH_GEMM_DOWN, skinny ? launch_skinny_gemm(GEMM_DOWN, false, dn, T, s, &halves)
                                                 : launch_gemm(GEMM_DOWN, false, dn, s));
         }
         CombineParams cp{};
         cp.O = h > 0 ? m->O : m->U; cp.slot_of = m->slot_of; cp.gate = m->gate;
         cp.Y = Y; cp.beta = beta; cp.T = T; cp.d = d; cp.K = K; cp.silu = h == 0;
+        if (halves) {  // the decode GEMM_DOWN left two fp32 K halves; O is formed here
+            cp.part = m->dpart; cp.O_out = m->O; cp.slots = T * K;
+        }
         LAUNCH(TMT_MOE_PH_COMBINE, launch_combine(cp, s));
     }
     m->last_T = T;

@@ -110,6 +110,9 @@ struct GemmParams {
     // the number of workgroups the GPU runs at once (one per CU).
     float* part;
     int resident;
+    // Decode GEMM_DOWN (skinny kernels): [2][slots][N] fp32 buffer for a
+    // split of K into two halves (nullptr: no split).
+    float* dpart;
 };
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s);
 // Rows of an activation-GEMM tile, and the fp32 partial buffer the split-K
@@ -123,7 +126,11 @@ hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn,
 // Decode-sized forward GEMMs (GEMM_UP / GEMM_DOWN, bf16 weights) for
 // T <= kSkinnyMaxTokens tokens: every expert then owns at most T rows.
 constexpr int kSkinnyMaxTokens = 64;
-hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s);
+// With p.dpart set, GEMM_DOWN may split K in halves (*halves = true): the
+// outputs are then the two fp32 partial rows in p.dpart, not bf16 rows in
+// p.c, and the combine adds them (CombineParams::part).
+hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s,
+                              bool* halves = nullptr);
 
 // ------------------------------------------------------------- pointwise --
 struct CombineParams {
@@ -134,6 +141,12 @@ struct CombineParams {
     float beta;
     int T, d, K;
     int silu;                // 1: apply SiLU to O (hidden == 0)
+    // Decode GEMM_DOWN split in K halves: O[slot] = bf16(part[0][slot] +
+    // part[1][slot]) is formed here and also stored to O_out (nullptr part:
+    // O is read as is).
+    const float* part;       // [2][slots][d]
+    uint16_t* O_out;         // [slots][d]
+    int slots;
 };
 hipError_t launch_combine(const CombineParams& p, hipStream_t s);
 

@@ -74,6 +74,63 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(CombineParams p) {
     }
 }
 
+// Decode GEMM_DOWN split in K halves: O[slot] = bf16(part[0][slot] +
+// part[1][slot]) is formed (and stored for the backward), then combined as in
+// combine_kernel<false, K> with the rounded values. One 512-column chunk per
+// pass, every load of the pass issued first.
+template <int K>
+__global__ __launch_bounds__(kThreads) void combine_part_kernel(CombineParams p) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= p.T) return;
+    const int d = p.d;
+    const int64_t half = (int64_t)p.slots * d;
+    int64_t pos[K];
+    float g[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        pos[j] = p.slot_of[(int64_t)r * K + j];
+        g[j] = p.gate[(int64_t)r * K + j];
+    }
+    const bool resid = p.beta != 0.0f;
+    for (int c0 = lane * 8; c0 < d; c0 += 512) {
+        const uint4 yv = resid ? *reinterpret_cast<const uint4*>(p.Y + (int64_t)r * d + c0) : make_uint4(0, 0, 0, 0);
+        f32x4 a[K][4];
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const float* q = p.part + pos[j] * d + c0;
+            a[j][0] = *reinterpret_cast<const f32x4*>(q);
+            a[j][1] = *reinterpret_cast<const f32x4*>(q + 4);
+            a[j][2] = *reinterpret_cast<const f32x4*>(q + half);
+            a[j][3] = *reinterpret_cast<const f32x4*>(q + half + 4);
+        }
+        float acc[8];
+        if (resid) {
+            unpack8(yv, acc);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc[t] *= p.beta;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc[t] = 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            float s8[8], o[8];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                s8[t] = a[j][0][t] + a[j][2][t];
+                s8[t + 4] = a[j][1][t] + a[j][3][t];
+            }
+            const uint4 ob = pack8(s8);
+            *reinterpret_cast<uint4*>(p.O_out + pos[j] * d + c0) = ob;
+            unpack8(ob, o);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) acc[t] += g[j] * o[t];
+        }
+        *reinterpret_cast<uint4*>(p.Y + (int64_t)r * d + c0) = pack8(acc);
+    }
+}
+
 // One pass over the row's 512-column chunks: each chunk of dY and X is loaded
 // once for all K picks (re-reading them per pick missed in L2 behind the
 // dO / Xg stores), with the K gathered O chunks in flight together. Each
@@ -459,6 +516,21 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterParams p, int 
 hipError_t launch_combine(const CombineParams& p, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     const int grid = (p.T + 3) / 4;
+    if (p.part != nullptr) {
+        if (p.silu || p.O_out == nullptr || p.slots != p.T * p.K) return hipErrorInvalidValue;
+        switch (p.K) {
+            case 1: combine_part_kernel<1><<<grid, kThreads, 0, s>>>(p); break;
+            case 2: combine_part_kernel<2><<<grid, kThreads, 0, s>>>(p); break;
+            case 3: combine_part_kernel<3><<<grid, kThreads, 0, s>>>(p); break;
+            case 4: combine_part_kernel<4><<<grid, kThreads, 0, s>>>(p); break;
+            case 5: combine_part_kernel<5><<<grid, kThreads, 0, s>>>(p); break;
+            case 6: combine_part_kernel<6><<<grid, kThreads, 0, s>>>(p); break;
+            case 7: combine_part_kernel<7><<<grid, kThreads, 0, s>>>(p); break;
+            case 8: combine_part_kernel<8><<<grid, kThreads, 0, s>>>(p); break;
+            default: return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
     switch (p.K * 2 + (p.silu ? 1 : 0)) {
 #define TMT_COMBINE(KK)                                                       \
     case 2 * KK: combine_kernel<false, KK><<<grid, kThreads, 0, s>>>(p); break; \

@@ -339,9 +339,15 @@ __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int ne
 // Lane/k assignment, MFMA order and wave order of the sums are the chunk
 // kernel's, so the results are bit-identical to it. A past-the-end tile reads
 // zeros from the buffer resource without touching memory.
-template <int KIND, bool DUAL, int RB, int NWMAX>
+//
+// KS = 2 (GEMM_DOWN with K = 16 * 256 and more than 16 rows): K is split in
+// two halves over twice the workgroups, (rank, s, half), so that 8 waves hold
+// the rows of one half; each half's sums (wave order) are stored as fp32 rows
+// of p.dpart and the combine adds the halves.
+template <int KIND, bool DUAL, int RB, int NWMAX, int KS = 1>
 __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p, int nexp, int split) {
     static_assert(KIND == GEMM_UP || KIND == GEMM_DOWN, "forward GEMMs only");
+    static_assert(KS == 1 || (KS == 2 && KIND == GEMM_DOWN && !DUAL), "K halves: GEMM_DOWN only");
     constexpr bool kGather = KIND == GEMM_UP;
     constexpr int J = 8;
     extern __shared__ f32x4 red[];  // [RB][nw][64] wave partials
@@ -350,7 +356,8 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
     const int nw = (int)blockDim.x >> 6;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rank = (int)blockIdx.x % nexp, s0 = (int)blockIdx.x / nexp;
+    const int rank = (int)blockIdx.x % nexp, sq = (int)blockIdx.x / nexp;
+    const int s0 = KS == 1 ? sq : sq % split, half = KS == 1 ? 0 : sq / split;
     args_in_sgprs(p.order, p.offsets, p.idx, p.a, p.c, p.c2, p.E, p.N, p.slots, p.topk, p.lda, p.ldb, p.ldc);
     int ent[kPickGroups];
     if constexpr (kGather) load_picks(p, lane, ent);
@@ -361,7 +368,7 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
     if (rows <= 0 || s0 >= ntile) return;
     const int nrb = (rows + 15) >> 4;
     const int g = lane >> 4, li = lane & 15;
-    const int kw = wave * (32 * J) + g * 8;
+    const int kw = half * nw * (32 * J) + wave * (32 * J) + g * 8;
 
     // The expert's weights [N][K] as one buffer (below 2 GiB: checked by the host).
     const int wbytes = p.N * (int)p.ldb * 2;
@@ -412,9 +419,13 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
             const int sl = (n >> 2) * 16 + m, r = n & 3;
             float v = red[(rb * nw) * 64 + sl][r];
             for (int w2 = 1; w2 < nw; ++w2) v += red[(rb * nw + w2) * 64 + sl][r];
-            const int64_t off = (int64_t)(row0 + row) * p.ldc + tile * 16 + n;
-            C[off] = f2bf(v);
-            if constexpr (DUAL) p.c2[off] = f2bf(silu_fast(v));
+            if constexpr (KS == 2) {
+                p.dpart[((int64_t)half * p.slots + row0 + row) * p.N + tile * 16 + n] = v;
+            } else {
+                const int64_t off = (int64_t)(row0 + row) * p.ldc + tile * 16 + n;
+                C[off] = f2bf(v);
+                if constexpr (DUAL) p.c2[off] = f2bf(silu_fast(v));
+            }
         }
         __syncthreads();
     };
@@ -464,6 +475,19 @@ hipError_t launch_chunk(int J, int ct, int rb, int nw, const GemmParams& p, int 
                   : launch_chunk_rb<KIND, DUAL, 2, 1>(rb, nw, p, nexp, s);
 }
 
+// GEMM_DOWN with K in two halves of 8 waves (rows of up to 64 tokens).
+hipError_t launch_stream_halves(int rb, const GemmParams& p, int nexp, int split, hipStream_t s) {
+    const unsigned grid = 2u * (unsigned)split * (unsigned)nexp;
+    const dim3 block(64 * 8);
+    const size_t lds = (size_t)rb * 8 * 64 * sizeof(f32x4);
+    switch (rb) {
+        case 2: skinny_stream_kernel<GEMM_DOWN, false, 2, 8, 2><<<grid, block, lds, s>>>(p, nexp, split); break;
+        case 4: skinny_stream_kernel<GEMM_DOWN, false, 4, 8, 2><<<grid, block, lds, s>>>(p, nexp, split); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 template <int KIND, bool DUAL>
 hipError_t launch_stream(int rb, int nw, const GemmParams& p, int nexp, int split, hipStream_t s) {
     const unsigned grid = (unsigned)split * (unsigned)nexp;
@@ -499,7 +523,9 @@ int cu_count() {
     return cached[dev];
 }
 
-hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s) {
+hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s,
+                              bool* halves) {
+    if (halves != nullptr) *halves = false;
     if (T <= 0) return hipSuccess;
     if (T > kSkinnyMaxTokens || p.N % 16 != 0 || p.K % 64 != 0 || p.N <= 0) return hipErrorInvalidValue;
     if (kind != GEMM_UP && kind != GEMM_DOWN) return hipErrorInvalidValue;
@@ -526,6 +552,16 @@ hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int
             return dual ? launch_stream<GEMM_UP, true>(rb, nw, p, nexp, split, s)
                         : launch_stream<GEMM_UP, false>(rb, nw, p, nexp, split, s);
         return launch_stream<GEMM_DOWN, false>(rb, nw, p, nexp, split, s);
+    }
+    // GEMM_DOWN over 16 waves with more than one row block: two K halves of
+    // 8 waves each keep the rows resident (one 8-wave workgroup per CU).
+    if (kind == GEMM_DOWN && J == 8 && nw == 16 && rb > 1 && T >= kSkinnyStreamTokens && p.dpart != nullptr &&
+        halves != nullptr && (int64_t)p.N * p.ldb * 2 < (1ll << 31)) {
+        const int ntile = p.N / 16;
+        int split = (cu_count() + 2 * nexp - 1) / (2 * nexp);
+        split = split < 1 ? 1 : (split > ntile ? ntile : split);
+        *halves = true;
+        return launch_stream_halves(rb, p, nexp, split, s);
     }
     if (J > 0) {
         const int ct = (T >= kSkinnyTwoTileTokens && p.N % 32 == 0) ? 2 : 1;

@@ -155,6 +155,7 @@ def test_c1_backward_against_oracle(orc):
     (8, 1024, 16, 4, 4096),    # c3 weights at T = 8 (persistent skinny forward), forward + backward
     (211, 256, 12, 6, 256),    # top-6: the K = 6 combine / combine_bwd / scatter instantiations
     (97, 128, 7, 5, 128),      # top-5 over 7 experts, T below one router block
+    (40, 256, 8, 2, 4096),     # decode DOWN in two K halves (combine forms O), then the backward reads O
 ])
 def test_shapes_against_oracle(orc, T, d, E, K, h):
     say(f"shape T={T} d={d} E={E} K={K} h={h} fwd+bwd")
