@@ -255,13 +255,17 @@ __global__ __launch_bounds__(kThreads) void router_dw_partial_kernel(RouterDwPar
     f32x4 acc[kDwExperts];
 #pragma unroll
     for (int q = 0; q < kDwExperts; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int rb = wave; rb < nr; rb += 4 * kDwUnroll) {
-        uint2 xv[kDwUnroll];
+    // Two alternating 8-row register sets: the next batch's X loads are in
+    // flight while the current batch is multiplied (addresses clamped to the
+    // chunk's last row; rows past the chunk are skipped).
+    auto xload = [&](int rb, uint2 (&xv)[kDwUnroll]) {
 #pragma unroll
         for (int u = 0; u < kDwUnroll; ++u) {
-            const int rr = min(rb + 4 * u, nr - 1);  // clamped; rows past the chunk are skipped below
+            const int rr = min(rb + 4 * u, nr - 1);
             xv[u] = *reinterpret_cast<const uint2*>(p.X + (int64_t)(r0 + rr) * d + ccol);
         }
+    };
+    auto xmul = [&](int rb, const uint2 (&xv)[kDwUnroll]) {
 #pragma unroll
         for (int u = 0; u < kDwUnroll; ++u) {
             const int rr = rb + 4 * u;
@@ -279,6 +283,18 @@ __global__ __launch_bounds__(kThreads) void router_dw_partial_kernel(RouterDwPar
                     acc[4 * q4 + t][3] += g * x3;
                 }
             }
+        }
+    };
+    constexpr int kStep = 4 * kDwUnroll;  // rows of one batch over the four waves
+    if (wave < nr) {  // uniform; an empty chunk (T == 0) loads nothing
+        uint2 xa[kDwUnroll], xb[kDwUnroll];
+        xload(wave, xa);
+        for (int rb = wave; rb < nr; rb += 2 * kStep) {
+            xload(rb + kStep, xb);
+            xmul(rb, xa);
+            if (rb + kStep >= nr) break;
+            xload(rb + 2 * kStep, xa);
+            xmul(rb + kStep, xb);
         }
     }
     if (wave > 0) {
