@@ -25,75 +25,86 @@ static std::string tmp_path(const char* tag) {
     return "/tmp/tmt-moe-ckpt-" + std::to_string(getpid()) + "-" + tag;
 }
 
+static bool throws(void (*f)(const std::string&), const std::string& arg) {
+    try {
+        f(arg);
+    } catch (const std::exception&) {
+        return true;
+    }
+    return false;
+}
+
+static void write_raw(const std::string& path, const std::vector<unsigned char>& bytes) {
+    FILE* f = std::fopen(path.c_str(), "wb");
+    require(f && std::fwrite(bytes.data(), 1, bytes.size(), f) == bytes.size(), "raw write");
+    std::fclose(f);
+}
+
+static std::vector<unsigned char> read_raw(const std::string& path) {
+    FILE* f = std::fopen(path.c_str(), "rb");
+    require(f != nullptr, "raw open");
+    std::vector<unsigned char> b;
+    int c;
+    while ((c = std::fgetc(f)) != EOF) b.push_back((unsigned char)c);
+    std::fclose(f);
+    return b;
+}
+
 // FNV-1a 64 known answers (the published test vectors of the algorithm),
-// and a hand-built file through the streaming hash.
+// a hand-built file checked byte by byte, and damaged files refused.
 static void test_host_format() {
-    using tmt_ckpt::hash_bytes;
-    using tmt_ckpt::kHashInit;
-    require(hash_bytes(kHashInit, "", 0) == UINT64_C(0xcbf29ce484222325), "FNV-1a of the empty string");
-    require(hash_bytes(kHashInit, "a", 1) == UINT64_C(0xaf63dc4c8601ec8c), "FNV-1a of \"a\"");
-    require(hash_bytes(kHashInit, "foobar", 6) == UINT64_C(0x85944171f73967e8), "FNV-1a of \"foobar\"");
-    // streaming equals one shot
-    require(hash_bytes(hash_bytes(kHashInit, "foo", 3), "bar", 3) == hash_bytes(kHashInit, "foobar", 6),
-            "FNV-1a streams");
+    using tmt_ckpt::fnv1a64;
+    require(fnv1a64("", 0) == UINT64_C(0xcbf29ce484222325), "FNV-1a of the empty string");
+    require(fnv1a64("a", 1) == UINT64_C(0xaf63dc4c8601ec8c), "FNV-1a of \"a\"");
+    require(fnv1a64("foobar", 6) == UINT64_C(0x85944171f73967e8), "FNV-1a of \"foobar\"");
+    require(fnv1a64("bar", 3, fnv1a64("foo", 3)) == fnv1a64("foobar", 6), "FNV-1a streams");
     const std::string path = tmp_path("host");
     {
-        tmt_ckpt::Checkpoint io(path, true);
-        uint64_t magic = tmt_ckpt::kMagicV3;
-        io.scalar(magic);
-        std::vector<float> vals = {1.f, -2.f, 3.5f};
-        io.bytes(vals.data(), vals.size() * 4);
-        io.finish();
+        tmt_ckpt::Writer w(path);
+        w.put_u64(tmt_ckpt::kMagic);
+        const float vals[3] = {1.f, -2.f, 3.5f};
+        w.put(vals, sizeof vals);
+        w.commit();
     }
-    tmt_ckpt::verify_checkpoint(path);
+    tmt_ckpt::check_file(path);
+    std::vector<unsigned char> b = read_raw(path);
+    require(b.size() == 8 + 12 + 8, "file = magic + payload + 8-byte trailer");
+    require(std::memcmp(b.data(), "TMTCPKT3", 8) == 0, "magic bytes spell TMTCPKT3");
+    uint64_t trailer;
+    std::memcpy(&trailer, b.data() + 20, 8);
+    require(trailer == fnv1a64(b.data(), 20), "trailer is the FNV-1a hash of all preceding bytes");
     {
-        FILE* f = std::fopen(path.c_str(), "rb");
-        unsigned char buf[64];
-        const size_t n = std::fread(buf, 1, sizeof(buf), f);
-        std::fclose(f);
-        require(n == 8 + 12 + 8, "file = magic + payload + 8-byte trailer");
-        require(std::memcmp(buf, "TMTCPKT3", 8) == 0, "magic bytes spell TMTCPKT3");
-        uint64_t trailer;
-        std::memcpy(&trailer, buf + 20, 8);
-        require(trailer == hash_bytes(kHashInit, buf, 20), "trailer is the FNV-1a hash of all preceding bytes");
+        std::vector<unsigned char> bad = b;
+        bad[9] ^= 1;
+        write_raw(path, bad);
+        require(throws(tmt_ckpt::check_file, path), "a flipped bit is rejected");
+        bad = b;
+        bad.push_back(0);
+        write_raw(path, bad);
+        require(throws(tmt_ckpt::check_file, path), "a byte after the trailer is rejected");
+        write_raw(path, std::vector<unsigned char>(b.begin(), b.begin() + 5));
+        require(throws(tmt_ckpt::check_file, path), "a truncated file is rejected");
     }
     {
-        FILE* f = std::fopen(path.c_str(), "r+b");
-        std::fseek(f, 9, SEEK_SET);
-        const int c = std::fgetc(f);
-        std::fseek(f, 9, SEEK_SET);
-        std::fputc(c ^ 1, f);
-        std::fclose(f);
-        bool rejected = false;
-        try {
-            tmt_ckpt::verify_checkpoint(path);
-        } catch (const std::exception&) {
-            rejected = true;
+        // a writer that never commits leaves no file behind
+        const std::string p2 = tmp_path("uncommitted");
+        {
+            tmt_ckpt::Writer w(p2);
+            w.put_u64(1);
         }
-        require(rejected, "a flipped bit is rejected");
-    }
-    {
-        FILE* f = std::fopen(path.c_str(), "wb");
-        std::fputs("short", f);
-        std::fclose(f);
-        bool rejected = false;
-        try {
-            tmt_ckpt::verify_checkpoint(path);
-        } catch (const std::exception&) {
-            rejected = true;
-        }
-        require(rejected, "a truncated file is rejected");
+        require(std::fopen(p2.c_str(), "rb") == nullptr, "an uncommitted write leaves no file");
     }
     std::remove(path.c_str());
     tmt_ckpt::LayerShape s;
     s.dim = 64; s.experts = 4; s.topk = 2;
     auto sz = tmt_ckpt::moe_layer_param_sizes(s);
     require(sz.size() == 5 && sz[0] == 256 && sz[1] == 64 * 64, "reference layer order: router, then W_e");
+    require(tmt_ckpt::layer_config_text(s) == "dim=64\nexperts=4\ntopk=2\n", "configuration text keys");
     s.hidden = 128; s.layernorm = true;
     sz = tmt_ckpt::moe_layer_param_sizes(s);
     require(sz.size() == 2 + 1 + 8 && sz[0] == 64 && sz[2] == 256 && sz[3] == 128 * 64 && sz[4] == 64 * 128,
             "gamma, beta, router, then W_up[e], W_down[e] per expert");
-    std::puts("PASS checkpoint format: FNV-1a vectors, trailer, corruption and truncation rejected");
+    std::puts("PASS checkpoint format: FNV-1a vectors, trailer, corruption, extra bytes and truncation rejected");
 }
 
 struct DevParams {
@@ -173,6 +184,26 @@ static void round_trip(tmt_ckpt::LayerShape s, const char* tag) {
         refused = true;
     }
     require(refused, "a checkpoint of another architecture is refused");
+    // a file cut inside the records but given a valid trailer again is
+    // refused by the parser (the trailer alone does not catch it)
+    {
+        std::vector<unsigned char> bytes = read_raw(path);
+        bytes.resize(bytes.size() - 8 - 40);
+        const uint64_t h = tmt_ckpt::fnv1a64(bytes.data(), bytes.size());
+        const unsigned char* hp = reinterpret_cast<const unsigned char*>(&h);
+        bytes.insert(bytes.end(), hp, hp + 8);
+        const std::string cut = tmp_path("cut");
+        write_raw(cut, bytes);
+        tmt_ckpt::check_file(cut);  // the trailer matches
+        bool cut_refused = false;
+        try {
+            tmt_ckpt::load_layer(cut, s, b.ps);
+        } catch (const std::exception&) {
+            cut_refused = true;
+        }
+        require(cut_refused, "a file cut inside the records is refused");
+        std::remove(cut.c_str());
+    }
     // corruption: flip one byte in the middle; the load is refused and the
     // parameters keep their values
     f = std::fopen(path.c_str(), "r+b");
