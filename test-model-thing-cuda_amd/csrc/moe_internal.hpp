@@ -35,6 +35,10 @@ struct RouterParams {
     float* blkstat;        // [nblk][E+1] sum of probs per expert, sum of lse^2
 };
 int router_ep(int E);  // padded expert count used by the router (power of 2)
+// Wr is staged in LDS by the router and the dX scatter when it fits in this
+// many bytes; wider routers (E*d*2 larger) are read from global memory.
+constexpr size_t kRouterWrLdsBytes = 65536;
+inline bool router_wr_in_lds(int E, int d) { return (size_t)E * (size_t)d * 2 <= kRouterWrLdsBytes; }
 int router_rows_per_wave(int E);
 hipError_t launch_router(const RouterParams& p, int nblk, hipStream_t s);
 

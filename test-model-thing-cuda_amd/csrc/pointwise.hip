@@ -380,35 +380,40 @@ __device__ __forceinline__ void scatter_chunk(const ScatterParams& p, const int*
 // columns over the wave's rows (ascending); the four waves are added in
 // order into one [2][d] partial per workgroup.
 constexpr int kRedOnWrExperts = 12;  // E*d*2 bytes of Wr hold the 3*2*d floats
-template <bool ROUTER, int NI>
+// WLDS: Wr is staged in LDS (router_wr_in_lds); otherwise it is read from
+// global memory, with the same arithmetic.
+template <bool ROUTER, int NI, bool WLDS>
 __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterParams p, int rows_per_block) {
     extern __shared__ uint4 smem_w[];
     constexpr int NR = NI > 0 ? NI : 1;
+    constexpr bool STAGE = ROUTER && WLDS;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d = p.d, K = p.K, E = p.E;
     const int rbeg = blockIdx.x * rows_per_block;
     const int rend = min(p.T, rbeg + rows_per_block);
-    float* s_dl = reinterpret_cast<float*>(smem_w + (ROUTER ? E * d / 8 : 0));  // [rows_per_block][E]
+    float* s_dl = reinterpret_cast<float*>(smem_w + (STAGE ? E * d / 8 : 0));  // [rows_per_block][E]
     // [3][2][d] wave partials of the LayerNorm variant: over the staged Wr
     // once every wave is done with it (E >= 12), else after the dlogits.
-    const bool red_on_wr = ROUTER && E >= kRedOnWrExperts;
+    const bool red_on_wr = STAGE && E >= kRedOnWrExperts;
     float* s_red = red_on_wr ? reinterpret_cast<float*>(smem_w) : s_dl + (ROUTER ? rows_per_block * E : 0);
     if (ROUTER) {
-        const uint4* src = reinterpret_cast<const uint4*>(p.Wr);
-        const int nvec = E * d / 8;
-        for (int i0 = threadIdx.x; i0 < nvec; i0 += 8 * kThreads) {
-            uint4 v[8];
+        if (STAGE) {
+            const uint4* src = reinterpret_cast<const uint4*>(p.Wr);
+            const int nvec = E * d / 8;
+            for (int i0 = threadIdx.x; i0 < nvec; i0 += 8 * kThreads) {
+                uint4 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = src[min(i0 + u * kThreads, nvec - 1)];
+                for (int u = 0; u < 8; ++u) v[u] = src[min(i0 + u * kThreads, nvec - 1)];
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (i0 + u * kThreads < nvec) smem_w[i0 + u * kThreads] = v[u];
+                for (int u = 0; u < 8; ++u)
+                    if (i0 + u * kThreads < nvec) smem_w[i0 + u * kThreads] = v[u];
+            }
         }
         const int ndl = (rend - rbeg) * E;
         for (int i = threadIdx.x; i < ndl; i += kThreads) s_dl[i] = p.dlogits[(int64_t)rbeg * E + i];
         __syncthreads();
     }
-    const uint16_t* wl = reinterpret_cast<const uint16_t*>(smem_w);
+    const uint16_t* wl = STAGE ? reinterpret_cast<const uint16_t*>(smem_w) : p.Wr;
 
     float gam[NR][8], pg[NR][8], pb[NR][8];
     if constexpr (NI > 0) {
@@ -611,31 +616,34 @@ constexpr int kScatterRowsPerWave = 4;
 // Rows per workgroup of the router variant: 32 gives 1024 workgroups at
 // T = 32768, four per CU (LDS: E*d*2 bytes of Wr + 32*E*4 of dlogits).
 constexpr int kScatterRowsRouter = 32;
-template <bool ROUTER, int K>
+template <bool ROUTER, int K, bool WLDS>
 __global__ __launch_bounds__(kThreads) void scatter_rows_kernel(ScatterParams p, int rows_per_block) {
     extern __shared__ uint4 smem_w[];
     constexpr int RPW = kScatterRowsPerWave;
+    constexpr bool STAGE = ROUTER && WLDS;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d = p.d, E = p.E;
     const int rbeg = blockIdx.x * rows_per_block;
     const int rend = min(p.T, rbeg + rows_per_block);
-    float* s_dl = reinterpret_cast<float*>(smem_w + (ROUTER ? E * d / 8 : 0));  // [rows_per_block][E]
+    float* s_dl = reinterpret_cast<float*>(smem_w + (STAGE ? E * d / 8 : 0));  // [rows_per_block][E]
     if (ROUTER) {
-        const uint4* src = reinterpret_cast<const uint4*>(p.Wr);
-        const int nvec = E * d / 8;
-        for (int i0 = threadIdx.x; i0 < nvec; i0 += 8 * kThreads) {
-            uint4 v[8];
+        if (STAGE) {
+            const uint4* src = reinterpret_cast<const uint4*>(p.Wr);
+            const int nvec = E * d / 8;
+            for (int i0 = threadIdx.x; i0 < nvec; i0 += 8 * kThreads) {
+                uint4 v[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = src[min(i0 + u * kThreads, nvec - 1)];
+                for (int u = 0; u < 8; ++u) v[u] = src[min(i0 + u * kThreads, nvec - 1)];
 #pragma unroll
-            for (int u = 0; u < 8; ++u)
-                if (i0 + u * kThreads < nvec) smem_w[i0 + u * kThreads] = v[u];
+                for (int u = 0; u < 8; ++u)
+                    if (i0 + u * kThreads < nvec) smem_w[i0 + u * kThreads] = v[u];
+            }
         }
         const int ndl = (rend - rbeg) * E;
         for (int i = threadIdx.x; i < ndl; i += kThreads) s_dl[i] = p.dlogits[(int64_t)rbeg * E + i];
         __syncthreads();
     }
-    const uint16_t* wl = reinterpret_cast<const uint16_t*>(smem_w);
+    const uint16_t* wl = STAGE ? reinterpret_cast<const uint16_t*>(smem_w) : p.Wr;
     for (int r = rbeg + wave; r < rend; r += 4 * RPW) {
         int row[RPW], pos[RPW][K];
         bool ok[RPW];
@@ -690,15 +698,15 @@ int scatter_blocks(int T) {
     return b < 1 ? 1 : b;
 }
 
-template <bool ROUTER>
+template <bool ROUTER, bool WLDS>
 hipError_t launch_scatter_ni(const ScatterParams& p, int ni, int rows, size_t lds, hipStream_t s) {
     const int grid = (p.T + rows - 1) / rows;
     switch (ni) {
-        case 0: scatter_kernel<ROUTER, 0><<<grid, kThreads, lds, s>>>(p, rows); break;
-        case 1: scatter_kernel<ROUTER, 1><<<grid, kThreads, lds, s>>>(p, rows); break;
-        case 2: scatter_kernel<ROUTER, 2><<<grid, kThreads, lds, s>>>(p, rows); break;
-        case 3: scatter_kernel<ROUTER, 3><<<grid, kThreads, lds, s>>>(p, rows); break;
-        case 4: scatter_kernel<ROUTER, 4><<<grid, kThreads, lds, s>>>(p, rows); break;
+        case 0: scatter_kernel<ROUTER, 0, WLDS><<<grid, kThreads, lds, s>>>(p, rows); break;
+        case 1: scatter_kernel<ROUTER, 1, WLDS><<<grid, kThreads, lds, s>>>(p, rows); break;
+        case 2: scatter_kernel<ROUTER, 2, WLDS><<<grid, kThreads, lds, s>>>(p, rows); break;
+        case 3: scatter_kernel<ROUTER, 3, WLDS><<<grid, kThreads, lds, s>>>(p, rows); break;
+        case 4: scatter_kernel<ROUTER, 4, WLDS><<<grid, kThreads, lds, s>>>(p, rows); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -738,17 +746,22 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
     const bool ln = p.ln_S != nullptr;
     if (ln && p.d > kLnFusedMaxD) return hipErrorInvalidValue;
     const int rows = (router || ln) ? kScatterRows : 4;
-    size_t lds = router ? (size_t)p.E * p.d * 2 + (size_t)rows * p.E * 4 : 0;
-    if (ln && !(router && p.E >= kRedOnWrExperts)) lds += (size_t)3 * 2 * p.d * 4;
+    const bool wlds = router && router_wr_in_lds(p.E, p.d);  // Wr staged in LDS
+    const size_t wr_lds = wlds ? (size_t)p.E * p.d * 2 : 0;
+    size_t lds = router ? wr_lds + (size_t)rows * p.E * 4 : 0;
+    if (ln && !(wlds && p.E >= kRedOnWrExperts)) lds += (size_t)3 * 2 * p.d * 4;
     const int ni = ln ? (p.d + 511) / 512 : 0;
     if (ni == 0) {
         const int rrows = router ? kScatterRowsRouter : 4 * kScatterRowsPerWave;
         const int grid = (p.T + rrows - 1) / rrows;
-        const size_t rlds = router ? (size_t)p.E * p.d * 2 + (size_t)rrows * p.E * 4 : 0;
+        const size_t rlds = router ? wr_lds + (size_t)rrows * p.E * 4 : 0;
         switch (p.K * 2 + (router ? 1 : 0)) {
 #define TMT_SCATTER_ROWS(KK)                                                                   \
-    case 2 * KK: scatter_rows_kernel<false, KK><<<grid, kThreads, 0, s>>>(p, rrows); break;      \
-    case 2 * KK + 1: scatter_rows_kernel<true, KK><<<grid, kThreads, rlds, s>>>(p, rrows); break;
+    case 2 * KK: scatter_rows_kernel<false, KK, false><<<grid, kThreads, 0, s>>>(p, rrows); break; \
+    case 2 * KK + 1:                                                                           \
+        if (wlds) scatter_rows_kernel<true, KK, true><<<grid, kThreads, rlds, s>>>(p, rrows);    \
+        else scatter_rows_kernel<true, KK, false><<<grid, kThreads, rlds, s>>>(p, rrows);        \
+        break;
             TMT_SCATTER_ROWS(1)
             TMT_SCATTER_ROWS(2)
             TMT_SCATTER_ROWS(3)
@@ -762,7 +775,9 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
         }
         return hipGetLastError();
     }
-    return router ? launch_scatter_ni<true>(p, ni, rows, lds, s) : launch_scatter_ni<false>(p, ni, rows, lds, s);
+    if (!router) return launch_scatter_ni<false, false>(p, ni, rows, lds, s);
+    return wlds ? launch_scatter_ni<true, true>(p, ni, rows, lds, s)
+                : launch_scatter_ni<true, false>(p, ni, rows, lds, s);
 }
 
 }  // namespace tmt

@@ -260,22 +260,25 @@ __device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t
 // A reduce-scatter xor butterfly (offsets 32..1) then leaves lane l with the
 // full dot product of row l/EP and expert l%EP; each addition pairs the same
 // partial trees as the full butterfly, so the bits equal the canonical order.
-template <int EP>
+// WLDS: Wr is staged in LDS (E*d*2 <= kRouterWrLdsBytes); otherwise the
+// waves read it from global memory (it stays in L2), with the same
+// arithmetic and therefore the same bits.
+template <int EP, bool WLDS>
 __global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
-    extern __shared__ uint4 smem_w[];  // Wr [E][d] bf16
+    extern __shared__ uint4 smem_w[];  // Wr [E][d] bf16 (WLDS)
     __shared__ int s_cnt[kMaxExperts];
     __shared__ float s_stat[4][kMaxExperts + 1];
 
     const int tid = threadIdx.x;
     const int E = p.E;
-    stage_router_weights(p.Wr, E * p.d / 8, smem_w);
+    if constexpr (WLDS) stage_router_weights(p.Wr, E * p.d / 8, smem_w);
     if (tid < kMaxExperts) s_cnt[tid] = 0;
     __syncthreads();
 
     const int row_begin = blockIdx.x * p.rows_per_block;
     const int row_end = min(p.T, row_begin + p.rows_per_block);
-    route_rows<EP, 4>(p, reinterpret_cast<const uint16_t*>(smem_w), row_begin, row_end, s_cnt, s_stat,
-                      nullptr);
+    const uint16_t* wl = WLDS ? reinterpret_cast<const uint16_t*>(smem_w) : p.Wr;
+    route_rows<EP, 4>(p, wl, row_begin, row_end, s_cnt, s_stat, nullptr);
     __syncthreads();
     // Block statistics: waves added in order.
     const int b = blockIdx.x;
@@ -291,16 +294,23 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
 }
 
 hipError_t launch_router(const RouterParams& p, int nblk, hipStream_t s) {
-    const size_t lds = (size_t)p.E * p.d * 2;
+    const bool wlds = router_wr_in_lds(p.E, p.d);
+    const size_t lds = wlds ? (size_t)p.E * p.d * 2 : 0;
     const int ep = router_ep(p.E);
     dim3 grid(nblk), block(kThreads);
+#define TMT_ROUTER(EP_)                                                                \
+    case EP_:                                                                         \
+        if (wlds) router_kernel<EP_, true><<<grid, block, lds, s>>>(p);               \
+        else router_kernel<EP_, false><<<grid, block, 0, s>>>(p);                     \
+        break;
     switch (ep) {
-        case 8: router_kernel<8><<<grid, block, lds, s>>>(p); break;
-        case 16: router_kernel<16><<<grid, block, lds, s>>>(p); break;
-        case 32: router_kernel<32><<<grid, block, lds, s>>>(p); break;
-        case 64: router_kernel<64><<<grid, block, lds, s>>>(p); break;
+        TMT_ROUTER(8)
+        TMT_ROUTER(16)
+        TMT_ROUTER(32)
+        TMT_ROUTER(64)
         default: return hipErrorInvalidValue;
     }
+#undef TMT_ROUTER
     return hipGetLastError();
 }
 

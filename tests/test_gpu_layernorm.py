@@ -134,6 +134,8 @@ def check_all(g, r, E, h):
     (64, 1024, 16, 4, 512),    # largest decode batch, c3 width
     (2100, 2048, 12, 2, 128),  # widest row of the scatter-fused backward (4 passes per lane)
     (300, 2560, 4, 2, 128),    # d > 2048: separate two-pass LayerNorm backward
+    (200, 2048, 32, 4, 128),   # E*d beyond the LDS-staged router: fused scatter reads Wr from memory
+    (160, 2560, 16, 4, 0),     # the same on the separate LayerNorm backward, reference experts
 ])
 def test_layernorm_block_against_oracle(orc, T, d, E, K, h):
     say(f"layernorm block T={T} d={d} E={E} K={K} h={h} fwd+bwd")
@@ -207,6 +209,28 @@ def test_backward_ln_needs_forward_ln():
         assert ei.value.code == -4
         with pytest.raises(tmt_moe.MoeError):
             m.norm()
+        torch.cuda.synchronize()
+    finally:
+        m.close()
+
+
+def test_plain_backward_after_forward_ln_is_rejected():
+    say("layernorm block: a plain backward after forward_ln is rejected")
+    T, d, E, K, h = 32, 128, 4, 2, 128
+    case = make_case(T, d, E, K, h, seed=5)
+    m = tmt_moe.MoE(T, d, E, K, h)
+    try:
+        S, Wr, Wu, Wd = dev(case["X"]), dev(case["Wr"]), dev(case["W_up"]), dev(case["W_down"])
+        Y = torch.zeros(T, d, dtype=torch.bfloat16, device="cuda")
+        g_d, b_d = torch.ones(d, device="cuda"), torch.zeros(d, device="cuda")
+        m.forward_ln(S, g_d, b_d, Wr, Wu, Wd, Y)
+        dX = torch.zeros_like(S)
+        dWr = torch.zeros(E, d, device="cuda")
+        dWu = torch.zeros(E, h, d, device="cuda")
+        dWd = torch.zeros(E, d, h, device="cuda")
+        with pytest.raises(tmt_moe.MoeError) as ei:
+            m.backward(Y, S, Wr, Wu, Wd, dX, dWr, dWu, dWd)
+        assert ei.value.code == -4
         torch.cuda.synchronize()
     finally:
         m.close()

@@ -156,6 +156,12 @@ def test_c1_backward_against_oracle(orc):
     (211, 256, 12, 6, 256),    # top-6: the K = 6 combine / combine_bwd / scatter instantiations
     (97, 128, 7, 5, 128),      # top-5 over 7 experts, T below one router block
     (40, 256, 8, 2, 4096),     # decode DOWN in two K halves (combine forms O), then the backward reads O
+    (24, 256, 8, 2, 4096),     # decode DOWN K halves with two row blocks (17..32 rows per expert)
+    (20, 256, 8, 4, 4096),     # the same with top-4: the K = 4 partial combine
+    (2048, 1280, 8, 2, 0),     # the reference's profile shape (tmt-cuda/src/profile.cu:17): h = 0, D = 1280
+    (256, 2560, 16, 4, 0),     # E*d = 40960: router and dX scatter read Wr from memory, not LDS
+    (96, 4096, 16, 4, 0),      # E*d = 65536, the widest TMT router (experts <= 16) at d = 4096
+    (40, 2560, 16, 4, 0),      # decode-sized batch on the wide router
 ])
 def test_shapes_against_oracle(orc, T, d, E, K, h):
     say(f"shape T={T} d={d} E={E} K={K} h={h} fwd+bwd")
