@@ -47,7 +47,7 @@ def moe_reference(X, Wr, W_up, W_down, idx, dY, h, bias=None, Y_in=None, beta=0.
         a = u * torch.sigmoid(u)
         o = a @ W_down[e].t() if h > 0 else a
         Y = Y.index_add(0, rows, gate[rows, js].unsqueeze(1) * o)
-    out = {"Y": Y.detach(), "aux": float(aux), "z": float(z)}
+    out = {"Y": Y.detach(), "aux": float(aux.detach()), "z": float(z.detach())}
     if need_grads:
         loss = (dY * Y).sum() + aux_coef * aux + z_coef * z
         loss.backward()
