@@ -25,6 +25,7 @@ sys.path.insert(0, os.path.join(ROOT, "test-model-thing-cuda_amd"))
 METRIC = "MoE fwd+bwd tokens/s (E16 top4 d1024 bf16), % MFMA peak; decode µs/step"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+PEAK_FP4_TFLOPS = 10100.0   # MI355X dense MXFP4 MFMA
 
 
 def kernel_work(phase, T, d, E, K, h):
@@ -65,12 +66,40 @@ def step_flops(T, d, E, K, h):
     return fwd, bwd
 
 
-def cpu_baseline(case, cfg, target_s=15.0, max_threads=16):
+def host_cpu():
+    """CPU model (from /proc/cpuinfo), the thread count the OS reports
+    (std::thread::hardware_concurrency / os.cpu_count) and the threads this
+    process may run on (its affinity mask)."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = os.cpu_count() or 1
+    return model, os.cpu_count() or 1, allowed
+
+
+# A GPU box grants one GPU's share of its host: 16 hardware threads, whatever
+# the OS reports, so worker pools are capped there.
+CPU_SHARE_THREADS = 16
+
+
+def cpu_baseline(case, cfg, target_s=6.0, reps=3):
     """CPU oracle (test infrastructure) on a bounded token slice of the same
-    workload, timed on this host. Returns the cpu_baseline object."""
+    workload, timed on this host's cores: one warm-up, then the median of
+    `reps` timed runs (std::chrono-equivalent wall clock). Returns the
+    cpu_baseline object."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import moe_oracle  # cpu_baseline leg only
-    threads = max(1, min(max_threads, os.cpu_count() or 1))
+    model, hw, allowed = host_cpu()
+    threads = max(1, min(CPU_SHARE_THREADS, allowed))
     K, h = cfg["K"], cfg["h"]
 
     def run(ts):
@@ -81,16 +110,23 @@ def cpu_baseline(case, cfg, target_s=15.0, max_threads=16):
         return time.perf_counter() - t0
 
     # Two probes separate the per-call fixed cost (weight conversion, dW
-    # buffers) from the per-token cost; the sample is then sized for target_s.
+    # buffers) from the per-token cost; the sample is sized for target_s per
+    # run, and the first full-size run is the warm-up.
     t0 = run(64)
     t1 = run(512)
     per_tok = max((t1 - t0) / 448.0, 1e-6)
     ts = int(max(512, min(16384, 64 + (target_s - t0) / per_tok)))
     ts -= ts % 64
-    dt = run(ts)
+    run(ts)
+    times = sorted(run(ts) for _ in range(reps))
+    dt = times[len(times) // 2]
     return {"value": round(ts / dt, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle fwd+bwd (recomputes the forward) on the first {ts} tokens of the c3 "
-                      f"workload with all 16 experts, {dt:.1f} s wall, fp32 C++ on {threads} threads"}
+            "cpu_model": model, "hardware_concurrency": hw, "affinity_threads": allowed,
+            "runs_s": [round(t, 2) for t in times],
+            "sample": f"oracle fwd+bwd (recomputes the forward) on the first {ts} tokens of the "
+                      f"{cfg.get('name', 'c3')} workload with all {case['W_up'].shape[0]} experts, "
+                      f"median of {reps} runs after one warm-up ({dt:.1f} s each), fp32 C++ on "
+                      f"{threads} threads (this GPU's host share; the OS reports {hw} on a {model})"}
 
 
 def bench_mxfp4(stream, reps=5):
@@ -127,7 +163,67 @@ def bench_mxfp4(stream, reps=5):
             "ms": round(ms, 4), "tokens_per_s": round(T / (ms / 1e3), 1),
             "tflops": round(flops / (ms / 1e3) / 1e12, 1),
             "mfma_frac_bf16_peak": round(flops / (ms / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "mfma_frac_fp4_peak": round(flops / (ms / 1e3) / 1e12 / PEAK_FP4_TFLOPS, 4),
             "note": "weights streamed as e2m1+e8m0 and expanded to bf16 for bf16 MFMA"}
+
+
+# The reference's own MoE benchmark (tmt-cuda/src/profile.cu:14-63): N=2048
+# tokens, E=8, top-2, D=1280, single-linear experts (h = 0), backward with
+# aux 0.01 and z 0.001; its FLOP model is fwd = 2NDE + 2NKD^2 and
+# bwd = 2.2 x fwd (profile.cu:41-42, 60). The reference reports about 50% of
+# its 49 TFLOP/s roof for this step (CHANGES.md:35, 46). The second shape is
+# TMT's default width with a small MoE (config.h: dim 256, batch 8 x seqlen
+# 128 tokens).
+H0_SHAPES = {
+    "reference_profile": dict(T=2048, d=1280, E=8, K=2, h=0, aux=0.01, z=0.001),
+    "tmt_default_width": dict(T=1024, d=256, E=4, K=2, h=0, aux=0.01, z=0.001),
+}
+
+
+def bench_h0(name, steps=50, warmup=10):
+    """fwd+bwd of the reference's expert shape (h = 0), timed with HIP events."""
+    import numpy as np
+    import torch
+
+    import tmt_moe
+    from synthetic import make_case
+
+    cfg = H0_SHAPES[name]
+    T, d, E, K = cfg["T"], cfg["d"], cfg["E"], cfg["K"]
+    case = make_case(T, d, E, K, 0, seed=1234)
+    dev16 = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+    X, Wr, Wu, dY = (dev16(case[k]) for k in ("X", "Wr", "W_up", "dY"))
+    Y = torch.zeros(T, d, dtype=torch.bfloat16, device="cuda")
+    dX = torch.empty_like(X)
+    dWr = torch.empty(E, d, device="cuda")
+    dWu = torch.empty(E, d, d, device="cuda")
+    m = tmt_moe.MoE(T, d, E, K, 0)
+    try:
+        def step():
+            m.forward(X, Wr, Wu, None, Y, beta=1.0)
+            m.backward(dY, X, Wr, Wu, None, dX, dWr, dWu, None, cfg["aux"], cfg["z"])
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+    finally:
+        m.close()
+    fwd = 2.0 * T * d * E + 2.0 * T * K * d * d
+    flops = fwd * 3.2  # profile.cu's model: bwd = 2.2 x fwd
+    tf = flops / (ms / 1e3) / 1e12
+    return {"workload": f"{name}: fwd+bwd T={T} d={d} E={E} top-{K} h=0 (aux {cfg['aux']}, z {cfg['z']})",
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(T / (ms / 1e3), 1),
+            "tflops_profile_model": round(tf, 2), "mfma_frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "reference_published": "about 50% of a 49 TFLOP/s roof at N=2048 E=8 K=2 D=1280 "
+                                   "(CHANGES.md:35,46), i.e. about 24.5 TFLOP/s, other hardware"}
 
 
 COPY_PROBE_BYTES = 1 << 30
@@ -146,20 +242,41 @@ def copy_probe(reps=5):
     print(json.dumps({"copy_probe_bytes": COPY_PROBE_BYTES, "reps": reps}))
 
 
+def source_digest():
+    """SHA-256 (first 16 hex digits) of the kernel sources and the ABI
+    header: the profiles under profiles/ record the digest of the code they
+    measured, so numbers read from them can be matched to this tree."""
+    import hashlib
+    csrc = os.path.join(ROOT, "test-model-thing-cuda_amd", "csrc")
+    files = sorted(os.path.join(csrc, f) for f in os.listdir(csrc)
+                   if f.endswith((".hip", ".cpp", ".hpp")))
+    files.append(os.path.join(ROOT, "include", "tmt_moe.h"))
+    h = hashlib.sha256()
+    for path in files:
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(phase):
     """HBM bytes per launch of `phase` on c3, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy-probe factor);
-    None when the summary does not list the kernel."""
+    FETCH_SIZE / WRITE_SIZE summary (already scaled by the copy-probe factor).
+    None when the summary does not list the kernel or was taken on other
+    kernel sources than this tree's (its source_digest line differs)."""
     path = os.path.join(ROOT, "profiles", "hbm_traffic_c3.txt")
+    digest, value = None, None
     try:
         with open(path) as f:
             for line in f:
                 parts = line.split()
+                if len(parts) >= 2 and parts[0] == "source_digest":
+                    digest = parts[1]
                 if len(parts) >= 4 and parts[0] == "traffic" and parts[1] == phase:
-                    return int(parts[2]) + int(parts[3])
+                    value = int(parts[2]) + int(parts[3])
     except OSError:
-        pass
-    return None
+        return None
+    return value if digest == source_digest() else None
 
 
 def bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream, reps=100):
@@ -328,7 +445,14 @@ def main():
                     help="only run a device copy of known size (HBM counter calibration)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the c4 decode measurement (T = 1, 8, 64 on the c3 weights)")
+    ap.add_argument("--no-h0", action="store_true",
+                    help="skip the reference-expert (h = 0) fwd+bwd measurements")
+    ap.add_argument("--source-digest", action="store_true",
+                    help="print the digest of the kernel sources the profiles are tagged with")
     args = ap.parse_args()
+    if args.source_digest:
+        print(source_digest())
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(asked for --gpus {args.gpus}); run with --gpus 1", file=sys.stderr)
@@ -374,8 +498,7 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    m.set_profiling(not args.no_profile)
-    m.profile(reset=True)
+    # Headline: the timed steps run without per-kernel events.
     stream = torch.cuda.current_stream()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -387,9 +510,18 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_step = ev0.elapsed_time(ev1) / args.steps
-    prof = m.profile(reset=True)
-    m.set_profiling(False)
     aux, z, counts = m.stats()
+    # Kernel table: a separate pass of the same step with HIP events around
+    # every launch, on the launch stream.
+    prof = {}
+    prof_steps = max(args.steps // 2, 5)
+    if not args.no_profile:
+        m.set_profiling(True)
+        m.profile(reset=True)
+        for _ in range(prof_steps):
+            step()
+        prof = m.profile(reset=True)
+        m.set_profiling(False)
 
     fwd_f, bwd_f = step_flops(T, d, E, K, h)
     kernels = {}
@@ -398,8 +530,8 @@ def main():
             continue
         avg = tot_ms / n
         kind, work = kernel_work(ph, T, d, E, K, h)
-        k = {"avg_ms": round(avg, 4), "launches_per_step": n / args.steps,
-             "share": round(tot_ms / args.steps / ms_step, 4)}
+        k = {"avg_ms": round(avg, 4), "launches_per_step": n / prof_steps,
+             "share": round(tot_ms / prof_steps / ms_step, 4)}
         if kind == "mfma":
             k["tflops"] = round(work / avg / 1e9, 1)
             k["mfma_frac"] = round(work / avg / 1e9 / PEAK_BF16_TFLOPS, 4)
@@ -418,13 +550,17 @@ def main():
                         "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(ach / PEAK_BF16_TFLOPS, 4),
                         "traffic": measured_traffic(dom) if args.config == "c3" else None,
-                        "work_per_launch": f"{work / 1e9:.1f} GFLOP = 2*T*K*d*h"}
+                        "work_per_launch": f"{work / 1e9:.1f} GFLOP = 2*T*K*d*h",
+                        "timing": f"HIP events on the launch stream, {prof_steps} profiled steps "
+                                  "after the headline steps",
+                        "source_digest": source_digest()}
         else:
             ach = work / avg / 1e6
             roofline = {"kernel": dom, "bound": "hbm", "achieved": round(ach, 1),
                         "peak": PEAK_HBM_GBS, "unit": "GB/s",
                         "frac": round(ach / PEAK_HBM_GBS, 4),
-                        "traffic": measured_traffic(dom) if args.config == "c3" else None}
+                        "traffic": measured_traffic(dom) if args.config == "c3" else None,
+                        "source_digest": source_digest()}
 
     ln = None
     if not args.no_ln:
@@ -443,9 +579,13 @@ def main():
     if not args.no_fp4 and args.config == "c3":
         fp4 = bench_mxfp4(stream)
 
+    h0 = None
+    if not args.no_h0 and args.config == "c3":
+        h0 = {name: bench_h0(name) for name in H0_SHAPES}
+
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(case, cfg)
+        cpu = cpu_baseline(case, dict(cfg, name=args.config))
 
     tokens_s = T / (ms_step / 1e3)
     out = {
@@ -475,6 +615,7 @@ def main():
         "adamw": adamw,
         "decode": decode,
         "mxfp4_forward": fp4,
+        "reference_experts_h0": h0,
         "aux": round(aux, 6),
         "z": round(z, 6),
     }
