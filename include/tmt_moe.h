@@ -64,8 +64,33 @@ typedef struct tmt_moe tmt_moe;
 int tmt_moe_create(const tmt_moe_desc* desc, tmt_moe** out);
 /* Replaces moe_keep_free + moe_ws_free (moe.cu:342-348, 363-370). */
 int tmt_moe_destroy(tmt_moe* moe);
-/* Arena bytes tmt_moe_create would allocate for this descriptor. */
+/* Arena bytes tmt_moe_create would allocate for this descriptor
+ * (per_layer + shared of tmt_moe_workspace_sizes). */
 int tmt_moe_workspace_size(const tmt_moe_desc* desc, size_t* bytes);
+
+/*
+ * The two parts of a handle's device memory (moe.cu:294-328):
+ *   per_layer  state kept from forward to backward (the reference's MoeKeep:
+ *              routing, offsets, permutation, expert activations, the
+ *              LayerNorm output and row statistics);
+ *   shared     buffers used only inside one call (the reference's MoeWs:
+ *              router block tables, split-K partials and every backward
+ *              operand), which layers that run one after another can share.
+ * Either pointer may be NULL.
+ */
+int tmt_moe_workspace_sizes(const tmt_moe_desc* desc, size_t* per_layer, size_t* shared);
+
+/*
+ * Replaces moe_keep_alloc over a moe_ws_alloc'd workspace (moe.cu:330-362,
+ * model.cu:252-254): the handle allocates only its per_layer part and uses
+ * `workspace` (device memory, 256-byte aligned, at least the shared size of
+ * tmt_moe_workspace_sizes for this descriptor) for the rest. Handles that
+ * share a workspace must not run concurrently: order their calls on one
+ * stream (or synchronise between streams), as the reference's layers run
+ * one after another. The workspace must outlive every handle using it.
+ */
+int tmt_moe_create_shared(const tmt_moe_desc* desc, void* workspace, size_t workspace_bytes,
+                          tmt_moe** out);
 
 /*
  * Replaces moe_forward (moe.cu:374-466).

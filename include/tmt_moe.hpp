@@ -34,8 +34,13 @@
  * Work goes to MoeKeep::stream (default: the null stream, the reference's
  * default stream). Unlike the reference there is no host synchronisation
  * inside moe_forward when MoeKeep::stat is set, and none in moe_backward.
- * MoeWs exists for source compatibility: each MoeKeep's handle owns its
- * workspace, so moe_ws_alloc / moe_ws_free do nothing.
+ * MoeWs is, as in the reference, one set of transient buffers shared by all
+ * layers (model.cu:104, 254): moe_ws_alloc sizes it from the layer shape
+ * (tmt_moe_workspace_sizes' shared part), and each layer's handle is created
+ * on its first moe_forward over the MoeWs passed there
+ * (tmt_moe_create_shared). Layers sharing one MoeWs must run one after
+ * another, as the reference's do. A MoeKeep used with an MoeWs that was
+ * never allocated gets a private workspace.
  */
 #pragma once
 
@@ -55,9 +60,12 @@ struct MoeKeep {
     uint16_t* H = nullptr;          // [N][D] bf16 copy of the forward input
     int32_t hcnt[64] = {0};         // tokens per expert (after the statistics were read)
     int N = 0, E = 0, K = 0, D = 0, hidden = 0, max_N = 0;
-    tmt_moe* handle = nullptr;
+    tmt_moe* handle = nullptr;  // created by the first moe_forward
 };
-struct MoeWs {};
+struct MoeWs {
+    void* ptr = nullptr;  // device workspace shared by the layers
+    size_t bytes = 0;
+};
 
 namespace tmt_moe_detail {
 [[noreturn]] inline void die(const char* where, const char* what) {
@@ -87,12 +95,28 @@ inline const uint16_t* const* table(B* const* p) {
     return reinterpret_cast<const uint16_t* const*>(p);
 }
 
+inline tmt_moe_desc keep_desc(const MoeKeep& k) {
+    tmt_moe_desc desc{};
+    desc.max_tokens = k.max_N > 0 ? k.max_N : 1;
+    desc.d = k.D;
+    desc.experts = k.E;
+    desc.topk = k.K;
+    desc.hidden = k.hidden;
+    desc.weight_format = TMT_MOE_WEIGHTS_BF16;
+    return desc;
+}
+
 // Copy the input for the backward, run the forward, deliver the statistics.
 inline float forward(const uint16_t* X, const uint16_t* Wr, const uint16_t* const* Wup,
-                     const uint16_t* const* Wdown, uint16_t* Y, MoeKeep& k, int N, int E,
+                     const uint16_t* const* Wdown, uint16_t* Y, MoeKeep& k, MoeWs& w, int N, int E,
                      int K, int D, float beta) {
     const char* where = "moe_forward";
-    if (!k.handle) die(where, "moe_keep_alloc was not called");
+    if (k.E == 0) die(where, "moe_keep_alloc was not called");
+    if (!k.handle) {
+        const tmt_moe_desc desc = keep_desc(k);
+        check(w.ptr ? tmt_moe_create_shared(&desc, w.ptr, w.bytes, &k.handle) : tmt_moe_create(&desc, &k.handle),
+              where);
+    }
     if (E != k.E || K != k.K || D != k.D) die(where, "E, K or D differ from moe_keep_alloc");
     if (N < 0 || N > k.max_N) die(where, "N exceeds the moe_keep_alloc size");
     k.N = N;
@@ -116,26 +140,23 @@ inline void backward(const uint16_t* dY, const uint16_t* const* Wup, const uint1
                      const uint16_t* Wr, float* dWr, float* const* dWup, float* const* dWdown,
                      uint16_t* dX, MoeKeep& k, float aux, float zcoef) {
     const char* where = "moe_backward";
-    if (!k.handle) die(where, "moe_keep_alloc was not called");
+    if (!k.handle) die(where, "no moe_forward ran on this layer");
     // With E == 1 the library zeroes dWr, as the reference does (moe.cu:487).
     check(tmt_moe_backward(k.handle, k.stream, dY, k.H, Wr, Wup, Wdown, aux, zcoef, dX, dWr, dWup,
                            dWdown), where);
 }
 }  // namespace tmt_moe_detail
 
-/* moe.cu:330-341. N is the largest token count a forward will see. */
+/* moe.cu:330-341. N is the largest token count a forward will see. The
+ * shape is checked here; the device state is created by the first
+ * moe_forward, over the MoeWs it is given. */
 inline void moe_keep_alloc(MoeKeep& k, int N, int E, int K, int D, int hidden = 0) {
-    tmt_moe_desc desc{};
-    desc.max_tokens = N;
-    desc.d = D;
-    desc.experts = E;
-    desc.topk = K;
-    desc.hidden = hidden;
-    desc.weight_format = TMT_MOE_WEIGHTS_BF16;
-    tmt_moe_detail::check(tmt_moe_create(&desc, &k.handle), "moe_keep_alloc");
+    k.E = E; k.K = K; k.D = D; k.hidden = hidden; k.max_N = N;
+    const tmt_moe_desc desc = tmt_moe_detail::keep_desc(k);
+    size_t layer = 0, shared = 0;
+    tmt_moe_detail::check(tmt_moe_workspace_sizes(&desc, &layer, &shared), "moe_keep_alloc");
     if (N > 0)
         tmt_moe_detail::check_hip(hipMalloc((void**)&k.H, (size_t)N * D * 2), "moe_keep_alloc");
-    k.E = E; k.K = K; k.D = D; k.hidden = hidden; k.max_N = N;
 }
 
 /* moe.cu:342-348 */
@@ -145,32 +166,51 @@ inline void moe_keep_free(MoeKeep& k) {
     k = MoeKeep();
 }
 
-/* moe.cu:349-370: the workspace lives in each MoeKeep's handle. */
-inline void moe_ws_alloc(MoeWs&, int, int, int, int) {}
-inline void moe_ws_free(MoeWs&) {}
+/* moe.cu:349-362: the transient buffers every layer of this shape shares
+ * (hidden selects the up/down expert, as in moe_keep_alloc). */
+inline void moe_ws_alloc(MoeWs& w, int N, int E, int K, int D, int hidden = 0) {
+    tmt_moe_desc desc{};
+    desc.max_tokens = N > 0 ? N : 1;
+    desc.d = D;
+    desc.experts = E;
+    desc.topk = K;
+    desc.hidden = hidden;
+    desc.weight_format = TMT_MOE_WEIGHTS_BF16;
+    size_t layer = 0, shared = 0;
+    tmt_moe_detail::check(tmt_moe_workspace_sizes(&desc, &layer, &shared), "moe_ws_alloc");
+    tmt_moe_detail::check_hip(hipMalloc(&w.ptr, shared), "moe_ws_alloc");
+    w.bytes = shared;
+}
+
+/* moe.cu:363-370. Free the layers' MoeKeep first. */
+inline void moe_ws_free(MoeWs& w) {
+    if (w.ptr) (void)hipFree(w.ptr);
+    w = MoeWs();
+}
 
 /* moe.cu:372-466: Y = beta*Y + MoE(X) with the reference's single-linear
  * experts Wexp[e] [D][D] (hidden == 0). Returns the Switch aux loss. */
 template <class B>
-inline float moe_forward(const B* X, const B* Wrouter, B** Wexp, B* Y, MoeKeep& k, MoeWs&,
+inline float moe_forward(const B* X, const B* Wrouter, B** Wexp, B* Y, MoeKeep& k, MoeWs& w,
                          int N, int E, int K, int D, float beta = 0.0f) {
     if (k.hidden != 0) tmt_moe_detail::die("moe_forward", "hidden > 0 needs the W_down table");
     using namespace tmt_moe_detail;
-    return forward(bits(X), bits(Wrouter), table(Wexp), nullptr, bits(Y), k, N, E, K, D, beta);
+    return forward(bits(X), bits(Wrouter), table(Wexp), nullptr, bits(Y), k, w, N, E, K, D, beta);
 }
 
 /* Up/SiLU/down experts (hidden > 0): W_up[e] [hidden][D], W_down[e] [D][hidden]. */
 template <class B>
 inline float moe_forward(const B* X, const B* Wrouter, B** W_up, B** W_down, B* Y, MoeKeep& k,
-                         MoeWs&, int N, int E, int K, int D, float beta = 0.0f) {
+                         MoeWs& w, int N, int E, int K, int D, float beta = 0.0f) {
     if (k.hidden == 0) tmt_moe_detail::die("moe_forward", "hidden == 0 takes one weight table");
     using namespace tmt_moe_detail;
-    return forward(bits(X), bits(Wrouter), table(W_up), table(W_down), bits(Y), k, N, E, K, D, beta);
+    return forward(bits(X), bits(Wrouter), table(W_up), table(W_down), bits(Y), k, w, N, E, K, D, beta);
 }
 
 /* moe.cu:468-475: aux from the statistics moe_forward copied to k.stat
  * (hsum = the host copy of that slot); sets k.zloss and k.hcnt. */
 inline float moe_aux_from(MoeKeep& k, const float* hsum) {
+    if (!k.handle) tmt_moe_detail::die("moe_aux_from", "no moe_forward ran on this layer");
     k.zloss = hsum[1];
     tmt_moe_detail::check(tmt_moe_read_stats(k.handle, k.stream, nullptr, nullptr, k.hcnt),
                           "moe_aux_from");

@@ -61,8 +61,11 @@ struct tmt_moe {
     int hn = 0;        // width of the first expert GEMM (h, or d for h == 0)
     int nblk_max = 0;  // router blocks at the largest T
     int device = 0;
-    char* arena = nullptr;
+    char* arena = nullptr;      // per-layer state (the reference's MoeKeep)
     size_t arena_bytes = 0;
+    char* ws = nullptr;         // transient buffers (the reference's MoeWs): in the
+                                // arena, or a caller workspace shared by handles
+    bool own_ws = true;
     // routing state (kept from forward for backward; the reference's MoeKeep)
     float *logits, *probs, *lse, *gate, *blkstat, *stats;
     int32_t* ticket = nullptr;  // decode router's completion counter (zero between calls)
@@ -98,9 +101,6 @@ int validate_desc(const tmt_moe_desc* d) {
         return fail(TMT_MOE_EINVAL, "require 1 <= topk <= min(experts, %d) (topk=%d)", kMaxTopK, d->topk);
     if (d->hidden < 0 || d->hidden % 64 != 0)
         return fail(TMT_MOE_EINVAL, "hidden=%d must be 0 or a multiple of 64", d->hidden);
-    if ((int64_t)d->experts * d->d > 32768)
-        return fail(TMT_MOE_EINVAL, "experts*d=%lld exceeds 32768 (router weights are staged in 64 KiB of LDS)",
-                    (long long)d->experts * d->d);
     if ((int64_t)d->max_tokens * d->topk >= (1ll << 31))
         return fail(TMT_MOE_EINVAL, "max_tokens*topk must fit in int32");
     if (d->weight_format != TMT_MOE_WEIGHTS_BF16 && d->weight_format != TMT_MOE_WEIGHTS_MXFP4)
@@ -124,17 +124,28 @@ int router_rows_per_block(int T, int E, int K) {
     return base * iter;
 }
 
-size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
+// Device memory of one handle, in two parts:
+//   layer  -- state kept from forward to backward (routing, offsets,
+//             permutation, U / SiLU(U) / O, the LayerNorm output and row
+//             statistics): the reference's MoeKeep (moe.cu:294-315);
+//   shared -- buffers that live within one call (router block tables, split-K
+//             partials, and every backward operand: dO, dU, dXg, Xg, dlogits,
+//             router-dW and LayerNorm partials, dH): the reference's MoeWs
+//             (moe.cu:316-328), which one set serves for all layers because
+//             layers run one after another (model.cu:104, 254).
+struct Sizes {
+    size_t layer = 0, shared = 0;
+};
+
+Sizes plan(const tmt_moe_desc* d, tmt_moe* m) {
     const int64_t T = d->max_tokens, E = d->experts, K = d->topk, D = d->d, h = d->hidden;
     const int64_t hn = h > 0 ? h : D;
     const int64_t TK = T * K;
     const int rpb_min = 4 * router_rows_per_wave((int)E);
     const int64_t nblk = (T + rpb_min - 1) / rpb_min;
-    Layout L;
+    Layout L, W;
     size_t o_logits = L.add(T * E * 4), o_probs = L.add(T * E * 4), o_lse = L.add(T * 4);
     size_t o_gate = L.add(TK * 4), o_idx = L.add(TK * 4);
-    size_t o_blkcnt = L.add(nblk * E * 4), o_blkbase = L.add(nblk * E * 4);
-    size_t o_blkstat = L.add(nblk * (E + 1) * 4);
     size_t o_counts = L.add(E * 4), o_offsets = L.add((E + 1) * 4), o_order = L.add(E * 4);
     size_t o_stats = L.add((2 + E) * 4);
     size_t o_ticket = L.add(4);
@@ -142,64 +153,68 @@ size_t plan(const tmt_moe_desc* d, tmt_moe* m) {
     size_t o_U = L.add(TK * hn * 2);
     size_t o_A = h > 0 ? L.add(TK * h * 2) : 0;
     size_t o_O = h > 0 ? L.add(TK * D * 2) : 0;
+    size_t o_H = L.add(T * D * 2), o_mean = L.add(T * 4), o_rstd = L.add(T * 4);
+    // transient
+    size_t o_blkcnt = W.add(nblk * E * 4), o_blkbase = W.add(nblk * E * 4);
+    size_t o_blkstat = W.add(nblk * (E + 1) * 4);
     // MXFP4 handles are forward-only: no backward buffers.
     const bool bwd = d->weight_format == TMT_MOE_WEIGHTS_BF16;
-    size_t o_dO = bwd ? L.add(TK * D * 2) : 0;
-    size_t o_dU = bwd && h > 0 ? L.add(TK * h * 2) : 0;
-    size_t o_dXg = bwd ? L.add(TK * D * 2) : 0;
-    size_t o_Xg = bwd ? L.add(TK * D * 2) : 0;
-    size_t o_dl = bwd ? L.add(T * E * 4) : 0;
-    size_t o_dwr = bwd ? L.add((size_t)router_dw_chunks((int)T) * E * D * 4) : 0;
-    size_t o_H = L.add(T * D * 2), o_mean = L.add(T * 4), o_rstd = L.add(T * 4);
-    size_t o_dH = bwd ? L.add(T * D * 2) : 0;
+    size_t o_dO = bwd ? W.add(TK * D * 2) : 0;
+    size_t o_dU = bwd && h > 0 ? W.add(TK * h * 2) : 0;
+    size_t o_dXg = bwd ? W.add(TK * D * 2) : 0;
+    size_t o_Xg = bwd ? W.add(TK * D * 2) : 0;
+    size_t o_dl = bwd ? W.add(T * E * 4) : 0;
+    size_t o_dwr = bwd ? W.add((size_t)router_dw_chunks((int)T) * E * D * 4) : 0;
+    size_t o_dH = bwd ? W.add(T * D * 2) : 0;
     // Split-K tail of the tiled GEMM_DOWN / GEMM_DX (decode-sized handles never tile).
     const bool split = d->weight_format == TMT_MOE_WEIGHTS_BF16 && T > kSkinnyMaxTokens;
     const int resident = cu_count();
-    size_t o_split = split ? L.add(gemm_split_floats(resident) * 4) : 0;
+    size_t o_split = split ? W.add(gemm_split_floats(resident) * 4) : 0;
     // Decode GEMM_DOWN in K halves: [2][min(T, 64) * K][d] fp32.
     const bool dsplit = d->weight_format == TMT_MOE_WEIGHTS_BF16 && h > 0;
-    size_t o_dpart = dsplit ? L.add((size_t)2 * std::min<int64_t>(T, kSkinnyMaxTokens) * K * D * 4) : 0;
+    size_t o_dpart = dsplit ? W.add((size_t)2 * std::min<int64_t>(T, kSkinnyMaxTokens) * K * D * 4) : 0;
     const int64_t ln_rows = std::max(scatter_blocks((int)T), ln_chunks((int)T));
-    size_t o_lnp = bwd ? L.add((size_t)ln_rows * 2 * D * 4) : 0;
-    size_t o_lnp2 = bwd ? L.add((size_t)colsum_groups((int)ln_rows) * 2 * D * 4) : 0;
+    size_t o_lnp = bwd ? W.add((size_t)ln_rows * 2 * D * 4) : 0;
+    size_t o_lnp2 = bwd ? W.add((size_t)colsum_groups((int)ln_rows) * 2 * D * 4) : 0;
     if (m) {
         char* a = m->arena;
+        char* w = m->ws;
         m->logits = (float*)(a + o_logits);
         m->probs = (float*)(a + o_probs);
         m->lse = (float*)(a + o_lse);
         m->gate = (float*)(a + o_gate);
         m->idx = (int32_t*)(a + o_idx);
-        m->blkcnt = (int32_t*)(a + o_blkcnt);
-        m->blkbase = (int32_t*)(a + o_blkbase);
-        m->blkstat = (float*)(a + o_blkstat);
+        m->blkcnt = (int32_t*)(w + o_blkcnt);
+        m->blkbase = (int32_t*)(w + o_blkbase);
+        m->blkstat = (float*)(w + o_blkstat);
         m->counts = (int32_t*)(a + o_counts);
         m->offsets = (int32_t*)(a + o_offsets);
         m->order = (int32_t*)(a + o_order);
         m->stats = (float*)(a + o_stats);
         m->ticket = (int32_t*)(a + o_ticket);
-        m->split = split ? (float*)(a + o_split) : nullptr;
-        m->dpart = dsplit ? (float*)(a + o_dpart) : nullptr;
+        m->split = split ? (float*)(w + o_split) : nullptr;
+        m->dpart = dsplit ? (float*)(w + o_dpart) : nullptr;
         m->resident = resident;
         m->perm = (int32_t*)(a + o_perm);
         m->slot_of = (int32_t*)(a + o_slot);
         m->U = (uint16_t*)(a + o_U);
         m->Aact = h > 0 ? (uint16_t*)(a + o_A) : nullptr;
         m->O = h > 0 ? (uint16_t*)(a + o_O) : nullptr;
-        m->dO = bwd ? (uint16_t*)(a + o_dO) : nullptr;
-        m->dU = bwd ? (h > 0 ? (uint16_t*)(a + o_dU) : m->dO) : nullptr;  // h == 0: combine_bwd writes dU
-        m->dXg = bwd ? (uint16_t*)(a + o_dXg) : nullptr;
-        m->Xg = bwd ? (uint16_t*)(a + o_Xg) : nullptr;
-        m->dlogits = bwd ? (float*)(a + o_dl) : nullptr;
-        m->dwr_partial = bwd ? (float*)(a + o_dwr) : nullptr;
+        m->dO = bwd ? (uint16_t*)(w + o_dO) : nullptr;
+        m->dU = bwd ? (h > 0 ? (uint16_t*)(w + o_dU) : m->dO) : nullptr;  // h == 0: combine_bwd writes dU
+        m->dXg = bwd ? (uint16_t*)(w + o_dXg) : nullptr;
+        m->Xg = bwd ? (uint16_t*)(w + o_Xg) : nullptr;
+        m->dlogits = bwd ? (float*)(w + o_dl) : nullptr;
+        m->dwr_partial = bwd ? (float*)(w + o_dwr) : nullptr;
         m->H = (uint16_t*)(a + o_H);
         m->ln_mean = (float*)(a + o_mean);
         m->ln_rstd = (float*)(a + o_rstd);
-        m->dH = bwd ? (uint16_t*)(a + o_dH) : nullptr;
-        m->ln_partial = bwd ? (float*)(a + o_lnp) : nullptr;
-        m->ln_partial2 = bwd ? (float*)(a + o_lnp2) : nullptr;
+        m->dH = bwd ? (uint16_t*)(w + o_dH) : nullptr;
+        m->ln_partial = bwd ? (float*)(w + o_lnp) : nullptr;
+        m->ln_partial2 = bwd ? (float*)(w + o_lnp2) : nullptr;
         m->nblk_max = (int)nblk;
     }
-    return L.total;
+    return Sizes{L.total, W.total};
 }
 
 int check_device(const tmt_moe* m) {
@@ -528,15 +543,36 @@ int tmt_moe_workspace_size(const tmt_moe_desc* desc, size_t* bytes) {
     int rc = validate_desc(desc);
     if (rc) return rc;
     if (!bytes) return fail(TMT_MOE_EINVAL, "bytes is NULL");
-    *bytes = plan(desc, nullptr);
+    const Sizes sz = plan(desc, nullptr);
+    *bytes = sz.layer + sz.shared;
     return TMT_MOE_OK;
 }
 
-int tmt_moe_create(const tmt_moe_desc* desc, tmt_moe** out) {
+int tmt_moe_workspace_sizes(const tmt_moe_desc* desc, size_t* per_layer, size_t* shared) {
+    int rc = validate_desc(desc);
+    if (rc) return rc;
+    const Sizes sz = plan(desc, nullptr);
+    if (per_layer) *per_layer = sz.layer;
+    if (shared) *shared = sz.shared;
+    return TMT_MOE_OK;
+}
+
+namespace {
+// Shared by tmt_moe_create (workspace == nullptr: the handle allocates its
+// own) and tmt_moe_create_shared.
+int create_handle(const tmt_moe_desc* desc, void* workspace, size_t workspace_bytes, tmt_moe** out) {
     if (!out) return fail(TMT_MOE_EINVAL, "out is NULL");
     *out = nullptr;
     int rc = validate_desc(desc);
     if (rc) return rc;
+    const Sizes sz = plan(desc, nullptr);
+    if (workspace) {
+        if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+            return fail(TMT_MOE_EINVAL, "the shared workspace must be 256-byte aligned");
+        if (workspace_bytes < sz.shared)
+            return fail(TMT_MOE_EINVAL, "shared workspace of %zu bytes is smaller than the %zu bytes this layer needs",
+                        workspace_bytes, sz.shared);
+    }
     tmt_moe* m = new (std::nothrow) tmt_moe();
     if (!m) return fail(TMT_MOE_ENOMEM, "host allocation failed");
     m->desc = *desc;
@@ -546,13 +582,15 @@ int tmt_moe_create(const tmt_moe_desc* desc, tmt_moe** out) {
         delete m;
         return fail(TMT_MOE_EDEVICE, "hipGetDevice failed: %s", hipGetErrorString(err));
     }
-    m->arena_bytes = plan(desc, nullptr);
+    m->own_ws = workspace == nullptr;
+    m->arena_bytes = sz.layer + (m->own_ws ? sz.shared : 0);
     err = hipMalloc(&m->arena, m->arena_bytes);
     if (err != hipSuccess) {
         delete m;
         (void)hipGetLastError();
         return fail(TMT_MOE_ENOMEM, "hipMalloc(%zu) failed: %s", m->arena_bytes, hipGetErrorString(err));
     }
+    m->ws = m->own_ws ? m->arena + sz.layer : static_cast<char*>(workspace);
     plan(desc, m);
     // The decode router's ticket starts at zero (each call leaves it at zero).
     err = hipMemset(m->ticket, 0, sizeof(int32_t));
@@ -565,6 +603,19 @@ int tmt_moe_create(const tmt_moe_desc* desc, tmt_moe** out) {
     }
     *out = m;
     return TMT_MOE_OK;
+}
+}  // namespace
+
+int tmt_moe_create(const tmt_moe_desc* desc, tmt_moe** out) {
+    return create_handle(desc, nullptr, 0, out);
+}
+
+int tmt_moe_create_shared(const tmt_moe_desc* desc, void* workspace, size_t workspace_bytes, tmt_moe** out) {
+    if (!workspace) {
+        if (out) *out = nullptr;
+        return fail(TMT_MOE_EINVAL, "workspace is NULL (use tmt_moe_create for a private one)");
+    }
+    return create_handle(desc, workspace, workspace_bytes, out);
 }
 
 int tmt_moe_destroy(tmt_moe* m) {
@@ -658,6 +709,11 @@ int tmt_moe_backward(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_
                      const uint16_t* Wr, const uint16_t* const* W_up,
                      const uint16_t* const* W_down, float aux_coef, float z_coef,
                      uint16_t* dX, float* dWr, float* const* dW_up, float* const* dW_down) {
+    // After tmt_moe_forward_ln the router ran on the internal LayerNorm output,
+    // which the caller cannot pass as X: that forward pairs with
+    // tmt_moe_backward_ln only.
+    if (m && m->last_T >= 0 && m->last_ln)
+        return fail(TMT_MOE_ESTATE, "the last forward was tmt_moe_forward_ln: use tmt_moe_backward_ln");
     int rc = check_backward(m, dY, X, Wr, W_up, W_down, dX, dWr, dW_up, dW_down);
     if (rc) return rc;
     return run_backward(m, (hipStream_t)stream, dY, X, Wr, W_up, W_down, aux_coef, z_coef, dX, dWr,

@@ -28,6 +28,8 @@ EXPORTED = (
     "tmt_moe_create",
     "tmt_moe_destroy",
     "tmt_moe_workspace_size",
+    "tmt_moe_workspace_sizes",
+    "tmt_moe_create_shared",
     "tmt_moe_forward",
     "tmt_moe_forward_mxfp4",
     "tmt_moe_backward",
@@ -85,6 +87,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.tmt_moe_create.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(vp)]
     lib.tmt_moe_destroy.argtypes = [vp]
     lib.tmt_moe_workspace_size.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t)]
+    lib.tmt_moe_workspace_sizes.argtypes = [ctypes.POINTER(Desc), ctypes.POINTER(ctypes.c_size_t),
+                                            ctypes.POINTER(ctypes.c_size_t)]
+    lib.tmt_moe_create_shared.argtypes = [ctypes.POINTER(Desc), vp, ctypes.c_size_t, ctypes.POINTER(vp)]
     lib.tmt_moe_forward.argtypes = [vp, vp, i32, vp, vp, vp, pp, pp, vp, f32]
     lib.tmt_moe_forward_mxfp4.argtypes = [vp, vp, i32, vp, vp, vp, pp, pp, pp, pp, vp, f32]
     lib.tmt_moe_backward.argtypes = [vp, vp, vp, vp, vp, pp, pp, f32, f32, vp, vp, pp, pp]
@@ -168,6 +173,16 @@ def workspace_size(max_tokens: int, d: int, experts: int, topk: int, hidden: int
     return int(out.value)
 
 
+def workspace_sizes(max_tokens: int, d: int, experts: int, topk: int, hidden: int,
+                    weight_format: int = WEIGHTS_BF16) -> tuple:
+    """(per-layer bytes, shared bytes) of a handle's device memory."""
+    lib = load_library()
+    desc = Desc(max_tokens, d, experts, topk, hidden, weight_format)
+    a, b = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    _check(lib.tmt_moe_workspace_sizes(ctypes.byref(desc), ctypes.byref(a), ctypes.byref(b)))
+    return int(a.value), int(b.value)
+
+
 def layernorm_workspace_size(T: int, d: int) -> int:
     """Bytes of device workspace layernorm_backward needs for [T, d]."""
     out = ctypes.c_size_t(0)
@@ -199,13 +214,22 @@ class MoE:
     """One MoE layer's device state (the reference's MoeKeep + MoeWs)."""
 
     def __init__(self, max_tokens: int, d: int, experts: int, topk: int,
-                 hidden: int = 0, weight_format: int = WEIGHTS_BF16):
+                 hidden: int = 0, weight_format: int = WEIGHTS_BF16, workspace=None):
+        """workspace: optional device tensor shared with other layers
+        (tmt_moe_create_shared; at least workspace_sizes(...)[1] bytes,
+        kept alive by the caller while this layer exists)."""
         self.lib = load_library()
         self.desc = Desc(max_tokens, d, experts, topk, hidden, weight_format)
         self.E, self.K, self.d, self.h = experts, topk, d, hidden
         self.hn = hidden if hidden > 0 else d
         h = ctypes.c_void_p(0)
-        _check(self.lib.tmt_moe_create(ctypes.byref(self.desc), ctypes.byref(h)))
+        if workspace is None:
+            _check(self.lib.tmt_moe_create(ctypes.byref(self.desc), ctypes.byref(h)))
+        else:
+            nbytes = workspace.numel() * workspace.element_size()
+            _check(self.lib.tmt_moe_create_shared(ctypes.byref(self.desc), _ptr(workspace),
+                                                  nbytes, ctypes.byref(h)))
+        self._workspace = workspace
         self.handle = h
         self.T = None
 

@@ -278,7 +278,8 @@ static void test_deferred_stats() {
 
 // The recurrent model's use of the layer (model.cu:252-258, 512-514,
 // 542-549, 672-677; capi.cu:131-136; train_main.cu:232-248): three layers
-// with E = 32 (above the reference's old limit of 16), one shared MoeWs,
+// with E = 32 (above the reference's old limit of 16), one shared MoeWs
+// (checked bit for bit against private workspaces),
 // residual add through beta = 1, statistics deferred into per-layer slots
 // with a stride of 17 floats and read with one copy, expert counts, the
 // router balance line, and the backward in reverse layer order with the
@@ -321,9 +322,11 @@ static void test_model_flow() {
     for (int l = 0; l < L; ++l) {
         aux_acc += moe_aux_from(layers[l], &hs[(size_t)l * 17]);
         z_acc += layers[l].zloss;
-        // the same layer read immediately gives the same statistics
+        // the same layer read immediately gives the same statistics; these
+        // copies run on private workspaces (an MoeWs that was never allocated)
         uint16_t* Yi = dev.alloc<uint16_t>((size_t)N * D);
-        const float ai = moe_forward(X[l], Wr[l], Wx[l].data(), Yi, immediate[l], ws, N, E, K, D, 0.f);
+        MoeWs priv;
+        const float ai = moe_forward(X[l], Wr[l], Wx[l].data(), Yi, immediate[l], priv, N, E, K, D, 0.f);
         require(ai == hs[(size_t)l * 17] && immediate[l].zloss == layers[l].zloss,
                 "deferred statistics differ from the immediate read");
     }
@@ -352,8 +355,20 @@ static void test_model_flow() {
     // backward, last layer first, coefficients / L
     uint16_t* dY = dev.upload(normal_bf16(g, (size_t)N * D, 1.f));
     uint16_t* dXl = dev.alloc<uint16_t>((size_t)N * D);
+    uint16_t* dXp = dev.alloc<uint16_t>((size_t)N * D);
+    float* dWrp = dev.alloc<float>((size_t)E * D);
+    std::vector<float*> dWxp(E);
+    for (int e = 0; e < E; ++e) dWxp[e] = dev.alloc<float>((size_t)D * D);
     for (int l = L - 1; l >= 0; --l) {
         moe_backward(dY, Wx[l].data(), Wr[l], dWr[l], dWx[l].data(), dXl, layers[l], ws, aux_c / L, z_c / L);
+        // the same backward on the layer copy with a private workspace: the
+        // shared workspace gives the same bits
+        MoeWs priv;
+        moe_backward(dY, Wx[l].data(), Wr[l], dWrp, dWxp.data(), dXp, immediate[l], priv, aux_c / L, z_c / L);
+        require(download(dXl, (size_t)N * D) == download(dXp, (size_t)N * D) &&
+                    download(dWr[l], (size_t)E * D) == download(dWrp, (size_t)E * D) &&
+                    download(dWx[l][E - 1], (size_t)D * D) == download(dWxp[E - 1], (size_t)D * D),
+                "backward over the shared workspace differs from a private workspace");
         auto gx = to_f32(download(dXl, (size_t)N * D));
         auto gr = download(dWr[l], (size_t)E * D);
         for (float v : gx) require(std::isfinite(v), "dX finite");

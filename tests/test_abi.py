@@ -41,6 +41,22 @@ def test_workspace_size_matches_layout():
     assert ref_mode < tmt_moe.workspace_size(2048, 256, 4, 2, 1024)
 
 
+def test_shared_workspace_split():
+    """The transient buffers (the reference's MoeWs) are reported apart from
+    the per-layer state, so several layers can share one set: at c3 the
+    backward operands dO, dU, dXg and Xg alone are 1.75 GiB."""
+    total = tmt_moe.workspace_size(32768, 1024, 16, 4, 4096)
+    layer, shared = tmt_moe.workspace_sizes(32768, 1024, 16, 4, 4096)
+    assert layer + shared == total
+    TK = 32768 * 4
+    assert shared >= TK * 4096 * 2 + 3 * TK * 1024 * 2
+    # per layer: U, SiLU(U) (TK x h) and O (TK x d) dominate
+    assert 2 * TK * 4096 * 2 + TK * 1024 * 2 <= layer <= 2 * TK * 4096 * 2 + TK * 1024 * 2 + (128 << 20)
+    # a forward-only MXFP4 handle keeps no backward buffers
+    l4, s4 = tmt_moe.workspace_sizes(65536, 1024, 32, 4, 4096, tmt_moe.WEIGHTS_MXFP4)
+    assert s4 < (64 << 20)
+
+
 @pytest.mark.parametrize("desc,msg", [
     ((16, 100, 4, 2, 0), "multiple of 64"),
     ((16, 128, 0, 1, 0), "experts"),
@@ -49,13 +65,25 @@ def test_workspace_size_matches_layout():
     ((16, 128, 16, 9, 0), "topk"),
     ((16, 128, 4, 2, 100), "hidden"),
     ((0, 128, 4, 2, 0), "max_tokens"),
-    ((16, 4096, 16, 2, 0), "LDS"),
+    ((16, 1000, 16, 2, 0), "multiple of 64"),  # contract difference: TMT accepts any dim
 ])
 def test_invalid_descriptors_are_rejected(desc, msg):
     with pytest.raises(tmt_moe.MoeError) as ei:
         tmt_moe.workspace_size(*desc)
     assert ei.value.code == -1
     assert msg in str(ei.value)
+
+
+@pytest.mark.parametrize("desc", [
+    (16, 4096, 16, 4, 0),     # E*d = 65536: router weights beyond the LDS-staged size
+    (16, 2560, 16, 4, 0),
+    (16, 1280, 8, 2, 0),      # the reference's profile shape (tmt-cuda/src/profile.cu:17)
+    (16, 2048, 64, 8, 512),   # widest router with up/down experts
+])
+def test_reference_dims_are_accepted(desc):
+    """TMT accepts experts <= 16 with any dim (tmt-cuda/src/config.h:46-52);
+    the library takes E up to 64 with any d that is a multiple of 64."""
+    assert tmt_moe.workspace_size(*desc) > 0
 
 
 def test_layernorm_workspace_and_argument_checks():
