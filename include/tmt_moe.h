@@ -232,6 +232,23 @@ int tmt_moe_layernorm_backward(void* stream, int32_t T, int32_t d, const uint16_
                                void* workspace, size_t workspace_bytes);
 
 /*
+ * tmt_moe_layernorm_backward without the workspace argument, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No reference counterpart
+ * (the reference's layernorm_bwd allocates nothing but also keeps no
+ * workspace, norm.cu:102-106). The scratch is a 4 MiB device array inside
+ * the library (one per GPU, held until the process ends): shapes whose
+ * workspace (tmt_moe_layernorm_workspace_size) exceeds 4 MiB are rejected
+ * with TMT_MOE_EINVAL, e.g. T = 32768 at d = 1024 uses 0.53 MiB. No call
+ * allocates. Every call on one GPU uses that GPU's same scratch: calls that
+ * overlap on one GPU (different streams, or threads, without ordering) race.
+ * Same results, bit for bit, as tmt_moe_layernorm_backward.
+ */
+int tmt_moe_layernorm_backward_noalloc(void* stream, int32_t T, int32_t d, const uint16_t* S,
+                                       const uint16_t* dH, const float* gamma, const float* mean,
+                                       const float* rstd, uint16_t* dS, float* dGamma, float* dBeta);
+
+/*
  * Parity/debug: waits for `stream` and copies what the last
  * tmt_moe_forward_ln kept: H [T][d] bf16, mean and rstd [T] fp32 (the
  * reference's Ly.mean / Ly.rstd, model.cu:510-511). Any pointer may be NULL.

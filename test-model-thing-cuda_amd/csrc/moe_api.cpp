@@ -14,6 +14,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -21,6 +22,14 @@
 #include "moe_internal.hpp"
 
 using namespace tmt;
+
+// Scratch of tmt_moe_layernorm_backward_noalloc: a file-scope device array,
+// so that entry point never allocates. Each GPU the library runs on holds
+// its own copy, at its own address, until the process ends. Host code uses
+// the per-device address from hipGetSymbolAddress (scratch_on_current_device),
+// never the array's name, which is only a host-side stand-in.
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
 namespace {
 
@@ -44,6 +53,31 @@ int fail(int code, const char* fmt, ...) {
     } while (0)
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Device address of `scratch` on the current device, looked up on the first
+// call made with that device current and kept per device.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_addr[kMaxDevices] = {};
+
+int scratch_on_current_device(float** out) {
+    int dev = -1;
+    HIP_TRY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(TMT_MOE_EINVAL, "device index %d is out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (g_scratch_addr[dev] == nullptr) {
+        void* addr = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || addr == nullptr) {
+            (void)hipGetLastError();
+            return fail(TMT_MOE_EDEVICE, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                        hipGetErrorString(err));
+        }
+        g_scratch_addr[dev] = static_cast<float*>(addr);
+    }
+    *out = g_scratch_addr[dev];
+    return TMT_MOE_OK;
+}
 
 struct Layout {
     size_t total = 0;
@@ -533,6 +567,36 @@ size_t ln_workspace_floats(int32_t T, int32_t d, size_t* level1_off) {
     return off + (size_t)colsum_groups((int)nch) * 2 * d;
 }
 
+int check_ln_backward_args(int32_t T, int32_t d, const uint16_t* S, const uint16_t* dH, const float* gamma,
+                           const float* mean, const float* rstd, const uint16_t* dS, const float* dGamma,
+                           const float* dBeta) {
+    int rc = check_ln_shape(T, d);
+    if (rc) return rc;
+    if (T > 0 && (!S || !dH || !mean || !rstd || !dS))
+        return fail(TMT_MOE_EINVAL, "S, dH, mean, rstd and dS must be non-NULL");
+    if (!gamma || !dGamma || !dBeta) return fail(TMT_MOE_EINVAL, "gamma, dGamma and dBeta must be non-NULL");
+    if (!aligned16(S) || !aligned16(dH) || !aligned16(dS) || !aligned16(gamma) || !aligned16(dGamma) ||
+        !aligned16(dBeta))
+        return fail(TMT_MOE_EINVAL, "S, dH, dS, gamma, dGamma and dBeta must be 16-byte aligned");
+    return TMT_MOE_OK;
+}
+
+// The LayerNorm backward's launches over a workspace at `ws` (chunk
+// partials, then the level-1 column sums from float offset `level1_off`).
+// Every workspace element the kernels read is written by them first.
+int run_ln_backward(hipStream_t s, int32_t T, int32_t d, const uint16_t* S, const uint16_t* dH,
+                    const float* gamma, const float* mean, const float* rstd, uint16_t* dS, float* dGamma,
+                    float* dBeta, float* ws, size_t level1_off) {
+    LayerNormParams p{};
+    p.S = S; p.gamma = gamma; p.T = T; p.d = d; p.mean = const_cast<float*>(mean);
+    p.rstd = const_cast<float*>(rstd); p.dH = dH; p.dS = dS;
+    p.partial = ws;
+    p.partial2 = ws + level1_off;
+    p.dgamma = dGamma; p.dbeta = dBeta;
+    HIP_TRY(launch_ln_bwd(p, s));
+    return TMT_MOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -849,28 +913,32 @@ int tmt_moe_layernorm_forward(void* stream, int32_t T, int32_t d, const uint16_t
 int tmt_moe_layernorm_backward(void* stream, int32_t T, int32_t d, const uint16_t* S, const uint16_t* dH,
                                const float* gamma, const float* mean, const float* rstd, uint16_t* dS,
                                float* dGamma, float* dBeta, void* workspace, size_t workspace_bytes) {
-    int rc = check_ln_shape(T, d);
+    int rc = check_ln_backward_args(T, d, S, dH, gamma, mean, rstd, dS, dGamma, dBeta);
     if (rc) return rc;
-    if (T > 0 && (!S || !dH || !mean || !rstd || !dS))
-        return fail(TMT_MOE_EINVAL, "S, dH, mean, rstd and dS must be non-NULL");
-    if (!gamma || !dGamma || !dBeta) return fail(TMT_MOE_EINVAL, "gamma, dGamma and dBeta must be non-NULL");
-    if (!aligned16(S) || !aligned16(dH) || !aligned16(dS) || !aligned16(gamma) || !aligned16(dGamma) ||
-        !aligned16(dBeta))
-        return fail(TMT_MOE_EINVAL, "S, dH, dS, gamma, dGamma and dBeta must be 16-byte aligned");
     size_t off;
     const size_t need = ln_workspace_floats(T, d, &off) * 4;
     if (!workspace || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
         return fail(TMT_MOE_EINVAL, "workspace must be a 256-byte aligned device pointer");
     if (workspace_bytes < need)
         return fail(TMT_MOE_EINVAL, "workspace of %zu bytes is smaller than the %zu bytes needed", workspace_bytes, need);
-    LayerNormParams p{};
-    p.S = S; p.gamma = gamma; p.T = T; p.d = d; p.mean = const_cast<float*>(mean);
-    p.rstd = const_cast<float*>(rstd); p.dH = dH; p.dS = dS;
-    p.partial = static_cast<float*>(workspace);
-    p.partial2 = static_cast<float*>(workspace) + off;
-    p.dgamma = dGamma; p.dbeta = dBeta;
-    HIP_TRY(launch_ln_bwd(p, (hipStream_t)stream));
-    return TMT_MOE_OK;
+    return run_ln_backward((hipStream_t)stream, T, d, S, dH, gamma, mean, rstd, dS, dGamma, dBeta,
+                           static_cast<float*>(workspace), off);
+}
+
+int tmt_moe_layernorm_backward_noalloc(void* stream, int32_t T, int32_t d, const uint16_t* S,
+                                       const uint16_t* dH, const float* gamma, const float* mean,
+                                       const float* rstd, uint16_t* dS, float* dGamma, float* dBeta) {
+    int rc = check_ln_backward_args(T, d, S, dH, gamma, mean, rstd, dS, dGamma, dBeta);
+    if (rc) return rc;
+    size_t off;
+    const size_t need = ln_workspace_floats(T, d, &off) * 4;
+    if (need > kNoAllocScratchBytes)
+        return fail(TMT_MOE_EINVAL,
+                    "T=%d, d=%d needs %zu bytes of scratch, more than the %zu bytes this entry point holds",
+                    T, d, need, kNoAllocScratchBytes);
+    float* ws = nullptr;
+    if ((rc = scratch_on_current_device(&ws))) return rc;
+    return run_ln_backward((hipStream_t)stream, T, d, S, dH, gamma, mean, rstd, dS, dGamma, dBeta, ws, off);
 }
 
 int tmt_moe_f32_to_bf16(void* stream, const float* in, uint16_t* out, int64_t n) {

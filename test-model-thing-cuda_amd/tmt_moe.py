@@ -42,6 +42,7 @@ EXPORTED = (
     "tmt_moe_layernorm_workspace_size",
     "tmt_moe_layernorm_forward",
     "tmt_moe_layernorm_backward",
+    "tmt_moe_layernorm_backward_noalloc",
     "tmt_moe_adamw_create",
     "tmt_moe_adamw_destroy",
     "tmt_moe_adamw_step",
@@ -101,6 +102,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.tmt_moe_layernorm_forward.argtypes = [vp, i32, i32, vp, vp, vp, vp, vp, vp]
     lib.tmt_moe_layernorm_backward.argtypes = [vp, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                                ctypes.c_size_t]
+    lib.tmt_moe_layernorm_backward_noalloc.argtypes = [vp, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp]
     lib.tmt_moe_adamw_create.argtypes = [vp, i32, ctypes.POINTER(vp)]
     lib.tmt_moe_adamw_destroy.argtypes = [vp]
     lib.tmt_moe_adamw_step.argtypes = [vp, vp, f32, f32, f32, f32, f32, f32, i32]
@@ -208,6 +210,15 @@ def layernorm_backward(S, dH, gamma, mean, rstd, dS, dGamma, dBeta, workspace,
     _check(load_library().tmt_moe_layernorm_backward(
         _stream(stream), T, d, _ptr(S), _ptr(dH), _ptr(gamma), _ptr(mean), _ptr(rstd), _ptr(dS),
         _ptr(dGamma), _ptr(dBeta), _ptr(workspace), ctypes.c_size_t(nbytes)))
+
+
+def layernorm_backward_noalloc(S, dH, gamma, mean, rstd, dS, dGamma, dBeta, stream=None) -> None:
+    """layernorm_backward over the library's own 4 MiB device scratch (no
+    allocation, no workspace argument; calls overlapping on one GPU race)."""
+    T, d = int(S.shape[0]), int(S.shape[1])
+    _check(load_library().tmt_moe_layernorm_backward_noalloc(
+        _stream(stream), T, d, _ptr(S), _ptr(dH), _ptr(gamma), _ptr(mean), _ptr(rstd), _ptr(dS),
+        _ptr(dGamma), _ptr(dBeta)))
 
 
 class MoE:

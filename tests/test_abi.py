@@ -106,6 +106,21 @@ def test_layernorm_workspace_and_argument_checks():
     assert "smaller than" in tmt_moe.last_error()
 
 
+def test_noalloc_layernorm_rejects_shapes_beyond_its_scratch():
+    """tmt_moe_layernorm_backward_noalloc holds 4 MiB of device scratch: a
+    shape whose workspace is larger fails its argument check, before any
+    device call (so this runs without a GPU)."""
+    lib = tmt_moe.load_library()
+    T, d = 1 << 20, 2048
+    assert tmt_moe.layernorm_workspace_size(T, d) > (4 << 20)
+    p = ctypes.c_void_p(256)  # aligned stand-in: never dereferenced
+    rc = lib.tmt_moe_layernorm_backward_noalloc(None, T, d, p, p, p, p, p, p, p, p)
+    assert rc == -1
+    assert b"bytes of scratch" in lib.tmt_moe_last_error()
+    # the largest c3-sized standalone LayerNorm fits
+    assert tmt_moe.layernorm_workspace_size(32768, 1024) <= (4 << 20)
+
+
 def test_adamw_argument_checks():
     lib = tmt_moe.load_library()
     out = ctypes.c_void_p(0)
