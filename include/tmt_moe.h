@@ -46,7 +46,16 @@ enum {
     TMT_MOE_ESTATE = -4    /* backward without a matching forward */
 };
 
-enum { TMT_MOE_WEIGHTS_BF16 = 0, TMT_MOE_WEIGHTS_MXFP4 = 1 };
+/* Expert weight formats (tmt_moe_desc::weight_format):
+ *   BF16      bf16 weights, forward and backward;
+ *   MXFP4     MXFP4 weights expanded to bf16 inside the GEMM, bf16
+ *             activations: the products equal the fp32 products with the
+ *             dequantised weights (forward only);
+ *   MXFP4_MX  MXFP4 weights on the scaled MFMA, activations rounded to the
+ *             sum of two MXFP6 (e2m3) terms per 32-element block (relative
+ *             L2 error of the block output about 1e-3), about twice the MFMA
+ *             rate of the bf16 products (forward only). */
+enum { TMT_MOE_WEIGHTS_BF16 = 0, TMT_MOE_WEIGHTS_MXFP4 = 1, TMT_MOE_WEIGHTS_MXFP4_MX = 2 };
 
 typedef struct tmt_moe_desc {
     int32_t max_tokens;     /* T_max: largest T a call may pass */
@@ -110,7 +119,8 @@ int tmt_moe_forward(tmt_moe* moe, void* stream, int32_t T, const uint16_t* X,
                     uint16_t* Y, float beta);
 
 /*
- * MXFP4 variant of tmt_moe_forward for weight_format == TMT_MOE_WEIGHTS_MXFP4
+ * MXFP4 variant of tmt_moe_forward for weight_format TMT_MOE_WEIGHTS_MXFP4 or
+ * TMT_MOE_WEIGHTS_MXFP4_MX
  * (no reference counterpart: the reference has no FP4 path). OCP MX format:
  * e2m1 values in blocks of 32 along the reduction dimension sharing one e8m0
  * scale 2^(s-127). Per expert e:
@@ -118,9 +128,11 @@ int tmt_moe_forward(tmt_moe* moe, void* stream, int32_t T, const uint16_t* X,
  *   W_up_scale[e]  scales [d/32][h] bytes (block-major: the scales of one
  *                  K block are contiguous over the output rows)
  *   W_down[e]      [d][h/2] bytes,  W_down_scale[e]  [h/32][d] bytes.
- * Activations stay bf16; weights are expanded to bf16 (exactly) inside the
- * GEMM, so the result matches the fp32 product with dequantised weights.
- * Forward only: backward needs bf16 master weights.
+ * With MXFP4, activations stay bf16 and the weights are expanded to bf16
+ * (exactly) inside the GEMM, so the result matches the fp32 product with
+ * dequantised weights. With MXFP4_MX, the block input and the SiLU output
+ * are rounded to two MXFP6 terms and both expert GEMMs run on the scaled
+ * FP6 x FP4 MFMA. Forward only: backward needs bf16 master weights.
  */
 int tmt_moe_forward_mxfp4(tmt_moe* moe, void* stream, int32_t T,
                           const uint16_t* X, const uint16_t* Wr,

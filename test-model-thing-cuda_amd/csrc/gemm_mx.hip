@@ -1,0 +1,460 @@
+// gemm_mx.hip -- MXFP4 expert GEMMs on gfx950's scaled MFMA.
+//
+// The MXFP4 forward (no counterpart in the reference, which has no FP4
+// path) with activations in MX form as well, so both operands feed
+// v_mfma_scale_f32_32x32x64_f8f6f4 directly:
+//   weights      e2m1 codes + e8m0 scales per 32 along K (the layout of
+//                tmt_moe_forward_mxfp4: codes [N][K/2], low nibble first;
+//                scales [K/32][N]);
+//   activations  the sum of two e2m3 (FP6) terms, each with its own e8m0
+//                scale per 32 along K: x ~ q0 * 2^(s0-127) + q1 * 2^(s1-127),
+//                q0 = RNE(x / 2^e0) with e0 = floor(log2 max|x|) - 2 over the
+//                block, q1 the same rounding of the residual x - q0 * 2^e0.
+//                Relative L2 error about 4e-4 on the c5 operands, against
+//                3e-2 for one term.
+// FP6 x FP4 products issue at the 8-pass rate, so the two terms together take
+// half the MFMA time of one bf16 product over the same K.
+//
+// Activation tensors ("MX6x2") in slot order, rows R, length K (K % 64 == 0):
+//   codes  [R][K/32][48] bytes: per 32-block, term 0 (24 bytes, element i at
+//          bits 6i..6i+5, little-endian) then term 1;
+//   scales [K/64][srows][4] bytes: per row and 64-column pair of blocks
+//          (block 2c term 0, block 2c term 1, block 2c+1 term 0, block 2c+1
+//          term 1); srows >= R + 256 so whole-tile loads stay in bounds.
+//
+// Lane layout of the scaled MFMA (checked on the GPU against a host model):
+// lane l supplies row l % 32, K elements 32 * (l / 32) .. + 31 of each
+// operand, and byte `opsel` of its scale register scales that row's block.
+// D[i][j] = sum_k src0[i][k] * src1[j][k] lands in lane j, register i as for
+// the bf16 32x32 MFMAs. Weights are src0 (rows = output columns n), the
+// activation terms src1 (lanes = token rows m), as in gemm.hip.
+#include "device_util.hpp"
+#include "moe_internal.hpp"
+
+namespace tmt {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned u32x6 __attribute__((ext_vector_type(6)));
+typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int BM = kGemmTileRows;  // 256 token rows per tile
+constexpr int BN = 256;            // output columns per tile
+constexpr int NST = 4;             // LDS ring stages of K = 64
+// One stage: activation codes [2 blocks][256 rows][48 B], weight codes
+// [2 blocks][256 n][16 B], activation scales [256 rows][4 B], weight scales
+// [2 blocks][256 n] (a 1 KiB load; the second half is unused).
+constexpr int A_BYTES = 2 * BM * 48;
+constexpr int B_BYTES = 2 * BN * 16;
+constexpr int AS_BYTES = 1024, BS_BYTES = 1024;
+constexpr int STAGE = A_BYTES + B_BYTES + AS_BYTES + BS_BYTES;
+constexpr int A_LOADS = A_BYTES / 1024 / 4;  // 1 KiB wave loads per wave
+constexpr int B_LOADS = B_BYTES / 1024 / 4;
+constexpr int DMA_PER_TILE = A_LOADS + B_LOADS + 1;
+constexpr int EPR = 64, WTN = 128;  // epilogue: rows per wave and pass, wave tile width
+constexpr int EPI = 4 * EPR * WTN * 4;
+constexpr int LDS_BYTES = NST * STAGE > EPI ? NST * STAGE : EPI;
+static_assert(LDS_BYTES <= 160 * 1024, "LDS ring too large");
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// One wave-wide 16-byte-per-lane load from global memory (wave-uniform base
+// plus a 32-bit per-lane byte offset) into LDS at lds_base + 16 * lane
+// (lds_base wave-uniform); M0 is declared clobbered.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base) : "m0");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
+}
+__device__ __forceinline__ void st16_nt(void* p, uint4 v) {
+    __builtin_nontemporal_store(u32x4_t{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4_t*>(p));
+}
+
+// floor(log2(amax)) - 2, the e8m0 exponent that maps the block maximum into
+// [4, 8) of e2m3's range (largest value 7.5), clamped to [-127, 127]; zero
+// and subnormal maxima give -127.
+__device__ __forceinline__ int mx6_exponent(float amax) {
+    const int be = (int)((__float_as_uint(amax) >> 23) & 255);
+    return be == 0 ? -127 : max(-127, be - 129);
+}
+__device__ __forceinline__ float exp2_int(int e) {  // 2^e for e in [-127, 127]
+    return e >= -126 ? __uint_as_float((uint32_t)(e + 127) << 23) : __uint_as_float(0x00400000u);
+}
+
+// 32 values (natural order) to e2m3 codes at scale 2^e (six packed dwords,
+// element i at bits 6i). The conversion writes its destination while it still
+// reads its sources, so the sources are kept live past it: the destination
+// never shares a register with them.
+__device__ __forceinline__ u32x6 to_e2m3(const float* x, float scale) {
+    f32x16 ev, od;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        ev[i] = x[2 * i];  // packed element 2i comes from the first operand
+        od[i] = x[2 * i + 1];
+    }
+    u32x6 q = __builtin_amdgcn_cvt_scalef32_2xpk16_fp6_f32(ev, od, scale);
+    asm volatile("" : "+v"(q) : "v"(ev), "v"(od), "v"(scale));
+    return q;
+}
+__device__ __forceinline__ void from_e2m3(u32x6 q, float scale, float* out) {
+    auto d = __builtin_amdgcn_cvt_scalef32_pk32_f32_fp6(q, scale);
+    asm volatile("" : "+v"(d) : "v"(q), "v"(scale));
+#pragma unroll
+    for (int i = 0; i < 32; ++i) out[i] = d[i];
+}
+
+// One 32-block to two e2m3 terms: codes t0, t1 and the scale bytes.
+__device__ __forceinline__ void quant_block2(const float* x, u32x6& t0, u32x6& t1, uint32_t& s0, uint32_t& s1) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
+    const int e0 = mx6_exponent(amax);
+    const float sc0 = exp2_int(e0);
+    t0 = to_e2m3(x, sc0);
+    float r[32];
+    from_e2m3(t0, sc0, r);
+    float amax1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+        r[i] = x[i] - r[i];
+        amax1 = fmaxf(amax1, fabsf(r[i]));
+    }
+    const int e1 = mx6_exponent(amax1);
+    t1 = to_e2m3(r, exp2_int(e1));
+    s0 = (uint32_t)(e0 + 127);
+    s1 = (uint32_t)(e1 + 127);
+}
+
+// Store a 64-column group (two 32-blocks) of one row: 96 code bytes and the
+// row's scale dword of that group.
+__device__ __forceinline__ void store_group(uint8_t* codes, uint8_t* scales, const u32x6* t, const uint32_t* s) {
+    uint4* dst = reinterpret_cast<uint4*>(codes);
+    dst[0] = make_uint4(t[0][0], t[0][1], t[0][2], t[0][3]);
+    dst[1] = make_uint4(t[0][4], t[0][5], t[1][0], t[1][1]);
+    dst[2] = make_uint4(t[1][2], t[1][3], t[1][4], t[1][5]);
+    dst[3] = make_uint4(t[2][0], t[2][1], t[2][2], t[2][3]);
+    dst[4] = make_uint4(t[2][4], t[2][5], t[3][0], t[3][1]);
+    dst[5] = make_uint4(t[3][2], t[3][3], t[3][4], t[3][5]);
+    *reinterpret_cast<uint32_t*>(scales) = s[0] | (s[1] << 8) | (s[2] << 16) | (s[3] << 24);
+}
+
+// bf16 rows (gathered through perm when given) to MX6x2: one thread per
+// (row, 64-column group).
+__global__ __launch_bounds__(kThreads) void mx_quant_rows_kernel(MxQuantParams p) {
+    const int groups = p.K / 64;
+    const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    if (idx >= (int64_t)p.rows * groups) return;
+    const int r = (int)(idx / groups), c = (int)(idx % groups);
+    const int src = p.perm ? p.perm[r] : r;
+    const uint4* x = reinterpret_cast<const uint4*>(p.X + (int64_t)src * p.ldx + c * 64);
+    uint4 v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = x[i];
+    float f[64];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) unpack8(v[i], f + 8 * i);
+    u32x6 t[4];
+    uint32_t s[4];
+    quant_block2(f, t[0], t[1], s[0], s[1]);
+    quant_block2(f + 32, t[2], t[3], s[2], s[3]);
+    store_group(p.codes + (int64_t)r * (p.K / 32 * 48) + c * 96, p.scales + ((int64_t)c * p.srows + r) * 4, t, s);
+}
+
+// Expert segment of activation M tile mt: expert, first slot, rows (e < 0: none).
+__device__ __forceinline__ void act_tile(const MxGemmParams& p, int mt, int& e, int& row0, int& rows) {
+    e = -1;
+    int t0 = 0;
+    for (int ee = 0; ee < p.E; ++ee) {
+        const int beg = p.offsets[ee], end = p.offsets[ee + 1];
+        const int tiles = (end - beg + BM - 1) / BM;
+        if (mt < t0 + tiles) {
+            e = ee;
+            row0 = beg + (mt - t0) * BM;
+            rows = min(BM, end - row0);
+            return;
+        }
+        t0 += tiles;
+    }
+}
+
+// QUANT_OUT: the output is SiLU(C) in MX6x2 (the next GEMM's activation);
+// otherwise C in bf16.
+template <bool QUANT_OUT>
+__global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
+    __shared__ uint4 lds_raw[LDS_BYTES / 16];
+    uint8_t* lds = reinterpret_cast<uint8_t*>(lds_raw);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int ntn = (p.N + BN - 1) / BN;
+
+    // ---- tile coordinates: XCD-aware groups of 32 tiles, as in gemm.hip ----
+    const int lid = ((((int)blockIdx.x >> 8) << 3) + ((int)blockIdx.x & 7)) * 32 + (((int)blockIdx.x >> 3) & 31);
+    const int G = lid >> 5, gi = lid & 31;
+    const int gn = min(ntn, 8), gm = 32 / gn;
+    const int ngn = (ntn + gn - 1) / gn;
+    if (gi >= gm * gn) return;
+    const int mt = (G / ngn) * gm + gi % gm;
+    const int nt = (G % ngn) * gn + gi / gm;
+    if (nt >= ntn) return;
+    int e, row0 = 0, rows = 0;
+    act_tile(p, mt, e, row0, rows);
+    if (e < 0) return;
+    const int mlim = rows, nlim = min(BN, p.N - nt * BN);
+    const int nk = p.K / 64;
+    const int64_t a_row_bytes = (int64_t)(p.K / 32) * 48;
+
+    // ---- DMA addressing: wave-uniform bases, 32-bit lane offsets ------------
+    // (the host keeps every offset below 2^31)
+    uint32_t a_off[A_LOADS];
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+        const int s = (wave * A_LOADS + i) * 64 + lane;  // 16-byte slot of the A region
+        const int kb = s / (BM * 3), rem = s % (BM * 3);
+        const int row = rem / 3, c = rem % 3;
+        a_off[i] = (uint32_t)(min(row0 + row, p.slots - 1) * a_row_bytes + kb * 48 + c * 16);
+    }
+    uint32_t b_off[B_LOADS];
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
+        const int s = (wave * B_LOADS + i) * 64 + lane;
+        const int kb = s / BN, n = s % BN;
+        b_off[i] = (uint32_t)(min(nt * BN + n, p.N - 1) * (int64_t)(p.K / 2) + kb * 16);
+    }
+    const uint8_t* wq = p.wq[e];
+    const uint8_t* wsc = p.wsc[e];
+    // scales: waves 0 and 2 load the activation scales (the same bytes to
+    // the same place), waves 1 and 3 the weight scales
+    const bool a_scale_wave = (wave & 1) == 0;
+    uint32_t sc_off;
+    if (a_scale_wave) {
+        sc_off = (uint32_t)(row0 + 4 * lane) * 4u;
+    } else {
+        const int kb = (lane >> 4) & 1;
+        sc_off = (uint32_t)(kb * p.N + min(nt * BN + (lane & 15) * 16, p.N - 16));
+    }
+    const uint32_t sc_lds = a_scale_wave ? A_BYTES + B_BYTES : A_BYTES + B_BYTES + AS_BYTES;
+    const uint32_t lds0 = lds_addr(lds);
+    auto dma_tile = [&](int t) {
+        const int kt = min(t, nk - 1);
+        const uint32_t sb = lds0 + (uint32_t)((t % NST) * STAGE);
+        const uint8_t* ab = p.a_codes + (int64_t)kt * 96;
+        const uint8_t* bb = wq + (int64_t)kt * 32;
+#pragma unroll
+        for (int i = 0; i < A_LOADS; ++i) dma16(ab, a_off[i], sb + (uint32_t)(wave * A_LOADS + i) * 1024u);
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) dma16(bb, b_off[i], sb + A_BYTES + (uint32_t)(wave * B_LOADS + i) * 1024u);
+        const uint8_t* sbase = a_scale_wave ? p.a_scales + (int64_t)kt * p.a_srows * 4 : wsc + (int64_t)kt * 2 * p.N;
+        dma16(sbase, sc_off, sb + sc_lds);
+    };
+
+    // ---- fragments ----------------------------------------------------------
+    // Weight codes (src0): 32 e2m1 per lane in four dwords; activation terms
+    // (src1): six dwords each, read as 16 + 8 bytes (term 0) and 8 + 16
+    // bytes (term 1) so that every operand lands in consecutive registers.
+    const int kb = lane >> 5;
+    const int b_lane = (kb * BN + wn * 128 + (lane & 31)) * 16;           // + 512 j
+    const int bs_lane = A_BYTES + B_BYTES + AS_BYTES + kb * BN + wn * 128 + (lane & 31);  // + 32 j
+    const int a_lane = (kb * BM + wm * 128 + (lane & 31)) * 48;          // + 1536 i
+    const int as_lane = A_BYTES + B_BYTES + (wm * 128 + (lane & 31)) * 4;  // + 128 i
+    const int as_shift = 16 * kb;
+    i32x4 bq[2][4];
+    uint32_t bsc[2][4];
+    i32x8 a0[4], a1[4];
+    uint32_t asc[4];
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+    // B fragments of the tile in stage `sg` into register set `B`.
+#define MX_LOAD_B(B, sg)                                                                              \
+    do {                                                                                              \
+        const uint8_t* st_ = lds + (sg) * STAGE;                                                      \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                               \
+            bq[B][j] = *reinterpret_cast<const i32x4*>(st_ + A_BYTES + b_lane + 512 * j);             \
+            bsc[B][j] = st_[bs_lane + 32 * j];                                                        \
+        }                                                                                             \
+    } while (0)
+    // A fragments of row block i of the tile in stage `sg`.
+#define MX_LOAD_A(i, sg)                                                                              \
+    do {                                                                                              \
+        const uint8_t* pa_ = lds + (sg) * STAGE + a_lane + 1536 * (i);                                \
+        const i32x4 x0_ = *reinterpret_cast<const i32x4*>(pa_);                                       \
+        const i32x2 x1_ = *reinterpret_cast<const i32x2*>(pa_ + 16);                                  \
+        const i32x2 x2_ = *reinterpret_cast<const i32x2*>(pa_ + 24);                                  \
+        const i32x4 x3_ = *reinterpret_cast<const i32x4*>(pa_ + 32);                                  \
+        const i32x4 x1w_ = __builtin_shufflevector(x1_, x1_, 0, 1, -1, -1);                           \
+        const i32x4 x2w_ = __builtin_shufflevector(x2_, x2_, 0, 1, -1, -1);                           \
+        a0[i] = __builtin_shufflevector(x0_, x1w_, 0, 1, 2, 3, 4, 5, -1, -1);                         \
+        a1[i] = __builtin_shufflevector(x2w_, x3_, 0, 1, 4, 5, 6, 7, -1, -1);                         \
+        asc[i] = *reinterpret_cast<const uint32_t*>(lds + (sg) * STAGE + as_lane + 128 * (i)) >> as_shift; \
+    } while (0)
+    // The MFMAs of row block i with register set B.
+#define MX_MMA_ROW(i, B)                                                                              \
+    do {                                                                                              \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                               \
+            const i32x8 w_ = __builtin_shufflevector(bq[B][j], bq[B][j], 0, 1, 2, 3, -1, -1, -1, -1); \
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w_, a0[i], acc[i][j], 4, 2, 0,  \
+                                                                       (int)bsc[B][j], 0, (int)asc[i]); \
+            acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w_, a1[i], acc[i][j], 4, 2, 0,  \
+                                                                       (int)bsc[B][j], 1, (int)asc[i]); \
+        }                                                                                             \
+    } while (0)
+    // One k64 tile t (stage S = t % NST, register set B = t % 2): wait for
+    // tile t+1, request tile t+NST-1, read tile t+1's weight fragments, and
+    // refill each activation row block with tile t+1's right after its MFMAs.
+#define MX_STEP(S, B)                                                                                 \
+    do {                                                                                              \
+        const int t_ = kt + (S);                                                                      \
+        if (t_ < nk) {                                                                                \
+            wait_vm<DMA_PER_TILE>();                                                                  \
+            __syncthreads();                                                                          \
+            dma_tile(t_ + NST - 1);                                                                   \
+            const int sn_ = t_ + 1 < nk ? ((S) + 1) % NST : (S);                                      \
+            MX_LOAD_B((B) ^ 1, sn_);                                                                  \
+            MX_MMA_ROW(0, B);                                                                         \
+            MX_LOAD_A(0, sn_);                                                                        \
+            MX_MMA_ROW(1, B);                                                                         \
+            MX_LOAD_A(1, sn_);                                                                        \
+            MX_MMA_ROW(2, B);                                                                         \
+            MX_LOAD_A(2, sn_);                                                                        \
+            MX_MMA_ROW(3, B);                                                                         \
+            MX_LOAD_A(3, sn_);                                                                        \
+        }                                                                                             \
+    } while (0)
+
+    // ---- main loop, unrolled by the ring depth so that every stage index is
+    // a compile-time constant --------------------------------------------------
+    if (nk > 0) {
+#pragma unroll
+        for (int t = 0; t < NST - 1; ++t) dma_tile(t);
+        wait_vm<(NST - 2) * DMA_PER_TILE>();
+        __syncthreads();
+        MX_LOAD_B(0, 0);
+        MX_LOAD_A(0, 0);
+        MX_LOAD_A(1, 0);
+        MX_LOAD_A(2, 0);
+        MX_LOAD_A(3, 0);
+        for (int kt = 0; kt < nk; kt += NST) {
+            MX_STEP(0, 0);
+            MX_STEP(1, 1);
+            MX_STEP(2, 0);
+            MX_STEP(3, 1);
+        }
+    }
+#undef MX_STEP
+#undef MX_MMA_ROW
+#undef MX_LOAD_A
+#undef MX_LOAD_B
+    wait_vm<0>();
+    __syncthreads();
+
+    // ---- epilogue -----------------------------------------------------------
+    // acc[i][j][r] = C[m][n] with m = wm*128 + 32i + (lane&31) and
+    // n = wn*128 + 32j + 8(r>>2) + 4(lane>>5) + (r&3); staged per wave as fp32
+    // rows [EPR][WTN] (16-byte chunks swizzled by row), two passes.
+    constexpr int CH = WTN / 4;
+    float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (EPR * WTN);
+    const int mbase = wm * 128, nbase = wn * 128;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii) {
+            const int i = pass * 2 + ii;
+            const int lr = ii * 32 + (lane & 31);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int ch = j * 8 + 2 * q + (lane >> 5);
+                    *reinterpret_cast<f32x4*>(stage_f + lr * WTN + ((ch ^ (lr & (CH - 1))) * 4)) =
+                        f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                }
+        }
+        __syncthreads();
+        if constexpr (QUANT_OUT) {
+            // lane -> (row rr, 64-column group g): two items per lane and pass
+#pragma unroll 1
+            for (int it = 0; it < 2; ++it) {
+                const int item = it * 64 + lane;
+                const int rr = item >> 1, g = item & 1;
+                const int m = mbase + pass * EPR + rr;
+                const int n = nbase + g * 64;
+                if (m < mlim && n < nlim) {
+                    float x[64];
+                    const float* src = stage_f + rr * WTN;
+#pragma unroll
+                    for (int c = 0; c < 16; ++c) {
+                        const f32x4 v = *reinterpret_cast<const f32x4*>(src + (((g * 16 + c) ^ (rr & (CH - 1))) * 4));
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) x[4 * c + u] = silu_fast(v[u]);
+                    }
+                    u32x6 t[4];
+                    uint32_t s[4];
+                    quant_block2(x, t[0], t[1], s[0], s[1]);
+                    quant_block2(x + 32, t[2], t[3], s[2], s[3]);
+                    const int slot = row0 + m;
+                    const int col = nt * BN + n;  // multiple of 64
+                    store_group(p.q_codes + (int64_t)slot * (p.N / 32 * 48) + (col / 32) * 48,
+                                p.q_scales + ((int64_t)(col / 64) * p.q_srows + slot) * 4, t, s);
+                }
+            }
+        } else {
+            constexpr int LPR = WTN / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
+            uint16_t* C = p.c;
+            const int cl = lane % LPR;
+            const int n = nbase + cl * 8;
+#pragma unroll
+            for (int k = 0; k < EPR / RPI; ++k) {
+                const int rr = lane / LPR + RPI * k;
+                const int m = mbase + pass * EPR + rr;
+                if (m >= mlim || n >= nlim) continue;
+                const float* src = stage_f + rr * WTN;
+                const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + (((2 * cl) ^ (rr & (CH - 1))) * 4));
+                const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + (((2 * cl + 1) ^ (rr & (CH - 1))) * 4));
+                const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                st16_nt(C + (int64_t)(row0 + m) * p.ldc + nt * BN + n, pack8(v));
+            }
+        }
+        __syncthreads();
+    }
+}
+
+}  // namespace
+
+hipError_t launch_mx_quant_rows(const MxQuantParams& p, hipStream_t s) {
+    if (p.rows <= 0) return hipSuccess;
+    if (p.K % 64 != 0 || p.srows < p.rows) return hipErrorInvalidValue;
+    const int64_t items = (int64_t)p.rows * (p.K / 64);
+    mx_quant_rows_kernel<<<(unsigned)((items + kThreads - 1) / kThreads), kThreads, 0, s>>>(p);
+    return hipGetLastError();
+}
+
+hipError_t launch_mx_gemm(bool quant_out, const MxGemmParams& p, hipStream_t s) {
+    if (p.slots <= 0) return hipSuccess;
+    if (p.K % 64 != 0 || p.N % 64 != 0 || p.N <= 0) return hipErrorInvalidValue;
+    const int64_t ntn = (p.N + BN - 1) / BN;
+    const int64_t gn = ntn < 8 ? ntn : 8, gm = 32 / gn;
+    const int64_t ngn = (ntn + gn - 1) / gn;
+    const int64_t mtiles = (int64_t)(p.slots + BM - 1) / BM + p.E;  // >= sum_e ceil(cnt_e / BM)
+    const int64_t groups = ((mtiles + gm - 1) / gm) * ngn;
+    const int64_t grid = (groups * 32 + 255) / 256 * 256;
+    if (grid > 0x7fffffff) return hipErrorInvalidValue;
+    if (quant_out) mx_gemm_kernel<true><<<(unsigned)grid, 256, 0, s>>>(p);
+    else mx_gemm_kernel<false><<<(unsigned)grid, 256, 0, s>>>(p);
+    return hipGetLastError();
+}
+
+}  // namespace tmt

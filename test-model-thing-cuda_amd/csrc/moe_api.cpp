@@ -109,6 +109,8 @@ struct tmt_moe {
     int32_t *idx, *blkcnt, *blkbase, *counts, *offsets, *order, *perm, *slot_of;
     // activations
     uint16_t *U, *Aact, *O, *dO, *dU, *dXg, *Xg;
+    // MX handles: activations of the two expert GEMMs as two MXFP6 terms
+    uint8_t *xq = nullptr, *xq_scales = nullptr, *aq = nullptr, *aq_scales = nullptr;
     float *dlogits, *dwr_partial;
     // LayerNorm in front of the block (tmt_moe_forward_ln / tmt_moe_backward_ln)
     uint16_t *H, *dH;
@@ -137,9 +139,18 @@ int validate_desc(const tmt_moe_desc* d) {
         return fail(TMT_MOE_EINVAL, "hidden=%d must be 0 or a multiple of 64", d->hidden);
     if ((int64_t)d->max_tokens * d->topk >= (1ll << 31))
         return fail(TMT_MOE_EINVAL, "max_tokens*topk must fit in int32");
-    if (d->weight_format != TMT_MOE_WEIGHTS_BF16 && d->weight_format != TMT_MOE_WEIGHTS_MXFP4)
+    if (d->weight_format != TMT_MOE_WEIGHTS_BF16 && d->weight_format != TMT_MOE_WEIGHTS_MXFP4 &&
+        d->weight_format != TMT_MOE_WEIGHTS_MXFP4_MX)
         return fail(TMT_MOE_EINVAL, "unknown weight_format %d", d->weight_format);
-    if (d->weight_format == TMT_MOE_WEIGHTS_MXFP4 && d->hidden == 0)
+    if (d->weight_format == TMT_MOE_WEIGHTS_MXFP4_MX) {
+        // the scaled-MFMA GEMMs address operands with 32-bit byte offsets
+        const int64_t TK = (int64_t)d->max_tokens * d->topk;
+        const int64_t widest = std::max<int64_t>(d->d, d->hidden);
+        if (TK * (widest / 32) * 48 >= (int64_t(1) << 31) || (int64_t)d->hidden * d->d / 2 >= (int64_t(1) << 31))
+            return fail(TMT_MOE_EINVAL, "max_tokens*topk=%lld is too large for MX activations at d=%d, hidden=%d",
+                        (long long)TK, d->d, d->hidden);
+    }
+    if (d->weight_format != TMT_MOE_WEIGHTS_BF16 && d->hidden == 0)
         return fail(TMT_MOE_EINVAL, "MXFP4 weights need hidden > 0");
     return TMT_MOE_OK;
 }
@@ -184,8 +195,10 @@ Sizes plan(const tmt_moe_desc* d, tmt_moe* m) {
     size_t o_stats = L.add((2 + E) * 4);
     size_t o_ticket = L.add(4);
     size_t o_perm = L.add(TK * 4), o_slot = L.add(TK * 4);
-    size_t o_U = L.add(TK * hn * 2);
-    size_t o_A = h > 0 ? L.add(TK * h * 2) : 0;
+    // MX handles (scaled-MFMA FP4 forward) keep activations in MX6x2 form instead of U / SiLU(U)
+    const bool mx = d->weight_format == TMT_MOE_WEIGHTS_MXFP4_MX;
+    size_t o_U = mx ? 0 : L.add(TK * hn * 2);
+    size_t o_A = h > 0 && !mx ? L.add(TK * h * 2) : 0;
     size_t o_O = h > 0 ? L.add(TK * D * 2) : 0;
     size_t o_H = L.add(T * D * 2), o_mean = L.add(T * 4), o_rstd = L.add(T * 4);
     // transient
@@ -207,6 +220,8 @@ Sizes plan(const tmt_moe_desc* d, tmt_moe* m) {
     // Decode GEMM_DOWN in K halves: [2][min(T, 64) * K][d] fp32.
     const bool dsplit = d->weight_format == TMT_MOE_WEIGHTS_BF16 && h > 0;
     size_t o_dpart = dsplit ? W.add((size_t)2 * std::min<int64_t>(T, kSkinnyMaxTokens) * K * D * 4) : 0;
+    size_t o_xq = mx ? W.add(mx_codes_bytes(TK, D)) : 0, o_xqs = mx ? W.add(mx_scales_bytes(TK, D)) : 0;
+    size_t o_aq = mx ? W.add(mx_codes_bytes(TK, h)) : 0, o_aqs = mx ? W.add(mx_scales_bytes(TK, h)) : 0;
     const int64_t ln_rows = std::max(scatter_blocks((int)T), ln_chunks((int)T));
     size_t o_lnp = bwd ? W.add((size_t)ln_rows * 2 * D * 4) : 0;
     size_t o_lnp2 = bwd ? W.add((size_t)colsum_groups((int)ln_rows) * 2 * D * 4) : 0;
@@ -231,8 +246,12 @@ Sizes plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->resident = resident;
         m->perm = (int32_t*)(a + o_perm);
         m->slot_of = (int32_t*)(a + o_slot);
-        m->U = (uint16_t*)(a + o_U);
-        m->Aact = h > 0 ? (uint16_t*)(a + o_A) : nullptr;
+        m->U = mx ? nullptr : (uint16_t*)(a + o_U);
+        m->Aact = h > 0 && !mx ? (uint16_t*)(a + o_A) : nullptr;
+        m->xq = mx ? (uint8_t*)(w + o_xq) : nullptr;
+        m->xq_scales = mx ? (uint8_t*)(w + o_xqs) : nullptr;
+        m->aq = mx ? (uint8_t*)(w + o_aq) : nullptr;
+        m->aq_scales = mx ? (uint8_t*)(w + o_aqs) : nullptr;
         m->O = h > 0 ? (uint16_t*)(a + o_O) : nullptr;
         m->dO = bwd ? (uint16_t*)(w + o_dO) : nullptr;
         m->dU = bwd ? (h > 0 ? (uint16_t*)(w + o_dU) : m->dO) : nullptr;  // h == 0: combine_bwd writes dU
@@ -730,7 +749,7 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
                           uint16_t* Y, float beta) {
     if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
     const tmt_moe_desc& ds = m->desc;
-    if (ds.weight_format != TMT_MOE_WEIGHTS_MXFP4)
+    if (ds.weight_format != TMT_MOE_WEIGHTS_MXFP4 && ds.weight_format != TMT_MOE_WEIGHTS_MXFP4_MX)
         return fail(TMT_MOE_EINVAL, "handle expects bf16 weights: use tmt_moe_forward");
     if (T < 0 || T > ds.max_tokens) return fail(TMT_MOE_EINVAL, "T=%d outside [0, %d]", T, ds.max_tokens);
     const int E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden;
@@ -747,7 +766,30 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
     m->last_T = -1;
     m->last_ln = false;
     if ((rc = route(m, s, T, X, Wr, logit_bias))) return rc;
-    if (T > 0) {
+    if (T > 0 && ds.weight_format == TMT_MOE_WEIGHTS_MXFP4_MX) {
+        const int TK = T * K;
+        const int64_t srows = (int64_t)ds.max_tokens * K + kMxScalePadRows;
+        MxQuantParams qp{};
+        qp.X = X; qp.ldx = d; qp.perm = E > 1 ? m->perm : nullptr; qp.rows = TK; qp.K = d;
+        qp.codes = m->xq; qp.scales = m->xq_scales; qp.srows = srows;
+        LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_quant_rows(qp, s));
+        MxGemmParams up{};
+        up.offsets = m->offsets; up.E = E; up.N = h; up.K = d; up.slots = TK;
+        up.a_codes = m->xq; up.a_scales = m->xq_scales; up.a_srows = srows;
+        for (int e = 0; e < E; ++e) { up.wq[e] = W_up[e]; up.wsc[e] = W_up_scale[e]; }
+        up.q_codes = m->aq; up.q_scales = m->aq_scales; up.q_srows = srows;
+        LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_gemm(true, up, s));
+        MxGemmParams dn{};
+        dn.offsets = m->offsets; dn.E = E; dn.N = d; dn.K = h; dn.slots = TK;
+        dn.a_codes = m->aq; dn.a_scales = m->aq_scales; dn.a_srows = srows;
+        for (int e = 0; e < E; ++e) { dn.wq[e] = W_down[e]; dn.wsc[e] = W_down_scale[e]; }
+        dn.c = m->O; dn.ldc = d;
+        LAUNCH(TMT_MOE_PH_GEMM_DOWN, launch_mx_gemm(false, dn, s));
+        CombineParams cp{};
+        cp.O = m->O; cp.slot_of = m->slot_of; cp.gate = m->gate;
+        cp.Y = Y; cp.beta = beta; cp.T = T; cp.d = d; cp.K = K; cp.silu = 0;
+        LAUNCH(TMT_MOE_PH_COMBINE, launch_combine(cp, s));
+    } else if (T > 0) {
         GemmParams up{};
         up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
         up.N = h; up.K = d; up.slots = T * K;

@@ -23,6 +23,7 @@ LIB_PATH = os.path.join(_HERE, "libtmt_moe.so")
 
 WEIGHTS_BF16 = 0
 WEIGHTS_MXFP4 = 1
+WEIGHTS_MXFP4_MX = 2
 
 EXPORTED = (
     "tmt_moe_create",

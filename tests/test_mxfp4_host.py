@@ -53,7 +53,9 @@ def test_activation_precision_choice():
     Quantising the bf16 activations to MXFP8 (e4m3) costs more than the
     2e-2 rel-L2 budget against the dequantised fp32 result, while bf16
     activations times exactly dequantised weights stay far inside it, so the
-    FP4 path expands weights to bf16 and runs bf16 MFMA."""
+    exact FP4 format expands weights to bf16 and runs bf16 MFMA; the MX
+    format instead splits each activation into two MXFP6 terms (pinned
+    below)."""
     rng = np.random.default_rng(0)
     T, d, h = 256, 512, 1024
     X = sy.bf16_to_f32(sy.bf16_bits(rng.standard_normal((T, d)).astype(np.float32)))
@@ -69,3 +71,80 @@ def test_activation_precision_choice():
     fp8_path = rel(_mxfp8(silu(_mxfp8(X) @ Wuq.T)) @ Wdq.T)
     assert bf16_path < 5e-3
     assert fp8_path > 2e-2
+
+
+# ---- activations as two MXFP6 (e2m3) terms: the WEIGHTS_MXFP4_MX format ----
+
+def _e2m3_grid():
+    """Non-negative e2m3 values: e = 0 subnormals m/8, else (1 + m/8) 2^(e-1)."""
+    return np.array([m / 8 if e == 0 else (1 + m / 8) * 2.0 ** (e - 1) for e in range(4) for m in range(8)])
+
+
+def _e2m3_round(y):
+    """Round to the nearest e2m3 value, ties to the even code, saturating at
+    7.5 (the rounding the gfx950 conversion performs on x / scale)."""
+    g = _e2m3_grid()
+    a = np.abs(y)
+    i = np.clip(np.searchsorted(g, a), 1, len(g) - 1)
+    lo, hi = g[i - 1], g[i]
+    up = (a - lo) > (hi - a)
+    tie = (a - lo) == (hi - a)
+    up = np.where(tie, i % 2 == 0, up)  # code of hi is i: even code wins
+    v = np.where(up, hi, lo)
+    v = np.where(a >= g[-1], g[-1], v)
+    return np.sign(y) * v
+
+
+def _mx6(x):
+    """One MXFP6 term per 32-block: scale 2^(floor(log2 max|x|) - 2)."""
+    b = x.reshape(-1, 32).astype(np.float64)
+    amax = np.abs(b).max(1)
+    e = np.where(amax > 0, np.floor(np.log2(np.where(amax > 0, amax, 1.0))) - 2, -127)
+    sc = 2.0 ** np.maximum(e, -127)
+    return (_e2m3_round(b / sc[:, None]) * sc[:, None]).reshape(x.shape)
+
+
+def _mx6x2(x):
+    t0 = _mx6(x)
+    return t0 + _mx6(x - t0)
+
+
+def test_e2m3_rounding_known_answers():
+    g = _e2m3_grid()
+    assert len(g) == 32 and g[-1] == 7.5 and g[1] == 0.125
+    # the grid itself is exact; midpoints go to the even code
+    assert np.array_equal(_e2m3_round(g), g)
+    assert _e2m3_round(np.array([0.0625]))[0] == 0.0      # between codes 0 and 1 -> 0
+    assert _e2m3_round(np.array([0.1875]))[0] == 0.25     # between codes 1 and 2 -> 2
+    assert _e2m3_round(np.array([2.125]))[0] == 2.0       # codes 16 (2.0) and 17 (2.25) -> 16
+    assert _e2m3_round(np.array([7.25]))[0] == 7.0        # codes 30 (7.0) and 31 (7.5) -> 30
+    assert _e2m3_round(np.array([7.3, 100.0, -9.0])).tolist() == [7.5, 7.5, -7.5]  # saturation
+    # the scale puts the block maximum in [4, 8), i.e. on the top binade
+    x = np.linspace(-3.3, 5.1, 32)
+    q = _mx6(x)
+    assert np.abs(q).max() == 5.0 and np.abs(q - x).max() <= 0.25  # half the top-binade step
+
+
+def test_two_term_mxfp6_activation_precision():
+    """The MX format rounds the block input and the SiLU output to two MXFP6
+    terms. On c5-like operands that costs ~4e-4 / 6e-4 relative L2 at the
+    up / down projection (one term: ~3e-2), far inside the 2e-2 budget."""
+    rng = np.random.default_rng(0)
+    T, d, h = 256, 1024, 2048
+    X = sy.bf16_to_f32(sy.bf16_bits(rng.standard_normal((T, d)).astype(np.float32))).astype(np.float64)
+    Wu = sy.mxfp4_dequantize(*sy.mxfp4_quantize((rng.standard_normal((h, d)) / math.sqrt(d)).astype(np.float32)))
+    Wd = sy.mxfp4_dequantize(*sy.mxfp4_quantize((rng.standard_normal((d, h)) / math.sqrt(h)).astype(np.float32)))
+    rel = lambda a, b: float(np.linalg.norm(a - b) / np.linalg.norm(b))
+    U = X @ Wu.T.astype(np.float64)
+    A = U / (1 + np.exp(-U))
+    up2, up1 = rel(_mx6x2(X) @ Wu.T, U), rel(_mx6(X) @ Wu.T, U)
+    dn2 = rel(_mx6x2(A) @ Wd.T, A @ Wd.T)
+    assert up2 < 1e-3 and dn2 < 1.5e-3
+    assert up1 > 1e-2  # one term alone is not enough
+    # a planted mistake -- the residual quantised at the first term's scale
+    # instead of its own -- loses most of the second term's benefit
+    t0 = _mx6(X)
+    b = (X - t0).reshape(-1, 32)
+    sc0 = np.repeat(2.0 ** (np.floor(np.log2(np.abs(X.reshape(-1, 32)).max(1))) - 2), 32).reshape(b.shape)
+    wrong = t0 + (_e2m3_round(b / sc0) * sc0).reshape(X.shape)
+    assert rel(wrong @ Wu.T, U) > 5 * up2
