@@ -314,56 +314,88 @@ def measured_traffic(phase):
     return value if digest == source_digest() else None
 
 
-def bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream, reps=100):
-    """c4: decode steps (forward, beta = 1) at T = 1, 8, 64 on the c3 weights;
-    µs per step from HIP events around `reps` back-to-back steps."""
+def bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream, reps=20, layers=8):
+    """c4: decode forwards (beta = 1) at T = 1, 8, 64 tokens on c3-shaped layers.
+
+    A step runs `layers` MoE layers, each with its own router and expert
+    weights (layer 0 the c3 weights, the others fresh draws of the same
+    distribution), so the experts stream from HBM as in a model: the experts
+    one layer touches (67 to 268 MB) would otherwise stay in the 256 MB
+    Infinity Cache across back-to-back calls of that one layer. µs per layer
+    from HIP events around `reps` steps: launched eagerly, and with each step
+    captured once as a HIP graph and replayed. The single-layer repeat of the
+    earlier measurement is kept beside it ("same_layer_us")."""
+    import math
+
     import numpy as np
     import torch
 
     import tmt_moe
 
-    out = {}
+    g = torch.Generator(device="cuda").manual_seed(11)
+    nets = [(Wr, Wu, Wd)]
+    for _ in range(layers - 1):
+        nets.append(((torch.randn(E, d, device="cuda", generator=g) / math.sqrt(d)).to(torch.bfloat16),
+                     (torch.randn(E, h, d, device="cuda", generator=g) / math.sqrt(d)).to(torch.bfloat16),
+                     (torch.randn(E, d, h, device="cuda", generator=g) / math.sqrt(h)).to(torch.bfloat16)))
+    out = {"layers": layers, "weights_per_layer_bytes": 2 * E * d * h * 2 + E * d * 2}
     md = tmt_moe.MoE(64, d, E, K, h)
-    for td in (1, 8, 64):
-        Xd = X[:td].contiguous()
-        Yd = torch.zeros(td, d, dtype=torch.bfloat16, device="cuda")
-        for _ in range(10):
-            md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def timed(fn, n):
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for _ in range(reps):
-            md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+        for _ in range(n):
+            fn()
         e1.record(stream)
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) / reps * 1000
-        # The same step captured once in a HIP graph and replayed: no host
-        # launch cost between steps (how a serving loop would run it).
+        return e0.elapsed_time(e1) * 1000.0 / n
+
+    for td in (1, 8, 64):
+        Xd = X[:td].contiguous()
+        Ys = [torch.zeros(td, d, dtype=torch.bfloat16, device="cuda") for _ in range(layers)]
+
+        def step():
+            for (wr, wu, wd), y in zip(nets, Ys):
+                md.forward(Xd, wr, wu, wd, y, beta=1.0)
+
+        # distinct experts per layer and the bytes they stream
+        distinct = []
+        for (wr, wu, wd), y in zip(nets, Ys):
+            md.forward(Xd, wr, wu, wd, y, beta=1.0)
+            distinct.append(int(np.unique(md.routing()["idx"]).size))
+        for _ in range(3):
+            step()
+        us_layer = timed(step, reps) / layers
+        # one step (all layers) captured as a HIP graph, replayed
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(stream)
         with torch.cuda.stream(side):
-            md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+            step()
         stream.wait_stream(side)
         torch.cuda.synchronize()
         with torch.cuda.graph(graph):
-            md.forward(Xd, Wr, Wu, Wd, Yd, beta=1.0)
+            step()
+        for _ in range(3):
+            graph.replay()
+        us_graph = timed(graph.replay, reps) / layers
+        # the earlier measurement: one layer called back to back
+        wr, wu, wd = nets[0]
+        one = lambda: md.forward(Xd, wr, wu, wd, Ys[0], beta=1.0)
         for _ in range(10):
-            graph.replay()
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(reps):
-            graph.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        us_graph = e0.elapsed_time(e1) / reps * 1000
-        routed = md.routing()
-        distinct = int(np.unique(routed["idx"]).size)
-        wbytes = distinct * 2 * d * h * 2 + E * d * 2
-        out[f"T{td}"] = {"us_per_step": round(us, 2), "us_per_step_graph": round(us_graph, 2),
-                         "distinct_experts": distinct, "weight_bytes": wbytes,
-                         "hbm_gbs": round(wbytes / (us * 1e-6) / 1e9, 1)}
+            one()
+        us_same = timed(one, 100)
+        wbytes = float(np.mean(distinct)) * 2 * d * h * 2 + E * d * 2
+        out[f"T{td}"] = {"us_per_layer": round(us_layer, 2), "us_per_layer_graph": round(us_graph, 2),
+                         "same_layer_us": round(us_same, 2),
+                         "distinct_experts_mean": round(float(np.mean(distinct)), 2),
+                         "weight_bytes_mean": int(wbytes),
+                         "hbm_gbs": round(wbytes / (us_layer * 1e-6) / 1e9, 1)}
+        del graph
     md.close()
+    del nets
+    torch.cuda.empty_cache()
     return out
 
 

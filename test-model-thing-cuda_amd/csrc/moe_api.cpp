@@ -324,7 +324,10 @@ int prof_end(tmt_moe* m, int slot, hipStream_t s) {
     } while (0)
 
 // Routing + dispatch: router / scan / permute (E > 1) or identity (E == 1).
-int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* Wr, const float* bias) {
+// picks_only (decode batches whose GEMM_UP runs with self_dispatch): the
+// router writes the picks and the GEMM_UP completes the dispatch.
+int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* Wr, const float* bias,
+          bool picks_only = false) {
     const int E = m->desc.experts, K = m->desc.topk, d = m->desc.d;
     if (E == 1) {
         LAUNCH(TMT_MOE_PH_PERMUTE, launch_dense_dispatch(T, m->perm, m->slot_of, m->gate, m->counts,
@@ -343,7 +346,7 @@ int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* W
         PermuteParams pp{};
         pp.T = T; pp.E = E; pp.K = K; pp.rows_per_block = T;
         pp.perm = m->perm; pp.slot_of = m->slot_of;
-        LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(rp, sp, pp, m->ticket, s));
+        LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(rp, sp, pp, picks_only ? nullptr : m->ticket, s));
         return TMT_MOE_OK;
     }
     const int rpb = router_rows_per_block(T, E, K);
@@ -408,7 +411,14 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
     int rc;
     m->last_T = -1;
 
-    if ((rc = route(m, s, T, X, Wr, logit_bias))) return rc;
+    // Decode-sized batches stream the weights with the skinny kernels. Where
+    // every expert GEMM runs on the stream variant, the router writes only
+    // the picks and each later kernel finds its rows from the pick table
+    // (no cross-block handoff inside the router); the combine's extra
+    // workgroup writes the dispatch tables.
+    const bool skinny = T <= kSkinnyMaxTokens;
+    const bool self = skinny && skinny_self_dispatch(T, E, K, d, h, hn);
+    if ((rc = route(m, s, T, X, Wr, logit_bias, self))) return rc;
     if (T > 0) {
         GemmParams up{};
         up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
@@ -417,8 +427,7 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
         up.a = X; up.lda = d; up.c = m->U; up.ldc = hn; up.c2 = m->Aact;
         for (int e = 0; e < E; ++e) up.w[e] = W_up[e];
         up.ldb = d;
-        // Decode-sized batches stream the weights with the skinny kernel.
-        const bool skinny = T <= kSkinnyMaxTokens;
+        up.self_dispatch = self ? 1 : 0;
         bool halves = false;  // decode GEMM_DOWN wrote fp32 K halves instead of O
         LAUNCH(TMT_MOE_PH_GEMM_UP, skinny ? launch_skinny_gemm(GEMM_UP, h > 0, up, T, s)
                                           : launch_gemm(GEMM_UP, h > 0, up, s));
@@ -431,6 +440,10 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
             dn.ldb = h;
             dn.part = m->split; dn.resident = m->resident;
             dn.dpart = skinny ? m->dpart : nullptr;
+            if (self) {
+                dn.self_dispatch = 1;
+                dn.idx = m->idx; dn.topk = K;
+            }
             LAUNCH(TMT_MOE_PH_GEMM_DOWN, skinny ? launch_skinny_gemm(GEMM_DOWN, false, dn, T, s, &halves)
                                                 : launch_gemm(GEMM_DOWN, false, dn, s));
         }
@@ -439,6 +452,13 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
         cp.Y = Y; cp.beta = beta; cp.T = T; cp.d = d; cp.K = K; cp.silu = h == 0;
         if (halves) {  // the decode GEMM_DOWN left two fp32 K halves; O is formed here
             cp.part = m->dpart; cp.O_out = m->O; cp.slots = T * K;
+        }
+        if (self) {
+            cp.self_dispatch = 1; cp.idx = m->idx;
+            DispatchTables& dt = cp.tables;
+            dt.T = T; dt.E = E; dt.K = K; dt.probs = m->probs; dt.lse = m->lse;
+            dt.offsets = m->offsets; dt.counts = m->counts; dt.order = m->order;
+            dt.perm = m->perm; dt.slot_of = m->slot_of; dt.stats = m->stats;
         }
         LAUNCH(TMT_MOE_PH_COMBINE, launch_combine(cp, s));
     }

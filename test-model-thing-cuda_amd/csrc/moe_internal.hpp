@@ -67,7 +67,9 @@ hipError_t launch_permute(const PermuteParams& p, int nblk, hipStream_t s);
 // per token row; with several rows the last block to finish (atomic
 // *ticket, zero between calls and re-armed by that block) completes the
 // dispatch. Uses sp.counts/offsets/order/stats and pp.perm/slot_of; no
-// block tables.
+// block tables. With ticket == nullptr and T > 1 the blocks only write their
+// rows' picks (idx, gate, logits, probs, lse): the decode GEMM_UP completes
+// the dispatch (GemmParams::self_dispatch).
 constexpr int kSmallRouteTokens = 64;
 hipError_t launch_route_small(const RouterParams& p, const ScanParams& sp, const PermuteParams& pp,
                               int* ticket, hipStream_t s);
@@ -117,6 +119,10 @@ struct GemmParams {
     // Decode GEMM_DOWN (skinny kernels): [2][slots][N] fp32 buffer for a
     // split of K into two halves (nullptr: no split).
     float* dpart;
+    // Decode batches with self_dispatch (skinny stream kernels): the router
+    // wrote only the picks; workgroup (e, s) takes expert e's rows straight
+    // from the [T][topk] pick table in idx (the grid is indexed by expert).
+    int self_dispatch;
 };
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s);
 // Rows of an activation-GEMM tile, and the fp32 partial buffer the split-K
@@ -135,6 +141,10 @@ constexpr int kSkinnyMaxTokens = 64;
 // p.c, and the combine adds them (CombineParams::part).
 hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s,
                               bool* halves = nullptr);
+// Whether a decode forward of these shapes runs every expert GEMM on the
+// skinny stream kernel (the kernel that supports self_dispatch): GEMM_UP
+// with hn output columns and, with h > 0, GEMM_DOWN (K = h, N = d).
+bool skinny_self_dispatch(int T, int E, int K, int d, int h, int hn);
 
 // ------------------------------------------------------------- gemm_mx ----
 // MXFP4 weights times activations held as two MXFP6 terms, on the scaled
@@ -174,6 +184,21 @@ struct MxGemmParams {
 hipError_t launch_mx_gemm(bool quant_out, const MxGemmParams& p, hipStream_t s);
 
 // ------------------------------------------------------------- pointwise --
+// Dispatch tables of a decode batch written from the pick table on the GPU
+// (dispatch.hpp): the outputs of the router's dispatch, and the router
+// outputs the aux / z statistics are summed from.
+struct DispatchTables {
+    int T, E, K;
+    const float* probs;  // [T][E]
+    const float* lse;    // [T]
+    int32_t* offsets;    // [E+1]
+    int32_t* counts;     // [E]
+    int32_t* order;      // [E] experts by descending count (ties: lower index first)
+    int32_t* perm;       // [T*K] slot -> token
+    int32_t* slot_of;    // [T][K]
+    float* stats;        // aux, z, then the counts as int32
+};
+
 struct CombineParams {
     const uint16_t* O;       // [TK][d] expert outputs (hidden > 0) or U (hidden == 0)
     const int32_t* slot_of;  // [T][K]
@@ -188,6 +213,12 @@ struct CombineParams {
     const float* part;       // [2][slots][d]
     uint16_t* O_out;         // [slots][d]
     int slots;
+    // Decode batches with self_dispatch (T <= kSkinnyMaxTokens): each row
+    // finds its picks' slots from the [T][K] pick table in idx instead of
+    // slot_of, and one extra workgroup writes the dispatch tables.
+    int self_dispatch;
+    const int32_t* idx;
+    DispatchTables tables;
 };
 hipError_t launch_combine(const CombineParams& p, hipStream_t s);
 

@@ -15,10 +15,47 @@
 #include <algorithm>
 
 #include "device_util.hpp"
+#include "dispatch.hpp"
 #include "moe_internal.hpp"
 
 namespace tmt {
 namespace {
+
+// self_dispatch: the grid's extra (last) workgroup writes the dispatch
+// tables from the pick table; true for that workgroup.
+__device__ __forceinline__ bool combine_tables_block(const CombineParams& p, int lane) {
+    if ((int)blockIdx.x != (int)gridDim.x - 1) return false;
+    if (threadIdx.x < 64) {
+        int ent[kPickGroups];
+        load_pick_table(p.idx, p.T * p.K, lane, ent);
+        write_dispatch(p.tables, ent, lane);
+    }
+    return true;
+}
+
+// Slots and gates of row r's K picks: from slot_of, or (self_dispatch) from
+// the pick table.
+template <int K>
+__device__ __forceinline__ void row_picks(const CombineParams& p, int r, int lane, int64_t (&pos)[K], float (&g)[K]) {
+    if (p.self_dispatch) {
+        int ent[kPickGroups];
+        load_pick_table(p.idx, p.T * K, lane, ent);
+        int e[K];
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            e[j] = p.idx[(int64_t)r * K + j];
+            g[j] = p.gate[(int64_t)r * K + j];
+        }
+#pragma unroll
+        for (int j = 0; j < K; ++j) pos[j] = pick_slot(ent, p.T * K, e[j], r * K + j, lane);
+    } else {
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            pos[j] = p.slot_of[(int64_t)r * K + j];
+            g[j] = p.gate[(int64_t)r * K + j];
+        }
+    }
+}
 
 // K is a template argument so that every load of a pass is issued
 // unconditionally, in one batch: with a runtime K the compiler places the
@@ -26,16 +63,13 @@ namespace {
 template <bool SILU, int K>
 __global__ __launch_bounds__(kThreads) void combine_kernel(CombineParams p) {
     const int lane = threadIdx.x & 63;
+    if (p.self_dispatch && combine_tables_block(p, lane)) return;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= p.T) return;
     const int d = p.d;
-    int pos[K];
+    int64_t pos[K];
     float g[K];
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-        pos[j] = p.slot_of[(int64_t)r * K + j];
-        g[j] = p.gate[(int64_t)r * K + j];
-    }
+    row_picks<K>(p, r, lane, pos, g);
     const bool resid = p.beta != 0.0f;
     // Two 512-column chunks per pass with all their loads in flight together
     // (a decode row waits for one round trip after the slot table, not one
@@ -81,17 +115,14 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(CombineParams p) {
 template <int K>
 __global__ __launch_bounds__(kThreads) void combine_part_kernel(CombineParams p) {
     const int lane = threadIdx.x & 63;
+    if (p.self_dispatch && combine_tables_block(p, lane)) return;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= p.T) return;
     const int d = p.d;
     const int64_t half = (int64_t)p.slots * d;
     int64_t pos[K];
     float g[K];
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-        pos[j] = p.slot_of[(int64_t)r * K + j];
-        g[j] = p.gate[(int64_t)r * K + j];
-    }
+    row_picks<K>(p, r, lane, pos, g);
     const bool resid = p.beta != 0.0f;
     for (int c0 = lane * 8; c0 < d; c0 += 512) {
         const uint4 yv = resid ? *reinterpret_cast<const uint4*>(p.Y + (int64_t)r * d + c0) : make_uint4(0, 0, 0, 0);
@@ -536,7 +567,8 @@ __global__ __launch_bounds__(kThreads) void scatter_kernel(ScatterParams p, int 
 
 hipError_t launch_combine(const CombineParams& p, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
-    const int grid = (p.T + 3) / 4;
+    if (p.self_dispatch && (p.T > kSkinnyMaxTokens || p.idx == nullptr)) return hipErrorInvalidValue;
+    const int grid = (p.T + 3) / 4 + (p.self_dispatch ? 1 : 0);
     if (p.part != nullptr) {
         if (p.silu || p.O_out == nullptr || p.slots != p.T * p.K) return hipErrorInvalidValue;
         switch (p.K) {

@@ -669,7 +669,7 @@ __global__ __launch_bounds__(kThreads) void route_small_kernel(RouterParams p, S
             if (e == 0) p.lse[row] = pk.lse;
         }
     }
-    if (single) return;
+    if (single || ticket == nullptr) return;
 
     // 3. the last block finishes the dispatch (every row read back in one batch)
     __threadfence();

@@ -29,6 +29,7 @@
 // expert's rows itself instead of reading the permutation (a second round
 // trip before the activation loads).
 #include "device_util.hpp"
+#include "dispatch.hpp"
 #include "moe_internal.hpp"
 
 namespace tmt {
@@ -89,15 +90,9 @@ __device__ __forceinline__ SkinnyExpert skinny_expert(const GemmParams& p, int r
     return x;
 }
 
-// UP: entries q * 64 + lane of the [T][K] pick table (-1 past T*K, or
-// without a table: E == 1, where slot == token).
-constexpr int kPickGroups = kSkinnyMaxTokens * kMaxTopK / 64;
+// The [T][K] pick table (dispatch.hpp), entries q * 64 + lane.
 __device__ __forceinline__ void load_picks(const GemmParams& p, int lane, int (&ent)[kPickGroups]) {
-#pragma unroll
-    for (int q = 0; q < kPickGroups; ++q) {
-        const int i = q * 64 + lane;
-        ent[q] = (p.idx != nullptr && i < p.slots) ? p.idx[i] : -1;
-    }
+    load_pick_table(p.idx, p.slots, lane, ent);
 }
 
 // tok[m] = token of row m of expert e, for the first 16 * RB rows. The
@@ -121,6 +116,15 @@ __device__ __forceinline__ void expert_tokens(const int (&ent)[kPickGroups], int
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// self_dispatch: expert e's first slot and row count from the pick table.
+__device__ __forceinline__ SkinnyExpert self_expert(const GemmParams& p, int e, const int (&ent)[kPickGroups]) {
+    SkinnyExpert x;
+    x.e = e;
+    expert_span(ent, p.slots, e, x.row0, x.rows);
+    x.w = p.w[e];
+    return x;
 }
 
 template <int KIND, bool DUAL, int RB>
@@ -344,14 +348,28 @@ __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int ne
 // two halves over twice the workgroups, (rank, s, half), so that 8 waves hold
 // the rows of one half; each half's sums (wave order) are stored as fp32 rows
 // of p.dpart and the combine adds the halves.
+//
+// Outputs are staged in LDS and written after the last tile. A global store
+// inside the loop would be counted on the same in-order vector-memory counter
+// as the weight loads issued before it, and the next register set's loads
+// reuse the store's registers, so each tile boundary would wait for every
+// outstanding load -- the prefetched tile included.
+template <int KIND, bool DUAL, int RB, int KS>
+__host__ __device__ constexpr int stream_stage_bytes() {  // staged outputs of one visited tile
+    return 16 * RB * 16 * (KS == 2 ? 4 : 2) * (DUAL ? 2 : 1);
+}
 template <int KIND, bool DUAL, int RB, int NWMAX, int KS = 1>
 __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p, int nexp, int split) {
     static_assert(KIND == GEMM_UP || KIND == GEMM_DOWN, "forward GEMMs only");
     static_assert(KS == 1 || (KS == 2 && KIND == GEMM_DOWN && !DUAL), "K halves: GEMM_DOWN only");
     constexpr bool kGather = KIND == GEMM_UP;
     constexpr int J = 8;
-    extern __shared__ f32x4 red[];  // [RB][nw][64] wave partials
+    // [RB][nw][64] wave partials, then the staged outputs of each visited
+    // tile: [16 RB rows][16 columns] fp32 (KS == 2) or bf16 C, then bf16
+    // SiLU(C) when DUAL
+    extern __shared__ f32x4 red[];
     __shared__ int s_tok[NWMAX][16 * RB];
+    constexpr int TSB = stream_stage_bytes<KIND, DUAL, RB, KS>();
 
     const int nw = (int)blockDim.x >> 6;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -359,9 +377,10 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
     const int rank = (int)blockIdx.x % nexp, sq = (int)blockIdx.x / nexp;
     const int s0 = KS == 1 ? sq : sq % split, half = KS == 1 ? 0 : sq / split;
     args_in_sgprs(p.order, p.offsets, p.idx, p.a, p.c, p.c2, p.E, p.N, p.slots, p.topk, p.lda, p.ldb, p.ldc);
+    const bool self = p.self_dispatch != 0;
     int ent[kPickGroups];
-    if constexpr (kGather) load_picks(p, lane, ent);
-    const SkinnyExpert x = skinny_expert(p, rank, lane);
+    if (kGather || self) load_picks(p, lane, ent);
+    const SkinnyExpert x = self ? self_expert(p, rank, ent) : skinny_expert(p, rank, lane);
     const int row0 = x.row0;
     const int rows = min(x.rows, 16 * RB);
     const int ntile = p.N >> 4;
@@ -370,15 +389,25 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
     const int g = lane >> 4, li = lane & 15;
     const int kw = half * nw * (32 * J) + wave * (32 * J) + g * 8;
 
-    // The expert's weights [N][K] as one buffer (below 2 GiB: checked by the host).
+    // The expert's weights [N][K] as one buffer (below 2 GiB: checked by the
+    // host). The tile offset is a wave-uniform scalar offset and the lane
+    // offsets are loop-invariant registers: an address register recomputed
+    // per tile would be a write after the previous set's loads, and the
+    // compiler waits for every outstanding load (the prefetched tile
+    // included) before it. Past the last tile the loads go through an empty
+    // resource (no records), which returns zeros without touching memory.
     const int wbytes = p.N * (int)p.ldb * 2;
     const __amdgpu_buffer_rsrc_t wr = weight_rsrc(x.w, wbytes);
+    const __amdgpu_buffer_rsrc_t wr_none = weight_rsrc(x.w, 0);
     const int lane_off = (li * (int)p.ldb + kw) * 2;
     const int tile_bytes = 16 * (int)p.ldb * 2;
     auto wload = [&](int tile, uint4 (&w)[J]) {
-        const int off = tile < ntile ? tile * tile_bytes + lane_off : wbytes;
+        const bool in = tile < ntile;  // uniform
+        const int soff = (in ? tile : ntile - 1) * tile_bytes;
 #pragma unroll
-        for (int i = 0; i < J; ++i) w[i] = ld16_buf(wr, off + 64 * i);
+        for (int i = 0; i < J; ++i)
+            w[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(in ? wr : wr_none,
+                                                                                   lane_off + 64 * i, soff, 0));
     };
     uint4 w0[J], w1[J];
     wload(s0, w0);
@@ -401,7 +430,7 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
         }
     }
 
-    uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
+    uint8_t* stage = reinterpret_cast<uint8_t*>(red + RB * nw * 64);
     auto step = [&](int tile, const uint4 (&w)[J]) {
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
@@ -412,6 +441,7 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
             red[(rb * nw + wave) * 64 + lane] = acc;
         }
         __syncthreads();
+        uint8_t* st = stage + ((tile - s0) / split) * TSB;
         for (int o = tid; o < nrb * 256; o += (int)blockDim.x) {
             const int rb = o >> 8, m = (o >> 4) & 15, n = o & 15;
             const int row = rb * 16 + m;
@@ -420,11 +450,10 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
             float v = red[(rb * nw) * 64 + sl][r];
             for (int w2 = 1; w2 < nw; ++w2) v += red[(rb * nw + w2) * 64 + sl][r];
             if constexpr (KS == 2) {
-                p.dpart[((int64_t)half * p.slots + row0 + row) * p.N + tile * 16 + n] = v;
+                reinterpret_cast<float*>(st)[row * 16 + n] = v;
             } else {
-                const int64_t off = (int64_t)(row0 + row) * p.ldc + tile * 16 + n;
-                C[off] = f2bf(v);
-                if constexpr (DUAL) p.c2[off] = f2bf(silu_fast(v));
+                reinterpret_cast<uint16_t*>(st)[row * 16 + n] = f2bf(v);
+                if constexpr (DUAL) reinterpret_cast<uint16_t*>(st)[16 * RB * 16 + row * 16 + n] = f2bf(silu_fast(v));
             }
         }
         __syncthreads();
@@ -439,6 +468,27 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
         wload(tile + 2 * split, w0);
         __builtin_amdgcn_sched_barrier(0);
         step(tile + split, w1);
+    }
+
+    // Staged outputs to global memory, 16 bytes per store: a row of one tile
+    // is 32 bytes of bf16 (two stores per plane) or 64 bytes of fp32 (four).
+    constexpr int CPR = KS == 2 ? 4 : 2;  // 16-byte chunks per staged row
+    constexpr int NPL = DUAL ? 2 : 1;     // output planes
+    const int visited = (ntile - s0 + split - 1) / split;
+    const int per_tile = rows * CPR * NPL;
+    for (int o = tid; o < visited * per_tile; o += (int)blockDim.x) {
+        const int j = o / per_tile, rem = o % per_tile;
+        const int pl = rem / (rows * CPR), rc = rem % (rows * CPR);
+        const int row = rc / CPR, c = rc % CPR;
+        const int tile = s0 + j * split;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + j * TSB + pl * (16 * RB * 16 * 2) +
+                                                        (row * CPR + c) * 16);
+        if constexpr (KS == 2) {
+            *reinterpret_cast<uint4*>(p.dpart + ((int64_t)half * p.slots + row0 + row) * p.N + tile * 16 + c * 4) = v;
+        } else {
+            uint16_t* dst = pl == 0 ? reinterpret_cast<uint16_t*>(p.c) : p.c2;
+            *reinterpret_cast<uint4*>(dst + (int64_t)(row0 + row) * p.ldc + tile * 16 + c * 8) = v;
+        }
     }
 }
 
@@ -475,14 +525,26 @@ hipError_t launch_chunk(int J, int ct, int rb, int nw, const GemmParams& p, int 
                   : launch_chunk_rb<KIND, DUAL, 2, 1>(rb, nw, p, nexp, s);
 }
 
+// Dynamic LDS of a stream-kernel workgroup: the wave partials and the staged
+// outputs of every tile it visits (at most ceil(ntile / split)).
+template <int KIND, bool DUAL, int RB, int KS>
+size_t stream_lds(int nw, int ntile, int split) {
+    return (size_t)RB * nw * 64 * sizeof(f32x4) +
+           (size_t)((ntile + split - 1) / split) * stream_stage_bytes<KIND, DUAL, RB, KS>();
+}
+// Largest dynamic LDS the stream kernels take (beyond it the chunk kernel runs).
+constexpr size_t kStreamMaxLds = 64 * 1024;
+
 // GEMM_DOWN with K in two halves of 8 waves (rows of up to 64 tokens).
 hipError_t launch_stream_halves(int rb, const GemmParams& p, int nexp, int split, hipStream_t s) {
     const unsigned grid = 2u * (unsigned)split * (unsigned)nexp;
     const dim3 block(64 * 8);
-    const size_t lds = (size_t)rb * 8 * 64 * sizeof(f32x4);
+    const int ntile = p.N / 16;
     switch (rb) {
-        case 2: skinny_stream_kernel<GEMM_DOWN, false, 2, 8, 2><<<grid, block, lds, s>>>(p, nexp, split); break;
-        case 4: skinny_stream_kernel<GEMM_DOWN, false, 4, 8, 2><<<grid, block, lds, s>>>(p, nexp, split); break;
+        case 2: skinny_stream_kernel<GEMM_DOWN, false, 2, 8, 2>
+                    <<<grid, block, stream_lds<GEMM_DOWN, false, 2, 2>(8, ntile, split), s>>>(p, nexp, split); break;
+        case 4: skinny_stream_kernel<GEMM_DOWN, false, 4, 8, 2>
+                    <<<grid, block, stream_lds<GEMM_DOWN, false, 4, 2>(8, ntile, split), s>>>(p, nexp, split); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -492,19 +554,33 @@ template <int KIND, bool DUAL>
 hipError_t launch_stream(int rb, int nw, const GemmParams& p, int nexp, int split, hipStream_t s) {
     const unsigned grid = (unsigned)split * (unsigned)nexp;
     const dim3 block(64 * nw);
-    const size_t lds = (size_t)rb * nw * 64 * sizeof(f32x4);
+    const int ntile = p.N / 16;
     if (nw > 8) {
         if (rb != 1) return hipErrorInvalidValue;
-        skinny_stream_kernel<KIND, DUAL, 1, 16><<<grid, block, lds, s>>>(p, nexp, split);
+        skinny_stream_kernel<KIND, DUAL, 1, 16>
+            <<<grid, block, stream_lds<KIND, DUAL, 1, 1>(nw, ntile, split), s>>>(p, nexp, split);
         return hipGetLastError();
     }
     switch (rb) {
-        case 1: skinny_stream_kernel<KIND, DUAL, 1, 8><<<grid, block, lds, s>>>(p, nexp, split); break;
-        case 2: skinny_stream_kernel<KIND, DUAL, 2, 8><<<grid, block, lds, s>>>(p, nexp, split); break;
-        case 4: skinny_stream_kernel<KIND, DUAL, 4, 8><<<grid, block, lds, s>>>(p, nexp, split); break;
+        case 1: skinny_stream_kernel<KIND, DUAL, 1, 8>
+                    <<<grid, block, stream_lds<KIND, DUAL, 1, 1>(nw, ntile, split), s>>>(p, nexp, split); break;
+        case 2: skinny_stream_kernel<KIND, DUAL, 2, 8>
+                    <<<grid, block, stream_lds<KIND, DUAL, 2, 1>(nw, ntile, split), s>>>(p, nexp, split); break;
+        case 4: skinny_stream_kernel<KIND, DUAL, 4, 8>
+                    <<<grid, block, stream_lds<KIND, DUAL, 4, 1>(nw, ntile, split), s>>>(p, nexp, split); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+// Whether launch_stream's workgroups fit kStreamMaxLds.
+size_t stream_lds_rt(bool halves, bool dual, int rb, int nw, int ntile, int split) {
+    if (halves) return rb == 2 ? stream_lds<GEMM_DOWN, false, 2, 2>(nw, ntile, split)
+                               : stream_lds<GEMM_DOWN, false, 4, 2>(nw, ntile, split);
+    switch (rb) {
+        case 1: return dual ? stream_lds<GEMM_UP, true, 1, 1>(nw, ntile, split) : stream_lds<GEMM_UP, false, 1, 1>(nw, ntile, split);
+        case 2: return dual ? stream_lds<GEMM_UP, true, 2, 1>(nw, ntile, split) : stream_lds<GEMM_UP, false, 2, 1>(nw, ntile, split);
+        default: return dual ? stream_lds<GEMM_UP, true, 4, 1>(nw, ntile, split) : stream_lds<GEMM_UP, false, 4, 1>(nw, ntile, split);
+    }
 }
 
 
@@ -523,46 +599,91 @@ int cu_count() {
     return cached[dev];
 }
 
+namespace {
+
+// Launch shape of the skinny kernels for a reduction length K.
+struct SkinnyShape {
+    int J = 0, nw = 0;  // MFMAs per wave chunk (8 or 2, 0: neither) and waves
+    int rb = 1;         // 16-row blocks held per workgroup
+};
+SkinnyShape skinny_shape(int K, int T) {
+    SkinnyShape sh;
+    // One K-chunk per wave, at most 16 waves.
+    if (K % 256 == 0 && K / 256 >= 4 && K / 256 <= 16) {
+        sh.J = 8;
+        sh.nw = K / 256;
+    } else if (K / 64 <= 16) {
+        sh.J = 2;
+        sh.nw = K / 64;
+    }
+    sh.rb = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
+    return sh;
+}
+// Workgroups per expert of the stream kernel, or 0 where it does not apply:
+// persistent workgroups where the activation chunks fit in registers next to
+// two weight sets (up to 8 waves for any row count, 16 waves for one row
+// block) and the staged outputs fit kStreamMaxLds.
+int stream_split(const SkinnyShape& sh, int T, int N, int64_t ldb, int nexp, bool dual) {
+    if (sh.J != 8 || T < kSkinnyStreamTokens || !(sh.nw <= 8 || sh.rb == 1) || (int64_t)N * ldb * 2 >= (1ll << 31))
+        return 0;
+    const int ntile = N / 16;
+    const int per_cu = sh.nw > 8 ? 1 : (sh.rb == 4 ? 2 : (sh.rb == 2 ? 3 : 4)) * 4 / sh.nw;
+    int split = (cu_count() * (per_cu > 0 ? per_cu : 1) + nexp - 1) / nexp;
+    split = split < 1 ? 1 : (split > ntile ? ntile : split);
+    return stream_lds_rt(false, dual, sh.rb, sh.nw, ntile, split) <= kStreamMaxLds ? split : 0;
+}
+// Workgroups per expert and K half of GEMM_DOWN over 16 waves with more than
+// one row block (two K halves of 8 waves each keep the rows resident, one
+// 8-wave workgroup per CU), or 0 where it does not apply.
+int halves_split(const SkinnyShape& sh, int T, int N, int64_t ldb, int nexp) {
+    if (sh.J != 8 || sh.nw != 16 || sh.rb <= 1 || T < kSkinnyStreamTokens || (int64_t)N * ldb * 2 >= (1ll << 31))
+        return 0;
+    const int ntile = N / 16;
+    int split = (cu_count() + 2 * nexp - 1) / (2 * nexp);
+    split = split < 1 ? 1 : (split > ntile ? ntile : split);
+    return stream_lds_rt(true, false, sh.rb, 8, ntile, split) <= kStreamMaxLds ? split : 0;
+}
+
+}  // namespace
+
+bool skinny_self_dispatch(int T, int E, int K, int d, int h, int hn) {
+    (void)K;
+    if (E <= 1 || T <= 1 || T > kSkinnyMaxTokens || hn % 16 != 0 || d % 64 != 0 || h % 64 != 0) return false;
+    if (stream_split(skinny_shape(d, T), T, hn, d, E, h > 0) == 0) return false;
+    if (h == 0) return true;
+    // GEMM_DOWN: the stream kernel, or its K halves
+    const SkinnyShape sh = skinny_shape(h, T);
+    if (stream_split(sh, T, d, h, E, false) > 0) return true;
+    return halves_split(sh, T, d, h, E) > 0;
+}
+
 hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s,
                               bool* halves) {
     if (halves != nullptr) *halves = false;
     if (T <= 0) return hipSuccess;
     if (T > kSkinnyMaxTokens || p.N % 16 != 0 || p.K % 64 != 0 || p.N <= 0) return hipErrorInvalidValue;
     if (kind != GEMM_UP && kind != GEMM_DOWN) return hipErrorInvalidValue;
-    const int nexp = min(p.E, p.slots);
-    // One K-chunk per wave, at most 16 waves.
-    int J = 0, nw = 0;
-    if (p.K % 256 == 0 && p.K / 256 >= 4 && p.K / 256 <= 16) {
-        J = 8;
-        nw = p.K / 256;
-    } else if (p.K / 64 <= 16) {
-        J = 2;
-        nw = p.K / 64;
-    }
-    const int rb = T <= 16 ? 1 : (T <= 32 ? 2 : 4);
-    // Persistent workgroups where the activation chunks fit in registers next
-    // to two weight sets: up to 8 waves for any row count, 16 waves for one
-    // row block.
-    if (J == 8 && T >= kSkinnyStreamTokens && (nw <= 8 || rb == 1) && (int64_t)p.N * p.ldb * 2 < (1ll << 31)) {
-        const int ntile = p.N / 16;
-        const int per_cu = nw > 8 ? 1 : (rb == 4 ? 2 : (rb == 2 ? 3 : 4)) * 4 / nw;
-        int split = (cu_count() * (per_cu > 0 ? per_cu : 1) + nexp - 1) / nexp;
-        split = split < 1 ? 1 : (split > ntile ? ntile : split);
+    const bool self = p.self_dispatch != 0;
+    // Ranks of the grid: experts in processing order, at most one per pick;
+    // self_dispatch indexes the grid by expert (empty experts exit at once).
+    const int nexp = self ? p.E : min(p.E, p.slots);
+    const SkinnyShape sh = skinny_shape(p.K, T);
+    const int J = sh.J, nw = sh.nw, rb = sh.rb;
+    const int split = stream_split(sh, T, p.N, p.ldb, nexp, kind == GEMM_UP && dual);
+    if (split > 0) {
         if (kind == GEMM_UP)
             return dual ? launch_stream<GEMM_UP, true>(rb, nw, p, nexp, split, s)
                         : launch_stream<GEMM_UP, false>(rb, nw, p, nexp, split, s);
         return launch_stream<GEMM_DOWN, false>(rb, nw, p, nexp, split, s);
     }
-    // GEMM_DOWN over 16 waves with more than one row block: two K halves of
-    // 8 waves each keep the rows resident (one 8-wave workgroup per CU).
-    if (kind == GEMM_DOWN && J == 8 && nw == 16 && rb > 1 && T >= kSkinnyStreamTokens && p.dpart != nullptr &&
-        halves != nullptr && (int64_t)p.N * p.ldb * 2 < (1ll << 31)) {
-        const int ntile = p.N / 16;
-        int split = (cu_count() + 2 * nexp - 1) / (2 * nexp);
-        split = split < 1 ? 1 : (split > ntile ? ntile : split);
-        *halves = true;
-        return launch_stream_halves(rb, p, nexp, split, s);
+    if (kind == GEMM_DOWN && p.dpart != nullptr && halves != nullptr) {
+        const int hs = halves_split(sh, T, p.N, p.ldb, nexp);
+        if (hs > 0) {
+            *halves = true;
+            return launch_stream_halves(rb, p, nexp, hs, s);
+        }
     }
+    if (self) return hipErrorInvalidValue;  // the host checked skinny_self_dispatch
     if (J > 0) {
         const int ct = (T >= kSkinnyTwoTileTokens && p.N % 32 == 0) ? 2 : 1;
         if (kind == GEMM_UP)

@@ -177,6 +177,36 @@ def test_shapes_against_oracle(orc, T, d, E, K, h):
     check_grads(g, r, h, E)
 
 
+@pytest.mark.parametrize("T,d,E,K,h", [
+    (4, 1024, 16, 1, 256),     # fewer picks than experts: most of the expert-indexed grid is empty
+    (16, 1024, 64, 2, 256),    # 64 experts: dispatch tables over every lane of the wave
+    (33, 1024, 8, 2, 512),     # four 16-row blocks per expert
+    (64, 2048, 16, 4, 256),    # the largest decode batch with 8-wave workgroups
+    (12, 4096, 4, 2, 128),     # 16-wave workgroups, one 16-row block
+    (20, 1024, 8, 8, 0),       # top-8 single-linear experts (no GEMM_DOWN; SiLU in the combine)
+])
+def test_decode_self_dispatch(orc, T, d, E, K, h):
+    """Decode batches whose GEMM_UP completes the router's dispatch: the
+    tables, the statistics and the block against the oracle, forward and
+    backward."""
+    say(f"decode self-dispatch T={T} d={d} E={E} K={K} h={h} fwd+bwd")
+    case = make_case(T, d, E, K, h, seed=3 * T + E)
+    Y0 = bf16_bits(np.random.default_rng(T + 1).standard_normal((T, d)).astype(np.float32))
+    g = run_gpu(case, K, h, beta=1.0, Y0=Y0, backward=True, aux=0.1, z=1e-3)
+    r = oracle_case(orc, case, K, h, Y0=Y0, beta=1.0, backward=True, aux=0.1, z=1e-3)
+    check_routing(g, r, E)
+    rr = orc.router(case["X"], case["Wr"], K, bias=case.get("bias"))
+    rd = orc.dispatch(rr["idx"], E)
+    assert np.array_equal(g["counts"], rd["counts"])
+    aux, z = orc.aux_z(rr["probs"], rd["counts"], rr["lse"], K)
+    near(g["aux"], aux, 1e-6, 1e-5, "aux")
+    near(g["z"], z, 1e-6, 1e-5, "z")
+    err = rel_l2(g["Y"], r["Y"])
+    say(f"  Y rel-L2 {err:.2e}")
+    assert err <= REL_L2
+    check_grads(g, r, h, E)
+
+
 def test_empty_batch():
     say("T=0 forward+backward")
     T, d, E, K, h = 0, 256, 4, 2, 256
