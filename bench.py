@@ -395,6 +395,24 @@ def bench_decode(X, Wr, Wu, Wd, d, E, K, h, stream, reps=20, layers=8):
         del graph
     md.close()
     del nets
+    # The fixed cost of one hipGraphLaunch on this stack, from a graph of one
+    # tiny kernel, beside the same kernel launched eagerly back to back: a
+    # graph pays it once per replay, so a step of several layers amortises it.
+    tiny = torch.zeros(256, device="cuda")
+    gt = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        tiny.add_(1.0)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(gt):
+        tiny.add_(1.0)
+    for _ in range(5):
+        gt.replay()
+    out["graph_replay_floor_us"] = round(timed(gt.replay, 200), 2)
+    out["eager_tiny_kernel_us"] = round(timed(lambda: tiny.add_(1.0), 200), 2)
+    del gt
     torch.cuda.empty_cache()
     return out
 
@@ -491,6 +509,45 @@ def bench_adamw(d, E, h, steps=10, warmup=2):
         torch.cuda.empty_cache()
 
 
+def gemm_probe(reps=3):
+    """For counter profiles: the c3 forward (router, grouped UP + DOWN,
+    combine) `reps` times, then hipBLASLt (torch.matmul) on the dense
+    equivalent of the DOWN GEMM -- all T*K routed rows against one expert's
+    [d][h] weight, A[TK][h] . W^T -- `reps` times, random N(0,1) operands.
+    Prints the hipBLASLt rate; the kernels' counters come from the profiler."""
+    import numpy as np
+    import torch
+
+    import tmt_moe
+    from synthetic import CONFIGS, make_case
+
+    cfg = CONFIGS["c3"]
+    T, d, E, K, h = (cfg[k] for k in ("T", "d", "E", "K", "h"))
+    case = make_case(**cfg)
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).cuda().view(torch.bfloat16)
+    X, Wr, Wu, Wd = (dev(case[k]) for k in ("X", "Wr", "W_up", "W_down"))
+    bias = torch.from_numpy(case["bias"]).cuda() if case.get("bias") is not None else None
+    Y = torch.zeros(T, d, dtype=torch.bfloat16, device="cuda")
+    m = tmt_moe.MoE(T, d, E, K, h)
+    for _ in range(reps):
+        m.forward(X, Wr, Wu, Wd, Y, beta=0.0, bias=bias)
+    m.close()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    a = torch.randn(T * K, h, device="cuda", generator=g).to(torch.bfloat16)
+    w = torch.randn(d, h, device="cuda", generator=g).to(torch.bfloat16)
+    c = a @ w.t()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        c = a @ w.t()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return {"hipblaslt_dense_down": {"shape": f"[{T * K}][{h}] x [{d}][{h}]^T", "ms": round(ms, 4),
+                                     "tflops": round(2 * T * K * h * d / ms / 1e9, 1)}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -512,6 +569,8 @@ def main():
                     help="only run a device copy of known size (HBM counter calibration)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the c4 decode measurement (T = 1, 8, 64 on the c3 weights)")
+    ap.add_argument("--gemm-probe", action="store_true",
+                    help="c3 forward GEMMs and hipBLASLt on the dense DOWN shape (for counter profiles)")
     ap.add_argument("--fp4-only", action="store_true",
                     help="only the c5 MXFP4 forward measurement (both weight formats)")
     ap.add_argument("--no-h0", action="store_true",
@@ -532,6 +591,10 @@ def main():
 
     if args.copy_probe:
         copy_probe()
+        return
+    if args.gemm_probe:
+        torch.cuda.set_device(0)
+        print(json.dumps(gemm_probe()))
         return
     if args.fp4_only:
         torch.cuda.set_device(0)
