@@ -166,6 +166,55 @@ def test_topk_ties_and_special_cases(orc):
     assert np.all(out["idx"] == np.array([2, 4]))
 
 
+def _topk_first_max(v, K):
+    """K rounds of arg-max with ties to the lower index (argmax's first hit)."""
+    v = v.copy()
+    rows = np.arange(v.shape[0])
+    out = []
+    for _ in range(K):
+        j = np.argmax(v, 1)
+        out.append(j)
+        v[rows, j] = -np.inf
+    return np.stack(out, 1)
+
+
+def test_selection_on_logits_vs_fp32_probs():
+    """The kernels (and the oracle) rank experts by logit; the reference ranks
+    by the fp32 softmax probability (moe.cu:41-63), both with ties to the
+    lower index. Softmax is monotone, so the two can differ only where
+    distinct logits give one fp32 probability: l - max, exp and the division
+    each merge inputs closer than about one ulp of their operands. This
+    bounds the case by the absolute logit gap: on random rows the selections
+    agree everywhere, and with a planted near-tie straddling the top-k
+    boundary (the higher logit on the higher index) they disagree only for
+    gaps below 2^-20 when |logit - max| < 8."""
+    rng = np.random.default_rng(17)
+    E, K = 16, 4
+
+    def probs(l):
+        m = l.max(1, keepdims=True)
+        e = np.exp((l - m).astype(np.float32)).astype(np.float32)
+        return (e / e.sum(1, keepdims=True, dtype=np.float32)).astype(np.float32)
+
+    l = (2.0 * rng.standard_normal((200000, E))).astype(np.float32)
+    assert np.array_equal(_topk_first_max(l, K), _topk_first_max(probs(l), K))
+
+    n = 20000
+    base = (2.0 * rng.standard_normal((n, E))).astype(np.float32)
+    kth = np.sort(base, 1)[:, E - K]  # the K-th largest logit of the row
+    base[:, 9] = -1e30
+    assert np.abs(base.max(1) - kth).max() < 8
+    disagree = {}
+    for x in (26, 24, 22, 21, 20, 18, 16):
+        l = base.copy()
+        l[:, 9] = (kth + np.float32(2.0 ** -x)).astype(np.float32)
+        l[:, 9] = np.where(l[:, 9] > kth, l[:, 9], np.nextafter(kth, np.float32(np.inf)))
+        a, b = _topk_first_max(l, K), _topk_first_max(probs(l), K)
+        disagree[x] = int((~np.all(np.sort(a, 1) == np.sort(b, 1), 1)).sum())
+    assert disagree[26] > 0 and disagree[21] > 0  # reachable
+    assert disagree[20] == disagree[18] == disagree[16] == 0
+
+
 # -------------------------------------------------------------- dispatch --
 
 def test_dispatch_brute_force(orc):
