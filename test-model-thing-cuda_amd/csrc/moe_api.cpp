@@ -429,8 +429,19 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
         up.ldb = d;
         up.self_dispatch = self ? 1 : 0;
         bool halves = false;  // decode GEMM_DOWN wrote fp32 K halves instead of O
+        // One token: the down GEMM and the combine in one launch.
+        const bool fused1 = T == 1 && skinny && h > 0 && E > 1 && decode1_down_combine_fits(d, h, K);
         LAUNCH(TMT_MOE_PH_GEMM_UP, skinny ? launch_skinny_gemm(GEMM_UP, h > 0, up, T, s)
                                           : launch_gemm(GEMM_UP, h > 0, up, s));
+        if (fused1) {
+            Down1Params dp{};
+            for (int e = 0; e < E; ++e) dp.w[e] = W_down[e];
+            dp.a = m->Aact; dp.idx = m->idx; dp.gate = m->gate; dp.slot_of = m->slot_of;
+            dp.O = m->O; dp.Y = Y; dp.beta = beta; dp.d = d; dp.h = h; dp.K = K;
+            LAUNCH(TMT_MOE_PH_GEMM_DOWN, launch_decode1_down_combine(dp, s));
+            m->last_T = T;
+            return TMT_MOE_OK;
+        }
         if (h > 0) {
             GemmParams dn{};
             dn.offsets = m->offsets; dn.order = m->order; dn.perm = m->perm; dn.E = E;

@@ -141,6 +141,24 @@ constexpr int kSkinnyMaxTokens = 64;
 // p.c, and the combine adds them (CombineParams::part).
 hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int T, hipStream_t s,
                               bool* halves = nullptr);
+// One-token decode: GEMM_DOWN of the token's K experts and the combine in
+// one launch. Workgroup b owns output columns 4b .. 4b+3 for all K picks, so
+// the combine needs no other workgroup's results. Needs K <= 8, h % 256 == 0
+// with 4 <= h / 256 <= 16, and d % 4 == 0.
+struct Down1Params {
+    const uint16_t* w[kMaxExperts];  // W_down[e] [d][h]
+    const uint16_t* a;               // SiLU(U) rows in slot order [K][h]
+    const int32_t* idx;              // [K] the token's experts
+    const float* gate;               // [K]
+    const int32_t* slot_of;          // [K]
+    uint16_t* O;                     // [K][d] expert outputs in slot order (kept for the backward)
+    uint16_t* Y;                     // [1][d]
+    float beta;
+    int d, h, K;
+};
+bool decode1_down_combine_fits(int d, int h, int K);
+hipError_t launch_decode1_down_combine(const Down1Params& p, hipStream_t s);
+
 // Whether a decode forward of these shapes runs every expert GEMM on the
 // skinny stream kernel (the kernel that supports self_dispatch): GEMM_UP
 // with hn output columns and, with h > 0, GEMM_DOWN (K = h, N = d).

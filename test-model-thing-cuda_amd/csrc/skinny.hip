@@ -700,3 +700,101 @@ hipError_t launch_skinny_gemm(GemmKind kind, bool dual, const GemmParams& p, int
 }
 
 }  // namespace tmt
+
+// ------------------------------------------------ one-token down + combine --
+namespace tmt {
+namespace {
+
+__device__ __forceinline__ float bf16_to_float(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+
+// One token, K experts: O_j = W_down[e_j] . a_j for the 4 columns of this
+// workgroup, then Y = beta * Y + sum_j gate_j * bf16(O_j) (the combine's
+// expression and pick order). Wave w reduces k in [256 w, 256 w + 256); lane
+// half hf covers rows hf, hf + 2, ... of the 4K (pick, column) rows with 8
+// consecutive k per lane; each half-wave adds its 32 lanes by a butterfly
+// and the waves are added in order through LDS.
+template <int K>
+__global__ __launch_bounds__(1024) void down_combine1_kernel(Down1Params p) {
+    constexpr int R = 4 * K, RH = R / 2;  // (pick, column) rows; per lane half
+    __shared__ float part[16][R];
+    __shared__ float o_s[R];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nw = (int)blockDim.x >> 6;
+    const int n0 = (int)blockIdx.x * 4;
+    const int hf = lane >> 5, sub = lane & 31;
+    const int k0 = wave * 256 + sub * 8;
+    // the token's picks (one round trip), then everything that depends on them
+    int e[K], sl[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        e[j] = __builtin_amdgcn_readfirstlane(p.idx[j]);
+        sl[j] = __builtin_amdgcn_readfirstlane(p.slot_of[j]);
+    }
+    uint4 wv[RH], av[K];
+#pragma unroll
+    for (int q = 0; q < RH; ++q) {
+        const int r = 2 * q + hf, j = r >> 2, c = r & 3;
+        wv[q] = *reinterpret_cast<const uint4*>(p.w[e[j]] + (int64_t)(n0 + c) * p.h + k0);
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) av[j] = *reinterpret_cast<const uint4*>(p.a + (int64_t)sl[j] * p.h + k0);
+    float acc[RH];
+#pragma unroll
+    for (int q = 0; q < RH; ++q) {
+        const int j = (2 * q + hf) >> 2;
+        float wf[8], af[8];
+        unpack8(wv[q], wf);
+        unpack8(av[j], af);
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) s = __builtin_fmaf(wf[t], af[t], s);
+        acc[q] = s;
+    }
+#pragma unroll
+    for (int q = 0; q < RH; ++q) {
+        float v = acc[q];
+        v += __shfl_xor(v, 16, 64);
+        v += __shfl_xor(v, 8, 64);
+        v += __shfl_xor(v, 4, 64);
+        v += __shfl_xor(v, 2, 64);
+        v += __shfl_xor(v, 1, 64);
+        if (sub == 0) part[wave][2 * q + hf] = v;
+    }
+    __syncthreads();
+    if (tid < R) {
+        float v = part[0][tid];
+        for (int w2 = 1; w2 < nw; ++w2) v += part[w2][tid];
+        const uint16_t ob = f2bf(v);
+        const int j = tid >> 2, c = tid & 3;
+        p.O[(int64_t)sl[j] * p.d + n0 + c] = ob;
+        o_s[tid] = bf16_to_float(ob);
+    }
+    __syncthreads();
+    if (tid < 4) {
+        float y = p.beta != 0.0f ? bf16_to_float(p.Y[n0 + tid]) * p.beta : 0.0f;
+#pragma unroll
+        for (int j = 0; j < K; ++j) y += p.gate[j] * o_s[4 * j + tid];
+        p.Y[n0 + tid] = f2bf(y);
+    }
+}
+
+}  // namespace
+
+bool decode1_down_combine_fits(int d, int h, int K) {
+    return K >= 1 && K <= 8 && h % 256 == 0 && h / 256 >= 4 && h / 256 <= 16 && d % 4 == 0 && d > 0;
+}
+
+hipError_t launch_decode1_down_combine(const Down1Params& p, hipStream_t s) {
+    if (!decode1_down_combine_fits(p.d, p.h, p.K)) return hipErrorInvalidValue;
+    const dim3 grid(p.d / 4), block(64 * (p.h / 256));
+    switch (p.K) {
+#define TMT_D1(KK) case KK: down_combine1_kernel<KK><<<grid, block, 0, s>>>(p); break;
+        TMT_D1(1) TMT_D1(2) TMT_D1(3) TMT_D1(4) TMT_D1(5) TMT_D1(6) TMT_D1(7) TMT_D1(8)
+#undef TMT_D1
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace tmt

@@ -324,6 +324,9 @@ def test_decode_steps_against_oracle(orc, T):
     (1, 64, 2, 1, 256),      # a single token and expert, d of one unit
     (24, 1024, 8, 2, 4096),  # persistent UP, two resident row blocks, 2-3 tiles per workgroup
     (12, 512, 3, 2, 2048),   # persistent DOWN over 8 waves, one tile and a past-the-end prefetch
+    (1, 256, 8, 1, 1024),    # one token: down GEMM + combine in one launch, top-1, 4 waves
+    (1, 512, 16, 8, 2048),   # one token, top-8 (32 rows per workgroup), 8 waves
+    (1, 1024, 64, 4, 4096),  # one token, 64 experts, 16 waves
 ])
 def test_decode_shapes_against_oracle(orc, T, d, E, K, h):
     """Decode-sized batches (T <= 64 use the weight-streaming expert GEMMs);
