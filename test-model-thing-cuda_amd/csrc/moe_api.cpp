@@ -155,11 +155,12 @@ int validate_desc(const tmt_moe_desc* d) {
     return TMT_MOE_OK;
 }
 
-// Router rows per workgroup: 4 waves x R rows x iterations, aiming at a few
-// hundred workgroups and staying within the permutation kernel's group limit.
+// Router rows per workgroup: kRouterWaves waves x R rows x iterations, aiming
+// at a few hundred workgroups and staying within the permutation kernel's
+// group limit.
 int router_rows_per_block(int T, int E, int K) {
     const int R = router_rows_per_wave(E);
-    const int base = 4 * R;
+    const int base = kRouterWaves * R;
     int iter = T / (base * 512);
     const int rg = 64 / K;
     int iter_max = (64 * rg) / base;

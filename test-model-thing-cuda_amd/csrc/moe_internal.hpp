@@ -17,7 +17,8 @@ namespace tmt {
 
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
-constexpr int kThreads = 256;  // every kernel runs 4 waves of 64
+constexpr int kThreads = 256;  // every kernel runs 4 waves of 64 ...
+constexpr int kRouterWaves = 8;  // ... except the router: 8 waves share one staged Wr
 
 // ---------------------------------------------------------------- router --
 struct RouterParams {
@@ -25,7 +26,7 @@ struct RouterParams {
     const uint16_t* Wr;    // [E][d] bf16
     const float* bias;     // [E] or nullptr
     int T, d, E, K;
-    int rows_per_block;    // multiple of 4 * (64 / EP)
+    int rows_per_block;    // multiple of kRouterWaves * (64 / EP)
     float* logits;         // [T][E]
     float* probs;          // [T][E]
     int32_t* idx;          // [T][K]

@@ -263,11 +263,13 @@ __device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t
 // WLDS: Wr is staged in LDS (E*d*2 <= kRouterWrLdsBytes); otherwise the
 // waves read it from global memory (it stays in L2), with the same
 // arithmetic and therefore the same bits.
-template <int EP, bool WLDS>
-__global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
+// NW waves per workgroup share one staged copy of Wr; the block statistics
+// add the waves' sums in wave order.
+template <int EP, bool WLDS, int NW>
+__global__ __launch_bounds__(64 * NW) void router_kernel(RouterParams p) {
     extern __shared__ uint4 smem_w[];  // Wr [E][d] bf16 (WLDS)
     __shared__ int s_cnt[kMaxExperts];
-    __shared__ float s_stat[4][kMaxExperts + 1];
+    __shared__ float s_stat[NW][kMaxExperts + 1];
 
     const int tid = threadIdx.x;
     const int E = p.E;
@@ -278,30 +280,29 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterParams p) {
     const int row_begin = blockIdx.x * p.rows_per_block;
     const int row_end = min(p.T, row_begin + p.rows_per_block);
     const uint16_t* wl = WLDS ? reinterpret_cast<const uint16_t*>(smem_w) : p.Wr;
-    route_rows<EP, 4>(p, wl, row_begin, row_end, s_cnt, s_stat, nullptr);
+    route_rows<EP, NW>(p, wl, row_begin, row_end, s_cnt, s_stat, nullptr);
     __syncthreads();
     // Block statistics: waves added in order.
     const int b = blockIdx.x;
-    if (tid < E) {
-        p.blkstat[(int64_t)b * (E + 1) + tid] =
-            ((s_stat[0][tid] + s_stat[1][tid]) + s_stat[2][tid]) + s_stat[3][tid];
-        p.blkcnt[(int64_t)b * E + tid] = s_cnt[tid];
+    if (tid <= E) {
+        const int col = tid < E ? tid : kMaxExperts;
+        float v = s_stat[0][col];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v += s_stat[w][col];
+        p.blkstat[(int64_t)b * (E + 1) + tid] = v;
+        if (tid < E) p.blkcnt[(int64_t)b * E + tid] = s_cnt[tid];
     }
-    if (tid == 0)
-        p.blkstat[(int64_t)b * (E + 1) + E] =
-            ((s_stat[0][kMaxExperts] + s_stat[1][kMaxExperts]) + s_stat[2][kMaxExperts]) +
-            s_stat[3][kMaxExperts];
 }
 
 hipError_t launch_router(const RouterParams& p, int nblk, hipStream_t s) {
     const bool wlds = router_wr_in_lds(p.E, p.d);
     const size_t lds = wlds ? (size_t)p.E * p.d * 2 : 0;
     const int ep = router_ep(p.E);
-    dim3 grid(nblk), block(kThreads);
+    dim3 grid(nblk), block(64 * kRouterWaves);
 #define TMT_ROUTER(EP_)                                                                \
     case EP_:                                                                         \
-        if (wlds) router_kernel<EP_, true><<<grid, block, lds, s>>>(p);               \
-        else router_kernel<EP_, false><<<grid, block, 0, s>>>(p);                     \
+        if (wlds) router_kernel<EP_, true, kRouterWaves><<<grid, block, lds, s>>>(p); \
+        else router_kernel<EP_, false, kRouterWaves><<<grid, block, 0, s>>>(p);       \
         break;
     switch (ep) {
         TMT_ROUTER(8)
