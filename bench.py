@@ -190,9 +190,9 @@ def bench_mxfp4(stream, reps=5):
             # rate): two activation terms, so twice the algorithmic flops
             r["gemm_down_frac_fp4_peak"] = round(2 * gemm_flops / (ph["gemm_down"] / 1e3) / 1e12 / PEAK_FP4_TFLOPS, 4)
             r["gemm_up_frac_fp4_peak"] = round(2 * gemm_flops / (ph["gemm_up"] / 1e3) / 1e12 / PEAK_FP4_TFLOPS, 4)
-            r["note"] = ("activations as two MXFP6 terms (quantised in the up GEMM's epilogue and one gather "
-                         "kernel), FP6 x FP4 v_mfma_scale_f32_32x32x64_f8f6f4; gemm_up includes the gather-quantise "
-                         "kernel; frac counts both terms' MFMA flops against the 10.1 PF FP4/FP6 peak")
+            r["note"] = ("activations as two MXFP6 terms (X once per token, gathered by the up GEMM; SiLU(U) in "
+                         "the up GEMM's epilogue), FP6 x FP4 v_mfma_scale_f32_32x32x64_f8f6f4; gemm_up includes the "
+                         "per-token quantise kernel; frac counts both terms' MFMA flops against the 10.1 PF FP4/FP6 peak")
         out[name] = r
     out["faster"] = "mx" if out["mx"]["ms"] < out["exact"]["ms"] else "exact"
     # headline fields keep their meaning: the faster format's numbers

@@ -53,7 +53,7 @@ constexpr int AS_BYTES = 1024, BS_BYTES = 1024;
 constexpr int STAGE = A_BYTES + B_BYTES + AS_BYTES + BS_BYTES;
 constexpr int A_LOADS = A_BYTES / 1024 / 4;  // 1 KiB wave loads per wave
 constexpr int B_LOADS = B_BYTES / 1024 / 4;
-constexpr int DMA_PER_TILE = A_LOADS + B_LOADS + 1;
+constexpr int DMA_PER_TILE = A_LOADS + B_LOADS + 2;  // + the wave's activation-scale rows, the weight scales
 constexpr int EPR = 64, WTN = 128;  // epilogue: rows per wave and pass, wave tile width
 constexpr int EPI = 4 * EPR * WTN * 4;
 constexpr int LDS_BYTES = NST * STAGE > EPI ? NST * STAGE : EPI;
@@ -69,6 +69,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // (lds_base wave-uniform); M0 is declared clobbered.
 __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base) : "m0");
+}
+// The same with 4 bytes per lane, to LDS at lds_base + 4 * lane.
+__device__ __forceinline__ void dma4(const void* sbase, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base) : "m0");
 }
 #pragma clang diagnostic pop
 template <int N>
@@ -215,13 +219,19 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
 
     // ---- DMA addressing: wave-uniform bases, 32-bit lane offsets ------------
     // (the host keeps every offset below 2^31)
+    // Activation row of tile row r: slot row0 + r (clamped to the last slot),
+    // or the token that slot gathers (a_perm).
+    auto a_src = [&](int r) {
+        const int slot = min(row0 + r, p.slots - 1);
+        return p.a_perm ? p.a_perm[slot] : slot;
+    };
     uint32_t a_off[A_LOADS];
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
         const int s = (wave * A_LOADS + i) * 64 + lane;  // 16-byte slot of the A region
         const int kb = s / (BM * 3), rem = s % (BM * 3);
         const int row = rem / 3, c = rem % 3;
-        a_off[i] = (uint32_t)(min(row0 + row, p.slots - 1) * a_row_bytes + kb * 48 + c * 16);
+        a_off[i] = (uint32_t)(a_src(row) * a_row_bytes + kb * 48 + c * 16);
     }
     uint32_t b_off[B_LOADS];
 #pragma unroll
@@ -232,17 +242,13 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     }
     const uint8_t* wq = p.wq[e];
     const uint8_t* wsc = p.wsc[e];
-    // scales: waves 0 and 2 load the activation scales (the same bytes to
-    // the same place), waves 1 and 3 the weight scales
-    const bool a_scale_wave = (wave & 1) == 0;
-    uint32_t sc_off;
-    if (a_scale_wave) {
-        sc_off = (uint32_t)(row0 + 4 * lane) * 4u;
-    } else {
-        const int kb = (lane >> 4) & 1;
-        sc_off = (uint32_t)(kb * p.N + min(nt * BN + (lane & 15) * 16, p.N - 16));
-    }
-    const uint32_t sc_lds = a_scale_wave ? A_BYTES + B_BYTES : A_BYTES + B_BYTES + AS_BYTES;
+    // scales: wave w loads the activation scales of tile rows 64w .. 64w+63
+    // (4 bytes per row and lane, rows gathered like the codes); every wave
+    // loads the tile's weight scales (the same bytes to the same place)
+    const uint32_t as_off = (uint32_t)a_src(64 * wave + lane) * 4u;
+    const uint32_t as_lds = A_BYTES + B_BYTES + 256u * (uint32_t)wave;
+    const uint32_t ws_off = (uint32_t)(((lane >> 4) & 1) * p.N + min(nt * BN + (lane & 15) * 16, p.N - 16));
+    constexpr uint32_t ws_lds = A_BYTES + B_BYTES + AS_BYTES;
     const uint32_t lds0 = lds_addr(lds);
     auto dma_tile = [&](int t) {
         const int kt = min(t, nk - 1);
@@ -253,8 +259,8 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
         for (int i = 0; i < A_LOADS; ++i) dma16(ab, a_off[i], sb + (uint32_t)(wave * A_LOADS + i) * 1024u);
 #pragma unroll
         for (int i = 0; i < B_LOADS; ++i) dma16(bb, b_off[i], sb + A_BYTES + (uint32_t)(wave * B_LOADS + i) * 1024u);
-        const uint8_t* sbase = a_scale_wave ? p.a_scales + (int64_t)kt * p.a_srows * 4 : wsc + (int64_t)kt * 2 * p.N;
-        dma16(sbase, sc_off, sb + sc_lds);
+        dma4(p.a_scales + (int64_t)kt * p.a_srows * 4, as_off, sb + as_lds);
+        dma16(wsc + (int64_t)kt * 2 * p.N, ws_off, sb + ws_lds);
     };
 
     // ---- fragments ----------------------------------------------------------

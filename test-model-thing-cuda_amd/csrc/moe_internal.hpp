@@ -189,9 +189,10 @@ struct MxGemmParams {
     const int32_t* offsets;  // [E+1] expert segments (slot space)
     int E;
     int N, K, slots;         // output columns, reduction length, routed rows
-    const uint8_t* a_codes;  // activations, MX6x2 [slots][K]
-    const uint8_t* a_scales;
+    const uint8_t* a_codes;  // activations, MX6x2 [rows][K]: slot order, or
+    const uint8_t* a_scales; // token order gathered through a_perm
     int64_t a_srows;
+    const int32_t* a_perm;   // [slots] slot -> activation row (nullptr: the slot)
     const uint8_t* wq[kMaxExperts];   // e2m1 codes [N][K/2] per expert
     const uint8_t* wsc[kMaxExperts];  // e8m0 scales [K/32][N] per expert
     uint16_t* c;             // bf16 output [slots][ldc] (quant_out == false)
