@@ -11,8 +11,17 @@
 // tiles (256 fp32 accumulators per lane, held in AGPRs).
 //
 // Operand staging: direct global -> LDS loads (global_load_lds_dwordx4, the
-// data never passes through VGPRs) into a ring of 4 LDS stages of K = 32
-// (32 KiB each), issued three tiles ahead of the MFMAs that use them.
+// data never passes through VGPRs). Two ring layouts:
+//   * split rings (the activation GEMMs on 256 x 256 tiles): K = 64 tiles,
+//     the A operand in a ring of 3 slots and B in a ring of 2 (32 KiB each,
+//     160 KiB in all). Iteration kt loads B(kt+1) and A(kt+2). K = 64 makes
+//     each K-contiguous row a full 128-byte segment: the CU accepts one
+//     1 KiB load per 16 cycles when every row segment of the load is >= 128
+//     bytes, but only one per 29-34 cycles with 64-byte segments from L2 or
+//     HBM, so with K = 32 stages the loads alone filled the CU's load path;
+//   * one ring of NST stages of K = 32 (32 KiB for 256 x 256, 24 KiB for
+//     256 x 128), issued NST - 1 tiles ahead (weight-gradient GEMMs, the
+//     MXFP4 variants and 128-column tiles).
 //   * K-contiguous operands (activations in every GEMM, weights in the
 //     forward) land as [256 rows][32] bf16, 16-byte chunks XOR-swizzled by
 //     (row >> 2) & 3, and are read with ds_read_b128.
@@ -67,11 +76,9 @@ struct Geo {
     static constexpr int KC_ROWS = 1024 / (2 * BK);    // K-contiguous rows per wave load
     static constexpr int STEPS = BK / 16;              // MFMA k16 steps per stage
     static constexpr int WGS = BN == 256 ? 1 : 2;      // workgroups per CU
-    // LDS of the ring, also the epilogue's fp32 staging ([64][WTN] per wave)
-    static constexpr int RING = NST * STAGE * 2;
+    // the epilogue's fp32 staging ([EPR][WTN] per wave); the kernel sizes the
+    // ring (single or split) and checks the total
     static constexpr int EPI = NW * EPR * WTN * 4;
-    static constexpr int LDS = RING > EPI ? RING : EPI;
-    static_assert(LDS * WGS <= 160 * 1024, "LDS ring too large");
     // K-contiguous rows: 16-byte chunk swizzle making 16 consecutive rows (the
     // lanes one ds_read_b128 cycle serves from the 64 banks = 256 bytes) hit
     // distinct banks: rows r and r + 4j share (r & 3) * 64 bytes of bank offset
@@ -226,14 +233,23 @@ __device__ __forceinline__ void act_tile(const GemmParams& p, int mt, int& e, in
     }
 }
 
+// Split rings (A in NST slots, B in NST - 1) for K = 64 tiles of the
+// activation GEMMs on 256 x 256 tiles.
+template <int KIND, int BK, int BN, int NWM>
+constexpr bool split_ring() {
+    return BK == 64 && BN == 256 && NWM == 2 && !Traits<KIND>::group_k && !Traits<KIND>::b_fp4;
+}
+
 template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2>
 __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
     using Tr = Traits<KIND>;
     using Gm = Geo<BK_, NST, BN_, NWM_>;
     constexpr int BK = Gm::BK, NSTAGE = Gm::NSTAGE, BN = Gm::BN, WTN = Gm::WTN, NJ = Gm::NJ;
     constexpr int WTM = Gm::WTM, MI = Gm::MI, NT = Gm::NT, EPR = Gm::EPR;
-    constexpr int OPND_A = Gm::OPND_A;
+    constexpr int OPND_A = Gm::OPND_A, OPND_B = Gm::OPND_B;
     constexpr int DMA_A = Gm::DMA_A, DMA_B = Gm::DMA_B;
+    constexpr bool kSplit = split_ring<KIND, BK_, BN_, NWM_>();
+    static_assert(!kSplit || NST == 3, "split rings: 3 A slots and 2 B slots");
     // MXFP4 B operand per stage: 256 rows x 16 bytes of codes (BK = 32 = one
     // scale block), then one 1 KiB copy of the 256 row scales per wave.
     static_assert(!Tr::b_fp4 || (BK == 32 && BN == 256 && NWM_ == 2), "MXFP4 tiles: one scale block, 256 columns, 4 waves");
@@ -241,7 +257,8 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     constexpr int STAGE = Tr::b_fp4 ? OPND_A + (FP4_CODES + FP4_SCALES) / 2 : Gm::STAGE;  // bf16 elements
     constexpr int DMA_PER_TILE = Tr::b_fp4 ? DMA_A + 2 : Gm::DMA_PER_TILE;
     constexpr int KCH = Gm::KCH, KC_ROWS = Gm::KC_ROWS, STEPS = Gm::STEPS;
-    constexpr int LDS_TOTAL = NSTAGE * STAGE * 2 > Gm::EPI ? NSTAGE * STAGE * 2 : Gm::EPI;
+    constexpr int RING = kSplit ? (NST * OPND_A + (NST - 1) * OPND_B) * 2 : NSTAGE * STAGE * 2;
+    constexpr int LDS_TOTAL = RING > Gm::EPI ? RING : Gm::EPI;
     static_assert(LDS_TOTAL * Gm::WGS <= 160 * 1024, "LDS ring too large");
     __shared__ uint4 lds_raw[LDS_TOTAL / 16];
     uint16_t* lds = reinterpret_cast<uint16_t*>(lds_raw);
@@ -382,6 +399,23 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
         sc_ptr = p.wsc[e] + (g < p.N ? g : nt * BN);
     }
     const uint32_t lds0 = lds_addr(lds);
+    // bf16 element offsets of tile t's A and B operand tiles in LDS
+    auto a_slot = [&](int t) -> int { return kSplit ? (t % NST) * OPND_A : (t % NSTAGE) * STAGE; };
+    auto b_slot = [&](int t) -> int {
+        return kSplit ? NST * OPND_A + (t % (NST - 1)) * OPND_B : (t % NSTAGE) * STAGE + OPND_A;
+    };
+    // Wave load i of tile t's A / B operand (t clamped to the last real tile
+    // so the per-tile load count stays constant).
+    auto dma_a = [&](int t, int i) {
+        const int k0 = kbeg + min(t, nk - 1) * BK;
+        const uint16_t* ga = Tr::a_kc ? a_ptr[i] + k0 : a_ptr[i] + (int64_t)min(k0 + a_k[i], kend - 1) * p.lda;
+        dma16(ga, lds0 + (uint32_t)a_slot(t) * 2u + (uint32_t)(wave * DMA_A + i) * 1024u);
+    };
+    auto dma_b = [&](int t, int i) {
+        const int k0 = kbeg + min(t, nk - 1) * BK;
+        const uint16_t* gb = Tr::b_kc ? b_ptr[i] + k0 : b_ptr[i] + (int64_t)min(k0 + b_k[i], kend - 1) * p.ldb;
+        dma16(gb, lds0 + (uint32_t)b_slot(t) * 2u + (uint32_t)(wave * DMA_B + i) * 1024u);
+    };
     // Issue the 8 wave loads of K tile t (clamped to the last real tile so the
     // per-tile load count stays constant) into stage t % NSTAGE.
     auto dma_tile = [&](int t) {
@@ -480,8 +514,8 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
         return dequant8(w, scales[r]);
     };
     auto load_frag = [&](Frag& f, int t, int s) {
-        const uint16_t* tA = lds + (t % NSTAGE) * STAGE;
-        const uint16_t* tB = tA + OPND_A;
+        const uint16_t* tA = lds + a_slot(t);
+        const uint16_t* tB = lds + b_slot(t);
 #pragma unroll
         for (int i = 0; i < MI; ++i)
             f.a[i] = Tr::a_kc ? read_kc(tA, wm * WTM + 32 * i, s) : read_mc(tA, BM, wm * WTM + 32 * i, s);
@@ -543,7 +577,68 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     // visible, and every wave is done reading the stage that the next
     // iteration refills); the last step then prefetches step 0 of tile kt+1.
     constexpr int VM_AHEAD = (NSTAGE - 2) * DMA_PER_TILE;
-    if (nk > 0) {
+    if constexpr (kSplit) {
+        // Split rings. Iteration kt multiplies tile kt in STEPS k16 steps;
+        // the loads of B(kt+1) and then A(kt+2) are spread over the MFMAs of
+        // the first STEPS - 1 steps (their slots were last read by tile kt-1,
+        // before the previous barrier). Loads complete in issue order, so
+        // waiting until only A(kt+2)'s loads are outstanding leaves all of
+        // tile kt+1 in LDS at the barrier; the last step then prefetches
+        // tile kt+1's first fragments.
+        constexpr int ND = DMA_A + DMA_B;
+        auto mma_loads = [&](const Frag& f, int kt, int d0, int dn) {
+            constexpr int NM = MI * NJ;
+            int dq = 0;
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8, f.b[j]), __builtin_bit_cast(bf16x8, f.a[i]),
+                        acc[i][j], 0, 0, 0);
+                    const int q = i * NJ + j;
+                    if (dq < dn && (q + 1) * dn >= (dq + 1) * NM) {
+                        const int d = d0 + dq;
+                        __builtin_amdgcn_sched_barrier(0);
+                        if (d < DMA_B) dma_b(kt + 1, d);
+                        else dma_a(kt + 2, d - DMA_B);
+                        __builtin_amdgcn_sched_barrier(0);
+                        ++dq;
+                    }
+                }
+        };
+        auto dfirst = [](int s) { return s * ND / (STEPS - 1); };
+        if (nk > 0) {
+#pragma unroll
+            for (int i = 0; i < DMA_A; ++i) dma_a(0, i);
+#pragma unroll
+            for (int i = 0; i < DMA_B; ++i) dma_b(0, i);
+#pragma unroll
+            for (int i = 0; i < DMA_A; ++i) dma_a(1, i);
+            wait_vm<DMA_A>();
+            __syncthreads();
+            Frag f[2];
+            load_frag(f[0], 0, 0);
+            for (int kt = 0; kt < nk; ++kt) {
+#pragma unroll
+                for (int s = 0; s < STEPS - 1; ++s) {
+                    load_frag(f[(s + 1) & 1], kt, s + 1);
+                    mma_loads(f[s & 1], kt, dfirst(s), dfirst(s + 1) - dfirst(s));
+                }
+                wait_vm<DMA_A>();
+                __syncthreads();
+                load_frag(f[0], min(kt + 1, nk - 1), 0);
+                mma(f[(STEPS - 1) & 1]);
+#pragma unroll
+                for (int q = 0; q < MI * NJ / 2; ++q) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // DS read
+                }
+                __builtin_amdgcn_sched_group_barrier(0x008, MI * NJ / 2, 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    } else if (nk > 0) {
 #pragma unroll
         for (int t = 0; t < NSTAGE - 1; ++t) dma_tile(t);
         wait_vm<(NSTAGE >= 2 ? VM_AHEAD : 0)>();
@@ -734,23 +829,31 @@ __global__ __launch_bounds__(256) void split_fixup_kernel(GemmParams p) {
 
 }  // namespace
 
-constexpr int kBK = 32, kNST = 4;  // fastest of BK 32/64 x 2-4 stages on the c3 shapes
+// Tile depth and ring per kind and tile width: split rings of K = 64 for the
+// activation GEMMs on 256 columns; K = 32 rings otherwise (4 stages of 32 KiB
+// at 256 columns, 3 of 24 KiB at 128 columns with two workgroups per CU).
+template <int KIND, int BN>
+struct Ring {
+    static constexpr bool split = split_ring<KIND, 64, BN, 2>();
+    static constexpr int BK = split ? 64 : 32;
+    static constexpr int NST = split ? 3 : (BN == 256 ? 4 : 3);
+};
 
 template <int KIND, bool DUAL, int BN, int NWM = 2>
 hipError_t launch_kind(const GemmParams& p, unsigned grid, hipStream_t s) {
-    constexpr int NST = BN == 256 ? kNST : 3;  // two workgroups per CU at BN 128: 3 x 24 KiB stages
-    grouped_gemm_kernel<KIND, DUAL, kBK, NST, BN, NWM><<<grid, 128 * NWM, 0, s>>>(p);
+    using R = Ring<KIND, BN>;
+    grouped_gemm_kernel<KIND, DUAL, R::BK, R::NST, BN, NWM><<<grid, 128 * NWM, 0, s>>>(p);
     return hipGetLastError();
 }
 
-// Tile width per GEMM kind (BN 128 = two workgroups per CU). Measured on the
-// c3 shapes with random operands: the second workgroup hides the heavy
-// epilogues (UP writes U and SiLU(U), DACT reads U) and the weight-gradient
-// tails; DOWN and DX are main-loop bound and lose to the 50% larger operand
-// traffic of the narrower tile.
+// Tile width per GEMM kind (BN 128 = two workgroups per CU). Measured in the
+// c3 step: UP, DOWN and DX run fastest on 256-column tiles with split rings
+// (UP 1.31 -> 1.26 ms against two 128-column workgroups per CU); DACT, whose
+// epilogue reads a U tile, keeps two 128-column workgroups per CU (1.33
+// against 1.39 ms), and so do the weight-gradient GEMMs, whose co-resident
+// workgroups hide each other's Zipf-sized tails.
 int gemm_tile_n(GemmKind kind) {
     switch (kind) {
-        case GEMM_UP:
         case GEMM_DACT:
         case GEMM_DW_DOWN:
         case GEMM_DW_UP: return 128;
@@ -773,7 +876,7 @@ hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn,
         const int64_t ntm = (p.M + BM - 1) / BM;
         groups = (int64_t)p.E * ((ntm + gm - 1) / gm) * ngn;
     } else {
-        if (p.K % kBK != 0) return hipErrorInvalidValue;
+        if (p.K % (bn == 256 && !fp4 ? 64 : 32) != 0) return hipErrorInvalidValue;
         // sum_e ceil(cnt_e / BM) <= ceil(slots / BM) + E - 1
         const int64_t mtiles = (int64_t)(p.slots + BM - 1) / BM + p.E;
         groups = ((mtiles + gm - 1) / gm) * ngn;
@@ -795,7 +898,8 @@ hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn,
         hipError_t err = kind == GEMM_DOWN ? launch_kind<GEMM_DOWN, false, 256>(p, g, s)
                                            : launch_kind<GEMM_DX, false, 256>(p, g, s);
         if (err != hipSuccess) return err;
-        split_fixup_kernel<kBK, 256><<<p.resident, 256, 0, s>>>(p);
+        static_assert(Ring<GEMM_DOWN, 256>::BK == Ring<GEMM_DX, 256>::BK, "one split plan for DOWN and DX");
+        split_fixup_kernel<Ring<GEMM_DOWN, 256>::BK, 256><<<p.resident, 256, 0, s>>>(p);
         return hipGetLastError();
     }
     switch (kind) {
