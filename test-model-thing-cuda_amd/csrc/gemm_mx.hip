@@ -45,8 +45,9 @@ constexpr int BM = kGemmTileRows;  // 256 token rows per tile
 constexpr int BN = 256;            // output columns per tile
 constexpr int NST = 4;             // LDS ring stages of K = 64
 // One stage: activation codes [2 blocks][256 rows][48 B], weight codes
-// [2 blocks][256 n][16 B], activation scales [256 rows][4 B], weight scales
-// [2 blocks][256 n] (a 1 KiB load; the second half is unused).
+// [256 n][2 halves][16 B] (block = half ^ bit 3 of n), activation scales
+// [256 rows][4 B], weight scales [2 blocks][256 n] (a 1 KiB load; the second
+// half is unused).
 constexpr int A_BYTES = 2 * BM * 48;
 constexpr int B_BYTES = 2 * BN * 16;
 constexpr int AS_BYTES = 1024, BS_BYTES = 1024;
@@ -233,11 +234,16 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
         const int row = rem / 3, c = rem % 3;
         a_off[i] = (uint32_t)(a_src(row) * a_row_bytes + kb * 48 + c * 16);
     }
+    // Weight codes: lane pair (2m, 2m+1) loads the 32 contiguous bytes (both
+    // 32-blocks) of row m, so a wave load covers 32 rows x 32 bytes rather
+    // than 64 rows x 16 bytes. In LDS the row's two 16-byte halves are swapped
+    // when bit 3 of the row is set, which keeps the fragment reads (16 rows
+    // at a 32-byte stride) free of bank conflicts.
     uint32_t b_off[B_LOADS];
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
-        const int s = (wave * B_LOADS + i) * 64 + lane;
-        const int kb = s / BN, n = s % BN;
+        const int s = (wave * B_LOADS + i) * 64 + lane;  // 16-byte slot of the B region: row s/2, half s%2
+        const int n = s >> 1, kb = (s & 1) ^ ((n >> 3) & 1);
         b_off[i] = (uint32_t)(min(nt * BN + n, p.N - 1) * (int64_t)(p.K / 2) + kb * 16);
     }
     const uint8_t* wq = p.wq[e];
@@ -268,7 +274,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     // (src1): six dwords each, read as 16 + 8 bytes (term 0) and 8 + 16
     // bytes (term 1) so that every operand lands in consecutive registers.
     const int kb = lane >> 5;
-    const int b_lane = (kb * BN + wn * 128 + (lane & 31)) * 16;           // + 512 j
+    const int b_lane = (2 * (wn * 128 + (lane & 31)) + (kb ^ ((lane >> 3) & 1))) * 16;  // + 1024 j
     const int bs_lane = A_BYTES + B_BYTES + AS_BYTES + kb * BN + wn * 128 + (lane & 31);  // + 32 j
     const int a_lane = (kb * BM + wm * 128 + (lane & 31)) * 48;          // + 1536 i
     const int as_lane = A_BYTES + B_BYTES + (wm * 128 + (lane & 31)) * 4;  // + 128 i
@@ -289,7 +295,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     do {                                                                                              \
         const uint8_t* st_ = lds + (sg) * STAGE;                                                      \
         _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                               \
-            bq[B][j] = *reinterpret_cast<const i32x4*>(st_ + A_BYTES + b_lane + 512 * j);             \
+            bq[B][j] = *reinterpret_cast<const i32x4*>(st_ + A_BYTES + b_lane + 1024 * j);            \
             bsc[B][j] = st_[bs_lane + 32 * j];                                                        \
         }                                                                                             \
     } while (0)
