@@ -44,7 +44,8 @@ typedef int i32x2 __attribute__((ext_vector_type(2)));
 constexpr int BM = kGemmTileRows;  // 256 token rows per tile
 constexpr int BN = 256;            // output columns per tile
 constexpr int NST = 4;             // LDS ring stages of K = 64
-// One stage: activation codes [2 blocks][256 rows][48 B], weight codes
+// One stage: activation codes [256 rows][2 halves][48 B] (block = half ^
+// bit 3 of the row), weight codes
 // [256 n][2 halves][16 B] (block = half ^ bit 3 of n), activation scales
 // [256 rows][4 B], weight scales [2 blocks][256 n] (a 1 KiB load; the second
 // half is unused).
@@ -226,12 +227,16 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
         const int slot = min(row0 + r, p.slots - 1);
         return p.a_perm ? p.a_perm[slot] : slot;
     };
+    // Activation codes: six consecutive 16-byte slots hold one row's 96 bytes
+    // of the stage (both 32-blocks, contiguous in memory), so a wave load
+    // covers ~11 rows x 96 bytes. The row's two 48-byte halves are swapped in
+    // LDS when bit 3 of the row is set (conflict-free fragment reads).
     uint32_t a_off[A_LOADS];
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
         const int s = (wave * A_LOADS + i) * 64 + lane;  // 16-byte slot of the A region
-        const int kb = s / (BM * 3), rem = s % (BM * 3);
-        const int row = rem / 3, c = rem % 3;
+        const int row = s / 6, part = s % 6;
+        const int kb = (part / 3) ^ ((row >> 3) & 1), c = part % 3;
         a_off[i] = (uint32_t)(a_src(row) * a_row_bytes + kb * 48 + c * 16);
     }
     // Weight codes: lane pair (2m, 2m+1) loads the 32 contiguous bytes (both
@@ -276,7 +281,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     const int kb = lane >> 5;
     const int b_lane = (2 * (wn * 128 + (lane & 31)) + (kb ^ ((lane >> 3) & 1))) * 16;  // + 1024 j
     const int bs_lane = A_BYTES + B_BYTES + AS_BYTES + kb * BN + wn * 128 + (lane & 31);  // + 32 j
-    const int a_lane = (kb * BM + wm * 128 + (lane & 31)) * 48;          // + 1536 i
+    const int a_lane = (wm * 128 + (lane & 31)) * 96 + (kb ^ ((lane >> 3) & 1)) * 48;  // + 3072 i
     const int as_lane = A_BYTES + B_BYTES + (wm * 128 + (lane & 31)) * 4;  // + 128 i
     const int as_shift = 16 * kb;
     i32x4 bq[2][4];
@@ -302,7 +307,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     // A fragments of row block i of the tile in stage `sg`.
 #define MX_LOAD_A(i, sg)                                                                              \
     do {                                                                                              \
-        const uint8_t* pa_ = lds + (sg) * STAGE + a_lane + 1536 * (i);                                \
+        const uint8_t* pa_ = lds + (sg) * STAGE + a_lane + 3072 * (i);                                \
         const i32x4 x0_ = *reinterpret_cast<const i32x4*>(pa_);                                       \
         const i32x2 x1_ = *reinterpret_cast<const i32x2*>(pa_ + 16);                                  \
         const i32x2 x2_ = *reinterpret_cast<const i32x2*>(pa_ + 24);                                  \
