@@ -237,7 +237,7 @@ __device__ __forceinline__ void act_tile(const GemmParams& p, int mt, int& e, in
 // activation GEMMs on 256 x 256 tiles.
 template <int KIND, int BK, int BN, int NWM>
 constexpr bool split_ring() {
-    return BK == 64 && BN == 256 && NWM == 2 && !Traits<KIND>::group_k && !Traits<KIND>::b_fp4;
+    return BK == 64 && BN == 256 && NWM == 2 && !Traits<KIND>::group_k;
 }
 
 template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2>
@@ -250,14 +250,18 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     constexpr int DMA_A = Gm::DMA_A, DMA_B = Gm::DMA_B;
     constexpr bool kSplit = split_ring<KIND, BK_, BN_, NWM_>();
     static_assert(!kSplit || NST == 3, "split rings: 3 A slots and 2 B slots");
-    // MXFP4 B operand per stage: 256 rows x 16 bytes of codes (BK = 32 = one
-    // scale block), then one 1 KiB copy of the 256 row scales per wave.
-    static_assert(!Tr::b_fp4 || (BK == 32 && BN == 256 && NWM_ == 2), "MXFP4 tiles: one scale block, 256 columns, 4 waves");
-    constexpr int FP4_CODES = 256 * 16, FP4_SCALES = 4 * 1024;
+    // MXFP4 B operand per tile: 256 rows x BK/2 bytes of codes, then one 1 KiB
+    // copy per wave of the tile's row scales (one 32-block at BK = 32, two at
+    // BK = 64: lanes 16-31 load the second block's).
+    static_assert(!Tr::b_fp4 || (BN == 256 && NWM_ == 2 && (BK == 32 || kSplit)), "MXFP4 tiles: 256 columns, 4 waves");
+    constexpr int FP4_CODES = 256 * (BK / 2), FP4_SCALES = 4 * 1024;
     constexpr int STAGE = Tr::b_fp4 ? OPND_A + (FP4_CODES + FP4_SCALES) / 2 : Gm::STAGE;  // bf16 elements
     constexpr int DMA_PER_TILE = Tr::b_fp4 ? DMA_A + 2 : Gm::DMA_PER_TILE;
+    // split rings: B slot size (bf16 elements) and wave loads per B tile
+    constexpr int B_SLOT = Tr::b_fp4 ? (FP4_CODES + FP4_SCALES) / 2 : OPND_B;
+    constexpr int DMA_BT = Tr::b_fp4 ? FP4_CODES / 1024 / 4 + 1 : DMA_B;
     constexpr int KCH = Gm::KCH, KC_ROWS = Gm::KC_ROWS, STEPS = Gm::STEPS;
-    constexpr int RING = kSplit ? (NST * OPND_A + (NST - 1) * OPND_B) * 2 : NSTAGE * STAGE * 2;
+    constexpr int RING = kSplit ? (NST * OPND_A + (NST - 1) * B_SLOT) * 2 : NSTAGE * STAGE * 2;
     constexpr int LDS_TOTAL = RING > Gm::EPI ? RING : Gm::EPI;
     static_assert(LDS_TOTAL * Gm::WGS <= 160 * 1024, "LDS ring too large");
     __shared__ uint4 lds_raw[LDS_TOTAL / 16];
@@ -390,19 +394,33 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     // MXFP4: wave w loads the codes of rows 64w + lane (16 bytes per tile) and
     // its own copy of the tile's 256 row scales (lane l -> rows 16(l%16)..+15;
     // row groups past N are clamped to the tile's first group).
+    // With split rings (BK = 64) lane pair (2m, 2m+1) loads the 32 code bytes
+    // of row m (two 16-byte halves, swapped in LDS when bit 3 of m is set) and
+    // lanes 16-31 load the second scale block.
     const uint8_t* q_ptr = nullptr;
+    const uint8_t* q2_ptr[2] = {nullptr, nullptr};
     const uint8_t* sc_ptr = nullptr;
     if constexpr (Tr::b_fp4) {
-        const int n = min(nt * BN + 64 * wave + lane, p.N - 1);
-        q_ptr = p.wq[e] + (int64_t)n * (p.K / 2);
         const int g = nt * BN + 16 * (lane & 15);
-        sc_ptr = p.wsc[e] + (g < p.N ? g : nt * BN);
+        if constexpr (kSplit) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int sl = (wave * 2 + i) * 64 + lane, m = sl >> 1;
+                const int half = (sl & 1) ^ ((m >> 3) & 1);
+                q2_ptr[i] = p.wq[e] + (int64_t)min(nt * BN + m, p.N - 1) * (p.K / 2) + half * 16;
+            }
+            sc_ptr = p.wsc[e] + (int64_t)((lane >> 4) & 1) * p.N + (g < p.N ? g : nt * BN);
+        } else {
+            const int n = min(nt * BN + 64 * wave + lane, p.N - 1);
+            q_ptr = p.wq[e] + (int64_t)n * (p.K / 2);
+            sc_ptr = p.wsc[e] + (g < p.N ? g : nt * BN);
+        }
     }
     const uint32_t lds0 = lds_addr(lds);
     // bf16 element offsets of tile t's A and B operand tiles in LDS
     auto a_slot = [&](int t) -> int { return kSplit ? (t % NST) * OPND_A : (t % NSTAGE) * STAGE; };
     auto b_slot = [&](int t) -> int {
-        return kSplit ? NST * OPND_A + (t % (NST - 1)) * OPND_B : (t % NSTAGE) * STAGE + OPND_A;
+        return kSplit ? NST * OPND_A + (t % (NST - 1)) * B_SLOT : (t % NSTAGE) * STAGE + OPND_A;
     };
     // Wave load i of tile t's A / B operand (t clamped to the last real tile
     // so the per-tile load count stays constant).
@@ -413,8 +431,14 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     };
     auto dma_b = [&](int t, int i) {
         const int k0 = kbeg + min(t, nk - 1) * BK;
-        const uint16_t* gb = Tr::b_kc ? b_ptr[i] + k0 : b_ptr[i] + (int64_t)min(k0 + b_k[i], kend - 1) * p.ldb;
-        dma16(gb, lds0 + (uint32_t)b_slot(t) * 2u + (uint32_t)(wave * DMA_B + i) * 1024u);
+        if constexpr (Tr::b_fp4) {
+            const uint32_t sb = lds0 + (uint32_t)b_slot(t) * 2u;
+            if (i < DMA_BT - 1) dma16(q2_ptr[i] + k0 / 2, sb + (uint32_t)(wave * (DMA_BT - 1) + i) * 1024u);
+            else dma16(sc_ptr + (int64_t)(k0 / 32) * p.N, sb + FP4_CODES + (uint32_t)wave * 1024u);
+        } else {
+            const uint16_t* gb = Tr::b_kc ? b_ptr[i] + k0 : b_ptr[i] + (int64_t)min(k0 + b_k[i], kend - 1) * p.ldb;
+            dma16(gb, lds0 + (uint32_t)b_slot(t) * 2u + (uint32_t)(wave * DMA_B + i) * 1024u);
+        }
     };
     // Issue the 8 wave loads of K tile t (clamped to the last real tile so the
     // per-tile load count stays constant) into stage t % NSTAGE.
@@ -510,8 +534,16 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
         const uint8_t* codes = reinterpret_cast<const uint8_t*>(tB);
         const uint8_t* scales = codes + FP4_CODES + wave * 1024;
         const int r = rbase + (lane & 31);
-        const uint32_t w = *reinterpret_cast<const uint32_t*>(codes + r * 16 + (2 * s + (lane >> 5)) * 4);
-        return dequant8(w, scales[r]);
+        if constexpr (kSplit) {
+            // k = 16s + 8(lane/32) .. +7: byte 8s + 4(lane/32) of the row's 32
+            const int blk = s >> 1, within = (8 * s + 4 * (lane >> 5)) & 15;
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(
+                codes + r * 32 + ((blk ^ ((lane >> 3) & 1)) * 16) + within);
+            return dequant8(w, scales[blk * 256 + r]);
+        } else {
+            const uint32_t w = *reinterpret_cast<const uint32_t*>(codes + r * 16 + (2 * s + (lane >> 5)) * 4);
+            return dequant8(w, scales[r]);
+        }
     };
     auto load_frag = [&](Frag& f, int t, int s) {
         const uint16_t* tA = lds + a_slot(t);
@@ -585,7 +617,7 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
         // waiting until only A(kt+2)'s loads are outstanding leaves all of
         // tile kt+1 in LDS at the barrier; the last step then prefetches
         // tile kt+1's first fragments.
-        constexpr int ND = DMA_A + DMA_B;
+        constexpr int ND = DMA_A + DMA_BT;
         auto mma_loads = [&](const Frag& f, int kt, int d0, int dn) {
             constexpr int NM = MI * NJ;
             int dq = 0;
@@ -600,8 +632,8 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
                     if (dq < dn && (q + 1) * dn >= (dq + 1) * NM) {
                         const int d = d0 + dq;
                         __builtin_amdgcn_sched_barrier(0);
-                        if (d < DMA_B) dma_b(kt + 1, d);
-                        else dma_a(kt + 2, d - DMA_B);
+                        if (d < DMA_BT) dma_b(kt + 1, d);
+                        else dma_a(kt + 2, d - DMA_BT);
                         __builtin_amdgcn_sched_barrier(0);
                         ++dq;
                     }
@@ -612,7 +644,7 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
 #pragma unroll
             for (int i = 0; i < DMA_A; ++i) dma_a(0, i);
 #pragma unroll
-            for (int i = 0; i < DMA_B; ++i) dma_b(0, i);
+            for (int i = 0; i < DMA_BT; ++i) dma_b(0, i);
 #pragma unroll
             for (int i = 0; i < DMA_A; ++i) dma_a(1, i);
             wait_vm<DMA_A>();
@@ -866,7 +898,7 @@ hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn,
     if (bn != 256 && bn != 128) return hipErrorInvalidValue;
     const bool group_k = kind == GEMM_DW_DOWN || kind == GEMM_DW_UP;
     const bool fp4 = kind == GEMM_UP_FP4 || kind == GEMM_DOWN_FP4;
-    if (fp4 && (p.K % 32 != 0 || bn != 256)) return hipErrorInvalidValue;
+    if (fp4 && (p.K % 64 != 0 || bn != 256)) return hipErrorInvalidValue;
     const int64_t ntn = (p.N + bn - 1) / bn;
     const int64_t gn = ntn < 8 ? ntn : 8, gm = 32 / gn;
     const int64_t ngn = (ntn + gn - 1) / gn;
