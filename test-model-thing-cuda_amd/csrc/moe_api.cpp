@@ -324,6 +324,26 @@ int prof_end(tmt_moe* m, int slot, hipStream_t s) {
         if (rc__) return rc__;                            \
     } while (0)
 
+// Router, scan and permutation arguments of a decode batch (T <= 64): the
+// outputs route_small_kernel writes, or the one-token GEMM_UP that routes its
+// token itself.
+Route1 small_route_params(tmt_moe* m, int T, const uint16_t* X, const uint16_t* Wr, const float* bias) {
+    const int E = m->desc.experts, K = m->desc.topk, d = m->desc.d;
+    Route1 r{};
+    RouterParams& rp = r.rp;
+    rp.X = X; rp.Wr = Wr; rp.bias = bias;
+    rp.T = T; rp.d = d; rp.E = E; rp.K = K; rp.rows_per_block = T;
+    rp.logits = m->logits; rp.probs = m->probs; rp.idx = m->idx; rp.gate = m->gate;
+    rp.lse = m->lse;
+    ScanParams& sp = r.sp;
+    sp.T = T; sp.E = E; sp.K = K; sp.nblk = 1;
+    sp.counts = m->counts; sp.offsets = m->offsets; sp.order = m->order; sp.stats = m->stats;
+    PermuteParams& pp = r.pp;
+    pp.T = T; pp.E = E; pp.K = K; pp.rows_per_block = T;
+    pp.perm = m->perm; pp.slot_of = m->slot_of;
+    return r;
+}
+
 // Routing + dispatch: router / scan / permute (E > 1) or identity (E == 1).
 // picks_only (decode batches whose GEMM_UP runs with self_dispatch): the
 // router writes the picks and the GEMM_UP completes the dispatch.
@@ -336,18 +356,8 @@ int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* W
         return TMT_MOE_OK;
     }
     if (T >= 1 && T <= kSmallRouteTokens) {
-        RouterParams rp{};
-        rp.X = X; rp.Wr = Wr; rp.bias = bias;
-        rp.T = T; rp.d = d; rp.E = E; rp.K = K; rp.rows_per_block = T;
-        rp.logits = m->logits; rp.probs = m->probs; rp.idx = m->idx; rp.gate = m->gate;
-        rp.lse = m->lse;
-        ScanParams sp{};
-        sp.T = T; sp.E = E; sp.K = K; sp.nblk = 1;
-        sp.counts = m->counts; sp.offsets = m->offsets; sp.order = m->order; sp.stats = m->stats;
-        PermuteParams pp{};
-        pp.T = T; pp.E = E; pp.K = K; pp.rows_per_block = T;
-        pp.perm = m->perm; pp.slot_of = m->slot_of;
-        LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(rp, sp, pp, picks_only ? nullptr : m->ticket, s));
+        const Route1 r = small_route_params(m, T, X, Wr, bias);
+        LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(r.rp, r.sp, r.pp, picks_only ? nullptr : m->ticket, s));
         return TMT_MOE_OK;
     }
     const int rpb = router_rows_per_block(T, E, K);
@@ -419,7 +429,11 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
     // workgroup writes the dispatch tables.
     const bool skinny = T <= kSkinnyMaxTokens;
     const bool self = skinny && skinny_self_dispatch(T, E, K, d, h, hn);
-    if ((rc = route(m, s, T, X, Wr, logit_bias, self))) return rc;
+    // One token whose down GEMM and combine run as one launch: the up GEMM
+    // routes the token itself, so the forward is two launches.
+    const bool fused1 = T == 1 && h > 0 && E > 1 && decode1_down_combine_fits(d, h, K);
+    const bool route1 = fused1 && skinny_up_route1_fits(d, E);
+    if (!route1 && (rc = route(m, s, T, X, Wr, logit_bias, self))) return rc;
     if (T > 0) {
         GemmParams up{};
         up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
@@ -430,10 +444,13 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
         up.ldb = d;
         up.self_dispatch = self ? 1 : 0;
         bool halves = false;  // decode GEMM_DOWN wrote fp32 K halves instead of O
-        // One token: the down GEMM and the combine in one launch.
-        const bool fused1 = T == 1 && skinny && h > 0 && E > 1 && decode1_down_combine_fits(d, h, K);
-        LAUNCH(TMT_MOE_PH_GEMM_UP, skinny ? launch_skinny_gemm(GEMM_UP, h > 0, up, T, s)
-                                          : launch_gemm(GEMM_UP, h > 0, up, s));
+        if (route1) {
+            const Route1 r = small_route_params(m, T, X, Wr, logit_bias);
+            LAUNCH(TMT_MOE_PH_GEMM_UP, launch_skinny_up_route1(true, up, r, s));
+        } else {
+            LAUNCH(TMT_MOE_PH_GEMM_UP, skinny ? launch_skinny_gemm(GEMM_UP, h > 0, up, T, s)
+                                              : launch_gemm(GEMM_UP, h > 0, up, s));
+        }
         if (fused1) {
             Down1Params dp{};
             for (int e = 0; e < E; ++e) dp.w[e] = W_down[e];

@@ -159,6 +159,18 @@ struct Down1Params {
 };
 bool decode1_down_combine_fits(int d, int h, int K);
 hipError_t launch_decode1_down_combine(const Down1Params& p, hipStream_t s);
+// One-token decode: GEMM_UP routes its token itself, with the arithmetic of
+// route_small_kernel's single-token path (every workgroup computes the picks
+// it needs; workgroup 0 also writes the router outputs and the dispatch
+// tables), so no router launch precedes it. Needs E > 1 and the chunk
+// kernel's reduction shape (d % 256 == 0, 4 <= d / 256 <= 16).
+struct Route1 {
+    RouterParams rp;
+    ScanParams sp;
+    PermuteParams pp;
+};
+bool skinny_up_route1_fits(int d, int E);
+hipError_t launch_skinny_up_route1(bool dual, const GemmParams& p, const Route1& r, hipStream_t s);
 
 // Whether a decode forward of these shapes runs every expert GEMM on the
 // skinny stream kernel (the kernel that supports self_dispatch): GEMM_UP

@@ -30,6 +30,7 @@
 // trip before the activation loads).
 #include "device_util.hpp"
 #include "dispatch.hpp"
+#include "route_row.hpp"
 #include "moe_internal.hpp"
 
 namespace tmt {
@@ -257,9 +258,14 @@ constexpr int kSkinnyStreamTokens = 4;
 // its activation chunk and multiplies; blocks past the expert's count are
 // skipped as a whole (uniform branch). No load sits under a divergent
 // branch, so the compiler's wait counts stay exact.
-template <int KIND, bool DUAL, int J, int RB, int CT>
-__global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int nexp) {
+// EP1 > 0 (GEMM_UP of one token, launch_skinny_up_route1): the workgroup
+// routes the token itself -- logits over its waves, softmax and top-k on EP1
+// lanes of wave 0 -- and takes the rank-th picked expert in ascending index
+// (the slot order); workgroup 0 also writes the router outputs and tables.
+template <int KIND, bool DUAL, int J, int RB, int CT, int EP1 = 0>
+__global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int nexp, Route1 r1) {
     static_assert(KIND == GEMM_UP || KIND == GEMM_DOWN, "forward GEMMs only");
+    static_assert(EP1 == 0 || (KIND == GEMM_UP && RB == 1), "self-routing: the one-token GEMM_UP");
     constexpr bool kGather = KIND == GEMM_UP;
     extern __shared__ f32x4 red[];  // [RB][CT][nw][64] wave partials
     __shared__ int s_tok[16][16 * RB];
@@ -270,8 +276,31 @@ __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int ne
     const int rank = (int)blockIdx.x % nexp, tile0 = ((int)blockIdx.x / nexp) * CT;
     args_in_sgprs(p.order, p.offsets, p.idx, p.a, p.c, p.c2, p.E, p.slots, p.topk, p.lda, p.ldb, p.ldc);
     int ent[kPickGroups];
-    if constexpr (kGather) load_picks(p, lane, ent);
-    const SkinnyExpert x = skinny_expert(p, rank, lane);
+    SkinnyExpert x;
+    if constexpr (EP1 > 0) {
+        __shared__ float s_logit1[kMaxExperts];
+        __shared__ int s_e1;
+        token_logits(r1.rp, 0, s_logit1, wave, nw, lane);
+        __syncthreads();
+        if (wave == 0) {
+            const int e = lane % EP1;
+            const bool ev = lane < EP1 && e < r1.rp.E;
+            const float logit = ev ? s_logit1[e] : 0.0f;
+            const RowPick pk = softmax_topk<EP1>(logit, ev, e, r1.rp.K);
+            if (blockIdx.x == 0) one_token_dispatch<EP1>(r1.rp, r1.sp, r1.pp, logit, ev, pk, lane);
+            uint64_t selm = __ballot(ev && pk.sel);
+            for (int i = 0; i < rank; ++i) selm &= selm - 1;  // drop the rank lowest picks
+            if (lane == 0) s_e1 = (int)__builtin_ctzll(selm);
+        }
+        __syncthreads();
+        x.e = __builtin_amdgcn_readfirstlane(s_e1);
+        x.row0 = rank;  // a single token's slots follow ascending expert index
+        x.rows = 1;
+        x.w = p.w[x.e];
+    } else {
+        if constexpr (kGather) load_picks(p, lane, ent);
+        x = skinny_expert(p, rank, lane);
+    }
     const int row0 = x.row0;
     const int rows = min(x.rows, 16 * RB);
     if (rows <= 0) return;
@@ -289,7 +318,7 @@ __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int ne
 #pragma unroll
         for (int i = 0; i < J; ++i) wv[c][i] = ld16_buf(wr, off + 64 * i);
     }
-    const bool by_pick = kGather && p.idx != nullptr;
+    const bool by_pick = kGather && EP1 == 0 && p.idx != nullptr;
     if (by_pick) expert_tokens(ent, p.slots, p.topk, x.e, lane, 16 * RB, s_tok[wave]);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -297,7 +326,7 @@ __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int ne
         const int m = rb * 16 + li;
         const bool ok = m < rows;
         const int mm = ok ? m : 0;
-        const int srow = by_pick ? s_tok[wave][mm] : row0 + mm;
+        const int srow = EP1 > 0 ? 0 : (by_pick ? s_tok[wave][mm] : row0 + mm);
         const uint16_t* ar = p.a + (int64_t)srow * p.lda + kw;
         uint4 av[J];
 #pragma unroll
@@ -509,9 +538,9 @@ hipError_t launch_chunk_rb(int rb, int nw, const GemmParams& p, int nexp, hipStr
     const dim3 block(64 * nw);
     const size_t lds = (size_t)rb * CT * nw * 64 * sizeof(f32x4);
     switch (rb) {
-        case 1: skinny_chunk_kernel<KIND, DUAL, J, 1, CT><<<grid, block, lds, s>>>(p, nexp); break;
-        case 2: skinny_chunk_kernel<KIND, DUAL, J, 2, CT><<<grid, block, lds, s>>>(p, nexp); break;
-        case 4: skinny_chunk_kernel<KIND, DUAL, J, 4, CT><<<grid, block, lds, s>>>(p, nexp); break;
+        case 1: skinny_chunk_kernel<KIND, DUAL, J, 1, CT><<<grid, block, lds, s>>>(p, nexp, Route1{}); break;
+        case 2: skinny_chunk_kernel<KIND, DUAL, J, 2, CT><<<grid, block, lds, s>>>(p, nexp, Route1{}); break;
+        case 4: skinny_chunk_kernel<KIND, DUAL, J, 4, CT><<<grid, block, lds, s>>>(p, nexp, Route1{}); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -645,6 +674,36 @@ int halves_split(const SkinnyShape& sh, int T, int N, int64_t ldb, int nexp) {
 }
 
 }  // namespace
+
+bool skinny_up_route1_fits(int d, int E) {
+    const SkinnyShape sh = skinny_shape(d, 1);
+    return E > 1 && E <= kMaxExperts && sh.J == 8 && sh.nw >= 1;
+}
+
+hipError_t launch_skinny_up_route1(bool dual, const GemmParams& p, const Route1& r, hipStream_t s) {
+    if (!skinny_up_route1_fits(p.K, p.E) || p.N % 16 != 0 || p.N <= 0 || r.rp.T != 1 || r.rp.d != p.K ||
+        r.rp.E != p.E || r.rp.K != p.topk || p.slots != p.topk || p.topk > kMaxTopK)
+        return hipErrorInvalidValue;
+    const SkinnyShape sh = skinny_shape(p.K, 1);
+    const int nexp = p.topk;  // one rank per pick
+    const unsigned grid = (unsigned)(p.N / 16) * (unsigned)nexp;
+    const dim3 block(64 * sh.nw);
+    const size_t lds = (size_t)sh.nw * 64 * sizeof(f32x4);
+#define TMT_R1(EP_)                                                                                      \
+    case EP_:                                                                                           \
+        if (dual) skinny_chunk_kernel<GEMM_UP, true, 8, 1, 1, EP_><<<grid, block, lds, s>>>(p, nexp, r);  \
+        else skinny_chunk_kernel<GEMM_UP, false, 8, 1, 1, EP_><<<grid, block, lds, s>>>(p, nexp, r);      \
+        break;
+    switch (router_ep(p.E)) {
+        TMT_R1(8)
+        TMT_R1(16)
+        TMT_R1(32)
+        TMT_R1(64)
+        default: return hipErrorInvalidValue;
+    }
+#undef TMT_R1
+    return hipGetLastError();
+}
 
 bool skinny_self_dispatch(int T, int E, int K, int d, int h, int hn) {
     (void)K;
