@@ -856,11 +856,22 @@ __global__ __launch_bounds__(256) void split_fixup_kernel(GemmParams p) {
         if (e < 0 || row >= rows || nt * BN + col >= p.N) continue;
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         const float* src = p.part + (int64_t)j * sp.S * BM * BN + (int64_t)row * BN + col;
-        for (int q = 0; q < sp.S; ++q) {
-            const f32x4 a = *reinterpret_cast<const f32x4*>(src + (int64_t)q * BM * BN);
-            const f32x4 b = *reinterpret_cast<const f32x4*>(src + (int64_t)q * BM * BN + 4);
-            acc[0] += a[0]; acc[1] += a[1]; acc[2] += a[2]; acc[3] += a[3];
-            acc[4] += b[0]; acc[5] += b[1]; acc[6] += b[2]; acc[7] += b[3];
+        // the loads of up to 8 parts in flight together (one round trip per
+        // 8 parts), then added in part order
+        for (int q0 = 0; q0 < sp.S; q0 += 8) {
+            f32x4 a[8], b[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int q = min(q0 + u, sp.S - 1);  // clamped: the extra loads are not added
+                a[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)q * BM * BN);
+                b[u] = *reinterpret_cast<const f32x4*>(src + (int64_t)q * BM * BN + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (q0 + u >= sp.S) break;
+                acc[0] += a[u][0]; acc[1] += a[u][1]; acc[2] += a[u][2]; acc[3] += a[u][3];
+                acc[4] += b[u][0]; acc[5] += b[u][1]; acc[6] += b[u][2]; acc[7] += b[u][3];
+            }
         }
         *reinterpret_cast<uint4*>(C + (int64_t)(row0 + row) * p.ldc + nt * BN + col) = pack8(acc);
     }
