@@ -162,8 +162,9 @@ hipError_t launch_decode1_down_combine(const Down1Params& p, hipStream_t s);
 // One-token decode: GEMM_UP routes its token itself, with the arithmetic of
 // route_small_kernel's single-token path (every workgroup computes the picks
 // it needs; workgroup 0 also writes the router outputs and the dispatch
-// tables), so no router launch precedes it. Needs E > 1 and the chunk
-// kernel's reduction shape (d % 256 == 0, 4 <= d / 256 <= 16).
+// tables), so no router launch precedes it. Needs E > 1 and a chunk
+// kernel reduction shape (d % 256 == 0 with 4 <= d / 256 <= 16, or
+// d % 64 == 0 with d / 64 <= 16).
 struct Route1 {
     RouterParams rp;
     ScanParams sp;

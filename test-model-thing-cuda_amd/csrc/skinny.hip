@@ -677,7 +677,7 @@ int halves_split(const SkinnyShape& sh, int T, int N, int64_t ldb, int nexp) {
 
 bool skinny_up_route1_fits(int d, int E) {
     const SkinnyShape sh = skinny_shape(d, 1);
-    return E > 1 && E <= kMaxExperts && sh.J == 8 && sh.nw >= 1;
+    return E > 1 && E <= kMaxExperts && (sh.J == 8 || sh.J == 2) && sh.nw >= 1;
 }
 
 hipError_t launch_skinny_up_route1(bool dual, const GemmParams& p, const Route1& r, hipStream_t s) {
@@ -689,10 +689,15 @@ hipError_t launch_skinny_up_route1(bool dual, const GemmParams& p, const Route1&
     const unsigned grid = (unsigned)(p.N / 16) * (unsigned)nexp;
     const dim3 block(64 * sh.nw);
     const size_t lds = (size_t)sh.nw * 64 * sizeof(f32x4);
-#define TMT_R1(EP_)                                                                                      \
-    case EP_:                                                                                           \
-        if (dual) skinny_chunk_kernel<GEMM_UP, true, 8, 1, 1, EP_><<<grid, block, lds, s>>>(p, nexp, r);  \
-        else skinny_chunk_kernel<GEMM_UP, false, 8, 1, 1, EP_><<<grid, block, lds, s>>>(p, nexp, r);      \
+#define TMT_R1(EP_)                                                                                       \
+    case EP_:                                                                                            \
+        if (sh.J == 8) {                                                                                 \
+            if (dual) skinny_chunk_kernel<GEMM_UP, true, 8, 1, 1, EP_><<<grid, block, lds, s>>>(p, nexp, r); \
+            else skinny_chunk_kernel<GEMM_UP, false, 8, 1, 1, EP_><<<grid, block, lds, s>>>(p, nexp, r);     \
+        } else {                                                                                         \
+            if (dual) skinny_chunk_kernel<GEMM_UP, true, 2, 1, 1, EP_><<<grid, block, lds, s>>>(p, nexp, r); \
+            else skinny_chunk_kernel<GEMM_UP, false, 2, 1, 1, EP_><<<grid, block, lds, s>>>(p, nexp, r);     \
+        }                                                                                                \
         break;
     switch (router_ep(p.E)) {
         TMT_R1(8)
