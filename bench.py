@@ -53,6 +53,10 @@ def kernel_work(phase, T, d, E, K, h):
         "scatter": ("hbm", 2 * TK * d + 2 * T * d + 4 * T * E + 4 * TK),
         # S read, H written, row mean + 1/std written, gamma + beta read
         "norm": ("hbm", 4 * T * d + 8 * T + 8 * d),
+        # the router with the LayerNorm of its rows (routed batches of the
+        # LayerNorm-fronted block): S read, H written, row statistics, gamma
+        # and beta, then the router's own outputs
+        "router_ln": ("hbm", 4 * T * d + 8 * T + 8 * d + 2 * E * d + 8 * T * E + 8 * TK + 4 * T),
         # scatter with the LayerNorm backward fused (d <= 2048): dXg rows, S,
         # dlogits, slots and row statistics read, dS written
         "scatter_ln": ("hbm", 2 * TK * d + 4 * T * d + 4 * T * E + 4 * TK + 8 * T),
@@ -455,11 +459,15 @@ def bench_layernorm(m, X, Wr, Wu, Wd, dY, T, d, E, K, h, aux_c, z_c, steps, warm
     prof = m.profile(reset=True)
     m.set_profiling(False)
     out = {"ms_per_step": round(ms, 4), "tokens_s": round(T / (ms / 1e3), 1)}
-    # "scatter" now carries the LayerNorm backward rows; "norm_bwd" is the
-    # fixed-order dGamma/dBeta column sum of the per-workgroup partials.
-    for ph, key in (("norm", "norm"), ("scatter", "scatter_ln"), ("norm_bwd", None)):
+    # The router normalises its rows itself on routed batches ("router" then
+    # carries the LayerNorm forward, and no "norm" launch runs); "scatter"
+    # carries the LayerNorm backward rows; "norm_bwd" is the fixed-order
+    # dGamma/dBeta column sum of the per-workgroup partials.
+    for ph, key in (("router", "router_ln"), ("norm", "norm"), ("scatter", "scatter_ln"), ("norm_bwd", None)):
         tot, n = prof[ph]
-        avg = tot / max(n, 1)
+        if n == 0:
+            continue
+        avg = tot / n
         k = {"avg_ms": round(avg, 4)}
         if key:
             _, work = kernel_work(key, T, d, E, K, h)

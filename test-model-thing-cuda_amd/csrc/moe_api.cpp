@@ -347,14 +347,27 @@ Route1 small_route_params(tmt_moe* m, int T, const uint16_t* X, const uint16_t* 
 // Routing + dispatch: router / scan / permute (E > 1) or identity (E == 1).
 // picks_only (decode batches whose GEMM_UP runs with self_dispatch): the
 // router writes the picks and the GEMM_UP completes the dispatch.
+// The LayerNorm that tmt_moe_forward_ln hands to the router (S, gamma, beta).
+struct LnFuse {
+    const uint16_t* S;
+    const float* gamma;
+    const float* beta;
+};
+// Routed batches (E > 1, more than kSmallRouteTokens tokens) whose rows the
+// router can normalise itself.
+bool ln_in_router(int T, int E, int d) { return E > 1 && T > kSmallRouteTokens && router_ln_fits(E, d); }
+
+// ln: the router computes H = LayerNorm(ln->S) into m->H (with the row
+// statistics) and routes H; only where ln_in_router holds.
 int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* Wr, const float* bias,
-          bool picks_only = false) {
+          bool picks_only = false, const LnFuse* ln = nullptr) {
     const int E = m->desc.experts, K = m->desc.topk, d = m->desc.d;
     if (E == 1) {
         LAUNCH(TMT_MOE_PH_PERMUTE, launch_dense_dispatch(T, m->perm, m->slot_of, m->gate, m->counts,
                                                         m->offsets, m->order, m->stats, s));
         return TMT_MOE_OK;
     }
+    if (ln && !ln_in_router(T, E, d)) return fail(TMT_MOE_EINVAL, "internal: LayerNorm not fusable into this router");
     if (T >= 1 && T <= kSmallRouteTokens) {
         const Route1 r = small_route_params(m, T, X, Wr, bias);
         LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(r.rp, r.sp, r.pp, picks_only ? nullptr : m->ticket, s));
@@ -369,6 +382,10 @@ int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* W
         rp.T = T; rp.d = d; rp.E = E; rp.K = K; rp.rows_per_block = rpb;
         rp.logits = m->logits; rp.probs = m->probs; rp.idx = m->idx; rp.gate = m->gate;
         rp.lse = m->lse; rp.blkcnt = m->blkcnt; rp.blkstat = m->blkstat;
+        if (ln) {
+            rp.X = ln->S; rp.ln_gamma = ln->gamma; rp.ln_beta = ln->beta;
+            rp.ln_H = m->H; rp.ln_mean = m->ln_mean; rp.ln_rstd = m->ln_rstd;
+        }
         LAUNCH(TMT_MOE_PH_ROUTER, launch_router(rp, nblk, s));
     }
     ScanParams sp{};
@@ -414,9 +431,11 @@ int check_forward(tmt_moe* m, int T, const uint16_t* X, const char* xname, const
 }
 
 // Routing, expert GEMMs and combine of the bf16 forward (arguments checked).
+// ln: the router normalises the block input itself (X is then m->H, which the
+// router writes before any expert GEMM reads it).
 int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* Wr,
                 const float* logit_bias, const uint16_t* const* W_up, const uint16_t* const* W_down,
-                uint16_t* Y, float beta) {
+                uint16_t* Y, float beta, const LnFuse* ln = nullptr) {
     const tmt_moe_desc& ds = m->desc;
     const int E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden, hn = m->hn;
     int rc;
@@ -433,7 +452,8 @@ int run_forward(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint1
     // routes the token itself, so the forward is two launches.
     const bool fused1 = T == 1 && h > 0 && E > 1 && decode1_down_combine_fits(d, h, K);
     const bool route1 = fused1 && skinny_up_route1_fits(d, E);
-    if (!route1 && (rc = route(m, s, T, X, Wr, logit_bias, self))) return rc;
+    if (ln && (route1 || self)) return fail(TMT_MOE_EINVAL, "internal: LayerNorm not fusable into this router");
+    if (!route1 && (rc = route(m, s, T, X, Wr, logit_bias, self, ln))) return rc;
     if (T > 0) {
         GemmParams up{};
         up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
@@ -785,8 +805,13 @@ int tmt_moe_forward_ln(tmt_moe* m, void* stream, int32_t T, const uint16_t* S,
     LayerNormParams ln{};
     ln.S = S; ln.gamma = ln_gamma; ln.beta = ln_beta; ln.T = T; ln.d = m->desc.d;
     ln.H = m->H; ln.mean = m->ln_mean; ln.rstd = m->ln_rstd;
-    LAUNCH(TMT_MOE_PH_NORM, launch_ln_fwd(ln, s));
-    if ((rc = run_forward(m, s, T, m->H, Wr, logit_bias, W_up, W_down, Y, beta))) return rc;
+    // Routed batches: the router normalises its rows itself (one read of S
+    // instead of a LayerNorm pass and a read of H); otherwise the LayerNorm
+    // runs first.
+    const LnFuse fuse{S, ln_gamma, ln_beta};
+    const bool fused = ln_in_router(T, m->desc.experts, m->desc.d);
+    if (!fused) LAUNCH(TMT_MOE_PH_NORM, launch_ln_fwd(ln, s));
+    if ((rc = run_forward(m, s, T, m->H, Wr, logit_bias, W_up, W_down, Y, beta, fused ? &fuse : nullptr))) return rc;
     m->last_ln = true;
     return TMT_MOE_OK;
 }

@@ -34,8 +34,20 @@ struct RouterParams {
     float* lse;            // [T]
     int32_t* blkcnt;       // [nblk][E] picks per expert in each block
     float* blkstat;        // [nblk][E+1] sum of probs per expert, sum of lse^2
+    // LayerNorm in front of the router (tmt_moe_forward_ln): X is then the
+    // block input S, and the router also writes H, the LayerNorm output that
+    // the expert GEMMs read, and the row statistics. ln_H == nullptr: X is the
+    // router input itself.
+    const float* ln_gamma;  // [d]
+    const float* ln_beta;   // [d]
+    uint16_t* ln_H;         // [T][d] bf16
+    float* ln_mean;         // [T]
+    float* ln_rstd;         // [T]
 };
 int router_ep(int E);  // padded expert count used by the router (power of 2)
+// The router can run the LayerNorm of its rows itself (a wave's rows of S
+// held in registers: rows per wave x 512-element chunks <= 16, d <= 2048).
+bool router_ln_fits(int E, int d);
 // Wr is staged in LDS by the router and the dX scatter when it fits in this
 // many bytes; wider routers (E*d*2 larger) are read from global memory.
 constexpr size_t kRouterWrLdsBytes = 65536;

@@ -2,16 +2,13 @@
 // the block (tmt-cuda/src/norm.cu:8-106; caller tmt-cuda/src/model.cu:509-514,
 // 678-680).
 //
-//   ln_fwd      H = bf16(((x - mean) * rstd) * gamma + beta), one wave per row.
-//               Row statistics in the canonical order the CPU oracle restates:
-//               element k on lane (k/8) mod 64, lane sums (x) and sums of x*x
-//               in ascending k from +0 (x*x of a bf16 value is exact, so the
-//               fused multiply-add equals multiply-then-add), xor butterfly
-//               32..1; mean = sum/D, var = sumsq/D - mean^2, rstd =
-//               1/sqrt(var + 1e-5), every operation correctly rounded on its
-//               own (the reference's block tree and rsqrtf are not
+//   ln_fwd      H = bf16(((x - mean) * rstd) * gamma + beta), one wave per row,
+//               in the canonical order of ln_row.hpp, which the CPU oracle
+//               restates (the reference's block tree and rsqrtf are not
 //               reproducible, this order is). H is therefore bit-identical to
 //               the oracle's, and so are the router logits computed from it.
+//               For routed batches the router computes the same rows itself
+//               (router.hip) and this kernel is not launched.
 //   ln_bwd_rows dS = rstd * ((g - mean(g)) - xh * mean(g * xh)) with g = dH * gamma,
 //               xh = (x - mean) * rstd, one wave per row.
 //   ln_dgb      dgamma = sum_r dH * xh, dbeta = sum_r dH: chunk partials over
@@ -22,10 +19,11 @@
 // the dX scatter instead (pointwise.hip) and only colsum runs from here; the
 // two kernels above are the path for wider rows.
 #include "device_util.hpp"
+#include "ln_row.hpp"
 #include "moe_internal.hpp"
 
 // Every float operation below is rounded on its own: no contraction into
-// fused multiply-adds except the explicit one in row_stats. Division and
+// fused multiply-adds except the explicit one in ln_row.hpp. Division and
 // sqrtf are correctly rounded (hipcc's default for fp32).
 #pragma clang fp contract(off)
 
@@ -37,28 +35,9 @@ __device__ __forceinline__ void row_stats(const uint16_t* x, int d, int lane, fl
     for (int k0 = lane * 8; k0 < d; k0 += 512) {
         float v[8];
         unpack8(*reinterpret_cast<const uint4*>(x + k0), v);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            ls = ls + v[t];
-            lq = __builtin_fmaf(v[t], v[t], lq);
-        }
+        ln_accumulate(v, ls, lq);
     }
-    ls += xor_lane<32>(ls);
-    lq += xor_lane<32>(lq);
-    ls += xor_lane<16>(ls);
-    lq += xor_lane<16>(lq);
-    ls += xor_lane<8>(ls);
-    lq += xor_lane<8>(lq);
-    ls += xor_lane<4>(ls);
-    lq += xor_lane<4>(lq);
-    ls += xor_lane<2>(ls);
-    lq += xor_lane<2>(lq);
-    ls += xor_lane<1>(ls);
-    lq += xor_lane<1>(lq);
-    const float D = (float)d;
-    mean = ls / D;
-    const float var = lq / D - mean * mean;
-    rstd = 1.0f / sqrtf(var + 1e-5f);
+    ln_finish(ls, lq, d, mean, rstd);
 }
 
 __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(LayerNormParams p) {
@@ -72,19 +51,7 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(LayerNormParams p) {
     for (int k0 = lane * 8; k0 < d; k0 += 512) {
         float v[8];
         unpack8(*reinterpret_cast<const uint4*>(x + k0), v);
-        const float4 g0 = *reinterpret_cast<const float4*>(p.gamma + k0);
-        const float4 g1 = *reinterpret_cast<const float4*>(p.gamma + k0 + 4);
-        const float4 b0 = *reinterpret_cast<const float4*>(p.beta + k0);
-        const float4 b1 = *reinterpret_cast<const float4*>(p.beta + k0 + 4);
-        const float g[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
-        const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-        float y[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            const float xh = (v[t] - mean) * rstd;
-            y[t] = xh * g[t] + b[t];
-        }
-        *reinterpret_cast<uint4*>(p.H + (int64_t)r * d + k0) = pack8(y);
+        *reinterpret_cast<uint4*>(p.H + (int64_t)r * d + k0) = ln_apply8(v, mean, rstd, p.gamma, p.beta, k0);
     }
     if (lane == 0) {
         p.mean[r] = mean;

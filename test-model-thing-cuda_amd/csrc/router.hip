@@ -11,6 +11,7 @@
 //    permutation is stable (ascending token inside each expert segment)
 //    instead of atomic-order (moe.cu:103-115).
 #include "device_util.hpp"
+#include "ln_row.hpp"
 #include "moe_internal.hpp"
 #include "route_row.hpp"
 
@@ -85,7 +86,12 @@ __device__ __forceinline__ void reduce_scatter_level(float* acc, int lane) {
     }
 }
 
-template <int EP, int NW>
+// NCH > 0: the rows are the block input S and pass through the LayerNorm
+// first (ln_row.hpp, the same arithmetic as ln_fwd_kernel): the wave loads
+// its R rows whole (NCH chunks of 512 elements), writes H and the row
+// statistics, and computes the logits from H as rounded to bf16, as the
+// router would read it back.
+template <int EP, int NW, int NCH = 0>
 __device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t* wl, int row_begin,
                                            int row_end, int* s_cnt,
                                            float (*s_stat)[kMaxExperts + 1], int* s_idx) {
@@ -103,18 +109,49 @@ __device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t
 #pragma unroll
         for (int i = 0; i < R * EP; ++i) acc[i] = 0.0f;
 
-        for (int c = 0; c < nch; ++c) {
-            const int k0 = c * 512 + lane * 8;
-            if (k0 >= d) continue;  // this lane owns no element of the chunk
-            float xf[R][8];
+        uint4 hv[R][NCH > 0 ? NCH : 1];  // LayerNorm: the rows' H pieces
+        if constexpr (NCH > 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    const int row = r0 + r, k0 = c * 512 + lane * 8;
+                    hv[r][c] = make_uint4(0, 0, 0, 0);
+                    if (row < row_end && k0 < d) hv[r][c] = *reinterpret_cast<const uint4*>(p.X + (int64_t)row * d + k0);
+                }
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int row = r0 + r;
-                uint4 xv = make_uint4(0, 0, 0, 0);
-                if (row < row_end)
-                    xv = *reinterpret_cast<const uint4*>(p.X + (int64_t)row * d + k0);
-                unpack8(xv, xf[r]);
+                float ls = 0.0f, lq = 0.0f;
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    if (c * 512 + lane * 8 < d) {
+                        float v[8];
+                        unpack8(hv[r][c], v);
+                        ln_accumulate(v, ls, lq);
+                    }
+                }
+                float mean, rstd;
+                ln_finish(ls, lq, d, mean, rstd);
+#pragma unroll
+                for (int c = 0; c < NCH; ++c) {
+                    const int k0 = c * 512 + lane * 8;
+                    if (k0 < d) {
+                        float v[8];
+                        unpack8(hv[r][c], v);
+                        hv[r][c] = ln_apply8(v, mean, rstd, p.ln_gamma, p.ln_beta, k0);
+                        if (row < row_end) *reinterpret_cast<uint4*>(p.ln_H + (int64_t)row * d + k0) = hv[r][c];
+                    }
+                }
+                if (lane == 0 && row < row_end) {
+                    p.ln_mean[row] = mean;
+                    p.ln_rstd[row] = rstd;
+                }
             }
+        }
+        // Logit partials of chunk c (k0 = c * 512 + 8 * lane < d) from the
+        // rows' elements xf.
+        auto dots = [&](int k0, const float (&xf)[R][8]) {
 #pragma unroll
             for (int e = 0; e < EP; ++e) {
                 if (e < E) {
@@ -126,6 +163,33 @@ __device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t
                         for (int t = 0; t < 8; ++t)
                             acc[r * EP + e] = __builtin_fmaf(xf[r][t], wf[t], acc[r * EP + e]);
                 }
+            }
+        };
+        if constexpr (NCH > 0) {
+#pragma unroll
+            for (int c = 0; c < NCH; ++c) {
+                const int k0 = c * 512 + lane * 8;
+                if (k0 < d) {
+                    float xf[R][8];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) unpack8(hv[r][c], xf[r]);
+                    dots(k0, xf);
+                }
+            }
+        } else {
+            for (int c = 0; c < nch; ++c) {
+                const int k0 = c * 512 + lane * 8;
+                if (k0 >= d) continue;  // this lane owns no element of the chunk
+                float xf[R][8];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int row = r0 + r;
+                    uint4 xv = make_uint4(0, 0, 0, 0);
+                    if (row < row_end)
+                        xv = *reinterpret_cast<const uint4*>(p.X + (int64_t)row * d + k0);
+                    unpack8(xv, xf[r]);
+                }
+                dots(k0, xf);
             }
         }
 
@@ -185,7 +249,8 @@ __device__ __forceinline__ void route_rows(const RouterParams& p, const uint16_t
 // arithmetic and therefore the same bits.
 // NW waves per workgroup share one staged copy of Wr; the block statistics
 // add the waves' sums in wave order.
-template <int EP, bool WLDS, int NW>
+// NCH > 0: the LayerNorm in front of the router is computed here (route_rows).
+template <int EP, bool WLDS, int NW, int NCH>
 __global__ __launch_bounds__(64 * NW) void router_kernel(RouterParams p) {
     extern __shared__ uint4 smem_w[];  // Wr [E][d] bf16 (WLDS)
     __shared__ int s_cnt[kMaxExperts];
@@ -200,7 +265,7 @@ __global__ __launch_bounds__(64 * NW) void router_kernel(RouterParams p) {
     const int row_begin = blockIdx.x * p.rows_per_block;
     const int row_end = min(p.T, row_begin + p.rows_per_block);
     const uint16_t* wl = WLDS ? reinterpret_cast<const uint16_t*>(smem_w) : p.Wr;
-    route_rows<EP, NW>(p, wl, row_begin, row_end, s_cnt, s_stat, nullptr);
+    route_rows<EP, NW, NCH>(p, wl, row_begin, row_end, s_cnt, s_stat, nullptr);
     __syncthreads();
     // Block statistics: waves added in order.
     const int b = blockIdx.x;
@@ -214,15 +279,33 @@ __global__ __launch_bounds__(64 * NW) void router_kernel(RouterParams p) {
     }
 }
 
+// LayerNorm chunks of the fused router: 512-element chunks rounded up to 1, 2
+// or 4; a wave holds R = 64 / EP rows of them in registers (R * NCH <= 16;
+// with 64 expert lanes, whose 64 partials per lane leave less room, NCH <= 2).
+static int router_ln_chunks(int E, int d) {
+    const int nch = (d + 511) / 512;
+    const int c = nch <= 1 ? 1 : nch <= 2 ? 2 : nch <= 4 ? 4 : 0;
+    const bool fits = c > 0 && router_rows_per_wave(E) * c <= 16 && (router_ep(E) < 64 || c <= 2);
+    return fits ? c : 0;
+}
+bool router_ln_fits(int E, int d) { return router_ln_chunks(E, d) > 0; }
+
 hipError_t launch_router(const RouterParams& p, int nblk, hipStream_t s) {
     const bool wlds = router_wr_in_lds(p.E, p.d);
     const size_t lds = wlds ? (size_t)p.E * p.d * 2 : 0;
     const int ep = router_ep(p.E);
+    const int nch = p.ln_H != nullptr ? router_ln_chunks(p.E, p.d) : 0;
+    if (p.ln_H != nullptr && nch == 0) return hipErrorInvalidValue;
     dim3 grid(nblk), block(64 * kRouterWaves);
-#define TMT_ROUTER(EP_)                                                                \
-    case EP_:                                                                         \
-        if (wlds) router_kernel<EP_, true, kRouterWaves><<<grid, block, lds, s>>>(p); \
-        else router_kernel<EP_, false, kRouterWaves><<<grid, block, 0, s>>>(p);       \
+#define TMT_ROUTER_NCH(EP_, NCH_)                                                               \
+    if (wlds) router_kernel<EP_, true, kRouterWaves, NCH_><<<grid, block, lds, s>>>(p);        \
+    else router_kernel<EP_, false, kRouterWaves, NCH_><<<grid, block, 0, s>>>(p);
+#define TMT_ROUTER(EP_)                              \
+    case EP_:                                        \
+        if (nch == 0) { TMT_ROUTER_NCH(EP_, 0) }     \
+        else if (nch == 1) { TMT_ROUTER_NCH(EP_, 1) } \
+        else if (nch == 2) { TMT_ROUTER_NCH(EP_, 2) } \
+        else if constexpr (EP_ > 8 && EP_ < 64) { TMT_ROUTER_NCH(EP_, 4) } \
         break;
     switch (ep) {
         TMT_ROUTER(8)
@@ -232,6 +315,7 @@ hipError_t launch_router(const RouterParams& p, int nblk, hipStream_t s) {
         default: return hipErrorInvalidValue;
     }
 #undef TMT_ROUTER
+#undef TMT_ROUTER_NCH
     return hipGetLastError();
 }
 

@@ -128,6 +128,7 @@ def check_all(g, r, E, h):
     (300, 256, 4, 2, 1024),    # a few 64-row workgroups of the fused dGamma/dBeta partials
     (1237, 384, 8, 2, 256),    # ragged T, d not a multiple of 512
     (520, 1088, 4, 2, 128),    # d > 512: three row passes per lane, the last partial
+    (520, 1088, 16, 4, 128),   # LayerNorm inside the router: 4 chunk slots, the third partial, the fourth empty
     (777, 256, 1, 1, 0),       # reference dense path (experts=1, no router)
     (700, 512, 16, 4, 0),      # reference single-linear experts
     (5, 192, 5, 2, 320),       # decode-sized: fused router, weight-streaming GEMMs
@@ -332,3 +333,32 @@ def test_c3_full_size_layernorm_block(orc):
         err = rel_l2(got[n], ref[n])
         say(f"  {n}: rel-L2 {err:.2e}")
         assert err <= REL_L2, f"{n} rel-L2 {err:.3e}"
+
+
+@pytest.mark.parametrize("T,d,E,norm_launches", [
+    (300, 256, 4, 0),     # routed batch: the router normalises its rows itself
+    (2100, 2048, 12, 0),  # the widest fused row (4 chunks of 512 per lane)
+    (40, 256, 4, 1),      # decode-sized batch: separate LayerNorm launch
+    (300, 2560, 4, 1),    # d > 2048: separate LayerNorm launch
+])
+def test_layernorm_forward_placement(T, d, E, norm_launches):
+    """Which kernel runs the LayerNorm forward: the phase profile counts the
+    separate LayerNorm launches; H and the statistics are checked bit for bit
+    against the oracle by the block tests above for each of these paths."""
+    say(f"layernorm placement T={T} d={d} E={E}: {norm_launches} LayerNorm launch(es)")
+    K, h = 2, 128
+    case = make_case(T, d, E, K, h, seed=T + d)
+    S, gamma, beta = ln_inputs(case["X"], seed=1)
+    m = tmt_moe.MoE(T, d, E, K, h)
+    try:
+        Wr, Wu, Wd = dev(case["Wr"]), dev(case["W_up"]), dev(case["W_down"])
+        Y = torch.zeros(T, d, dtype=torch.bfloat16, device="cuda")
+        m.set_profiling(True)
+        m.profile(reset=True)
+        m.forward_ln(dev(S), torch.from_numpy(gamma).cuda(), torch.from_numpy(beta).cuda(), Wr, Wu, Wd, Y)
+        prof = m.profile(reset=True)
+        m.set_profiling(False)
+        assert prof["norm"][1] == norm_launches
+        assert prof["router"][1] + prof["gemm_up"][1] >= 1
+    finally:
+        m.close()
