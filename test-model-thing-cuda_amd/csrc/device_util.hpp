@@ -17,8 +17,12 @@ __device__ __forceinline__ float bf1(uint16_t v) { return __uint_as_float((uint3
 __device__ __forceinline__ uint16_t f2bf(float f) {
     return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
+// Two values in one v_cvt_pk_bf16_f32 (the same rounding as f2bf on each;
+// converting them one at a time costs two conversions, a shift and an or).
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
 // Unpack 8 bf16 held in a uint4 into fp32.
@@ -46,6 +50,14 @@ __device__ __forceinline__ float silu_fast(float x) { return x * sigmoid_fast(x)
 __device__ __forceinline__ float dsilu_fast(float x) {
     float s = sigmoid_fast(x);
     return s * (1.0f + x * (1.0f - s));
+}
+// Both from one sigmoid: the up GEMM's epilogue writes SiLU(U) for the down
+// GEMM and silu'(U) for the backward (GEMM_DACT multiplies by it), so the
+// exp / reciprocal pair runs once per element of U, in the forward.
+__device__ __forceinline__ void silu_dsilu(float x, float& a, float& da) {
+    const float s = sigmoid_fast(x);
+    a = x * s;
+    da = s * (1.0f + x * (1.0f - s));
 }
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }

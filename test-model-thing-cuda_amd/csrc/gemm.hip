@@ -107,7 +107,8 @@ template <> struct Traits<GEMM_UP> {
 template <> struct Traits<GEMM_DOWN> {
     static constexpr bool group_k = false, a_kc = true, b_kc = true, gather = false, b_fp4 = false;
 };
-// C[slot][n] = (dO[slot] . W_down[e][:, n]) * silu'(U)  B: [K][N]
+// C[slot][n] = (dO[slot] . W_down[e][:, n]) * silu'(U)  B: [K][N]; silu'(U) as the
+// up GEMM wrote it (p.u)
 template <> struct Traits<GEMM_DACT> {
     static constexpr bool group_k = false, a_kc = true, b_kc = false, gather = false, b_fp4 = false;
 };
@@ -744,9 +745,9 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     constexpr int FPP = EPR / 32, PASSES = MI / FPP;  // row fragments per pass, passes
     float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (EPR * WTN);
     const int mbase = wm * WTM, nbase = wn * WTN;
-    // GEMM_DACT: the pre-activations of every pass are requested here, in one
-    // batch, so the tile waits for one memory round trip instead of one per
-    // pass (the mainloop's operand fragments are dead, which leaves room).
+    // GEMM_DACT: silu'(U) of every pass is requested here, in one batch, so
+    // the tile waits for one memory round trip instead of one per pass (the
+    // mainloop's operand fragments are dead, which leaves room).
     constexpr int UPP = KIND == GEMM_DACT ? EPR / RPI : 1;  // U loads per lane and pass
     uint4 uin[KIND == GEMM_DACT ? PASSES : 1][UPP];
     if constexpr (KIND == GEMM_DACT && !Tr::group_k) {
@@ -805,17 +806,22 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
                 const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + (((2 * cl + 1) ^ (rr & (CH - 1))) * 4));
                 float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
                 const int64_t off = (int64_t)(row0 + m) * p.ldc + nt * BN + n;
-                if constexpr (KIND == GEMM_DACT) {
-                    float u[8];
-                    unpack8(uin[pass][k], u);
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) v[t] *= dsilu_fast(u[t]);
-                }
-                st16_nt(C + off, pack8(v));
                 if constexpr (DUAL) {
+                    // U itself is not kept: C = silu'(U) (skipped when C is
+                    // null, for forward-only handles), c2 = SiLU(U)
+                    float a[8], da[8];
 #pragma unroll
-                    for (int t = 0; t < 8; ++t) v[t] = silu_fast(v[t]);
-                    st16_nt(p.c2 + off, pack8(v));
+                    for (int t = 0; t < 8; ++t) silu_dsilu(v[t], a[t], da[t]);
+                    if (C != nullptr) st16_nt(C + off, pack8(da));
+                    st16_nt(p.c2 + off, pack8(a));
+                } else {
+                    if constexpr (KIND == GEMM_DACT) {
+                        float ds[8];
+                        unpack8(uin[pass][k], ds);  // silu'(U) from the up GEMM
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) v[t] *= ds[t];
+                    }
+                    st16_nt(C + off, pack8(v));
                 }
             }
         } else {

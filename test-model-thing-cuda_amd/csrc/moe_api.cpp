@@ -107,7 +107,8 @@ struct tmt_moe {
     float* dpart = nullptr;     // decode GEMM_DOWN: fp32 rows of the two K halves (nullptr: none)
     int resident = 0;           // workgroups the GPU runs at once (one per CU)
     int32_t *idx, *blkcnt, *blkbase, *counts, *offsets, *order, *perm, *slot_of;
-    // activations
+    // activations (U: the single linear's output when hidden = 0, silu'(U)
+    // when hidden > 0)
     uint16_t *U, *Aact, *O, *dO, *dU, *dXg, *Xg;
     // MX handles: activations of the two expert GEMMs as two MXFP6 terms
     uint8_t *xq = nullptr, *xq_scales = nullptr, *aq = nullptr, *aq_scales = nullptr;
@@ -198,7 +199,10 @@ Sizes plan(const tmt_moe_desc* d, tmt_moe* m) {
     size_t o_perm = L.add(TK * 4), o_slot = L.add(TK * 4);
     // MX handles (scaled-MFMA FP4 forward) keep activations in MX6x2 form instead of U / SiLU(U)
     const bool mx = d->weight_format == TMT_MOE_WEIGHTS_MXFP4_MX;
-    size_t o_U = mx ? 0 : L.add(TK * hn * 2);
+    // U: the single linear's output (hidden = 0), else silu'(U) for the
+    // backward; MXFP4 handles are forward-only and keep neither
+    const bool fp4 = d->weight_format != TMT_MOE_WEIGHTS_BF16;
+    size_t o_U = fp4 ? 0 : L.add(TK * hn * 2);
     size_t o_A = h > 0 && !mx ? L.add(TK * h * 2) : 0;
     size_t o_O = h > 0 ? L.add(TK * D * 2) : 0;
     size_t o_H = L.add(T * D * 2), o_mean = L.add(T * 4), o_rstd = L.add(T * 4);
@@ -247,7 +251,7 @@ Sizes plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->resident = resident;
         m->perm = (int32_t*)(a + o_perm);
         m->slot_of = (int32_t*)(a + o_slot);
-        m->U = mx ? nullptr : (uint16_t*)(a + o_U);
+        m->U = fp4 ? nullptr : (uint16_t*)(a + o_U);
         m->Aact = h > 0 && !mx ? (uint16_t*)(a + o_A) : nullptr;
         m->xq = mx ? (uint8_t*)(w + o_xq) : nullptr;
         m->xq_scales = mx ? (uint8_t*)(w + o_xqs) : nullptr;
@@ -869,7 +873,7 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
         GemmParams up{};
         up.offsets = m->offsets; up.order = m->order; up.perm = m->perm; up.E = E;
         up.N = h; up.K = d; up.slots = T * K;
-        up.a = X; up.lda = d; up.c = m->U; up.ldc = h; up.c2 = m->Aact;
+        up.a = X; up.lda = d; up.c = nullptr; up.ldc = h; up.c2 = m->Aact;  // no backward: silu'(U) not kept
         for (int e = 0; e < E; ++e) { up.wq[e] = W_up[e]; up.wsc[e] = W_up_scale[e]; }
         LAUNCH(TMT_MOE_PH_GEMM_UP, launch_gemm(GEMM_UP_FP4, true, up, s));
         GemmParams dn{};

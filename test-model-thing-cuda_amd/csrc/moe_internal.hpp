@@ -118,8 +118,8 @@ struct GemmParams {
     const uint16_t* a; int64_t lda;   // activation operand
     const uint16_t* b; int64_t ldb;   // second activation operand (dW GEMMs)
     void* c; int64_t ldc;             // output (activation GEMMs)
-    uint16_t* c2;                     // SiLU copy (GEMM_UP with hidden > 0)
-    const uint16_t* u;                // pre-activation for GEMM_DACT
+    uint16_t* c2;                     // GEMM_UP with hidden > 0: SiLU(U) (c then gets silu'(U))
+    const uint16_t* u;                // GEMM_DACT: silu'(U) as the up GEMM wrote it
     const uint16_t* w[kMaxExperts];   // per-expert weights (activation GEMMs)
     float* dw[kMaxExperts];           // per-expert fp32 outputs (dW GEMMs)
     const uint8_t* wq[kMaxExperts];   // MXFP4 weights: packed e2m1 [N][K/2] (low nibble = even k)

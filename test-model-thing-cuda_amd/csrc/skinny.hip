@@ -55,6 +55,21 @@ __device__ __forceinline__ uint4 ld16_buf(__amdgpu_buffer_rsrc_t r, int off) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
+// One output element: the up GEMM with hidden > 0 (DUAL) writes silu'(U) to C
+// and SiLU(U) to c2 (U itself is not kept: the backward only needs silu'(U));
+// otherwise C = v.
+template <bool DUAL>
+__device__ __forceinline__ void store_up(uint16_t* C, uint16_t* c2, int64_t off, float v) {
+    if constexpr (DUAL) {
+        float a, da;
+        silu_dsilu(v, a, da);
+        C[off] = f2bf(da);
+        c2[off] = f2bf(a);
+    } else {
+        C[off] = f2bf(v);
+    }
+}
+
 // Kernel arguments are brought into registers before the first data load:
 // a scalar argument load that the compiler sinks below the table loads
 // would add a round trip to the workgroup's critical path.
@@ -230,8 +245,7 @@ __global__ __launch_bounds__(kThreads) void skinny_gemm_kernel(GemmParams p, int
         v += red[2][rb][src_lane][r];
         v += red[3][rb][src_lane][r];
         const int64_t off = (int64_t)(row0 + row) * p.ldc + n0 + n;
-        C[off] = f2bf(v);
-        if constexpr (DUAL) p.c2[off] = f2bf(silu_fast(v));
+        store_up<DUAL>(C, p.c2, off, v);
     }
 }
 
@@ -357,8 +371,7 @@ __global__ __launch_bounds__(1024) void skinny_chunk_kernel(GemmParams p, int ne
         float v = red[(rbc * nw) * 64 + sl][r];
         for (int w2 = 1; w2 < nw; ++w2) v += red[(rbc * nw + w2) * 64 + sl][r];
         const int64_t off = (int64_t)(row0 + row) * p.ldc + (tile0 + c) * 16 + n;
-        C[off] = f2bf(v);
-        if constexpr (DUAL) p.c2[off] = f2bf(silu_fast(v));
+        store_up<DUAL>(C, p.c2, off, v);
     }
 }
 
@@ -481,8 +494,14 @@ __global__ __launch_bounds__(64 * NWMAX) void skinny_stream_kernel(GemmParams p,
             if constexpr (KS == 2) {
                 reinterpret_cast<float*>(st)[row * 16 + n] = v;
             } else {
-                reinterpret_cast<uint16_t*>(st)[row * 16 + n] = f2bf(v);
-                if constexpr (DUAL) reinterpret_cast<uint16_t*>(st)[16 * RB * 16 + row * 16 + n] = f2bf(silu_fast(v));
+                if constexpr (DUAL) {
+                    float a, da;
+                    silu_dsilu(v, a, da);
+                    reinterpret_cast<uint16_t*>(st)[row * 16 + n] = f2bf(da);
+                    reinterpret_cast<uint16_t*>(st)[16 * RB * 16 + row * 16 + n] = f2bf(a);
+                } else {
+                    reinterpret_cast<uint16_t*>(st)[row * 16 + n] = f2bf(v);
+                }
             }
         }
         __syncthreads();
