@@ -241,8 +241,23 @@ constexpr bool split_ring() {
     return BK == 64 && BN == 256 && NWM == 2 && !Traits<KIND>::group_k;
 }
 
+// Persistent kernels: the split-ring GEMMs (every tile of a launch has the
+// same K, so a static schedule stays balanced) run one workgroup per CU that
+// walks the tiles vb = blockIdx.x, blockIdx.x + gridDim.x, ... . A tile's
+// first operand loads then go out while the previous tile's epilogue stores
+// drain, and the per-workgroup launch and set-up cost is paid once per CU
+// instead of once per tile. vb keeps the launch-order meaning of blockIdx.x
+// (gridDim.x is a multiple of 8 whenever it is below the tile count, so vb
+// runs on XCD vb % 8 as the tile map assumes).
+template <int KIND, int BK, int BN, int NWM>
+constexpr bool persistent_tiles() {
+    return split_ring<KIND, BK, BN, NWM>();
+}
+
+// One output tile (or split-K part) of the grouped GEMM: launch-order block
+// index vb; returns without touching memory when vb maps to no tile.
 template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2>
-__global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
+__device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int vb) {
     using Tr = Traits<KIND>;
     using Gm = Geo<BK_, NST, BN_, NWM_>;
     constexpr int BK = Gm::BK, NSTAGE = Gm::NSTAGE, BN = Gm::BN, WTN = Gm::WTN, NJ = Gm::NJ;
@@ -281,7 +296,7 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     // that the XCD's L2 serves each operand slice to several workgroups.
     // Consecutive groups go to different XCDs, which spreads the long tiles
     // of the weight-gradient GEMMs (experts in descending-count order).
-    const int lid = ((((int)blockIdx.x >> 8) << 3) + ((int)blockIdx.x & 7)) * 32 + (((int)blockIdx.x >> 3) & 31);
+    const int lid = (((vb >> 8) << 3) + (vb & 7)) * 32 + ((vb >> 3) & 31);
     const int G = lid >> 5, gi = lid & 31;
     const int gn = min(ntn, 8), gm = 32 / gn;
     const int ngn = (ntn + gn - 1) / gn;
@@ -298,8 +313,8 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
         if constexpr (kSplitK) {
             if (p.part != nullptr) sp = split_plan<BK>(p, ntn, act_mtiles(p));
         }
-        if (sp.S >= 2 && (int)blockIdx.x >= sp.F) {
-            const int u = (int)blockIdx.x - sp.F;
+        if (sp.S >= 2 && vb >= sp.F) {
+            const int u = vb - sp.F;
             if (u >= sp.R * sp.S) return;
             const int j = u / sp.S, q = u - j * sp.S;
             mt = sp.cut + j / ntn;
@@ -329,7 +344,7 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
         //    16r + x and 16r + 15 - x). With 32-tile groups the XCD holding
         //    the heaviest expert's group could not be balanced.
         constexpr int GSZ = BN == 256 ? 16 : 32;
-        const int rnd = (int)blockIdx.x >> 8, xcd = (int)blockIdx.x & 7, sub = ((int)blockIdx.x >> 3) & 31;
+        const int rnd = vb >> 8, xcd = vb & 7, sub = (vb >> 3) & 31;
         const int Gs = GSZ == 16 ? 16 * rnd + (sub < 16 ? xcd : 15 - xcd) : 8 * rnd + ((rnd & 1) ? 7 - xcd : xcd);
         const int gk = sub & (GSZ - 1), gnk = min(ntn, 8), gmk = GSZ / gnk, ngnk = (ntn + gnk - 1) / gnk;
         if (gk >= gmk * gnk) return;
@@ -841,6 +856,16 @@ __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm
     }
 }
 
+template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2>
+__global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
+    if constexpr (persistent_tiles<KIND, BK_, BN_, NWM_>()) {
+        for (int vb = blockIdx.x; vb < p.vblocks; vb += gridDim.x)
+            grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_>(p, vb);
+    } else {
+        grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_>(p, blockIdx.x);
+    }
+}
+
 // The split-K tail's second pass: tail tile j is the sum of its S partials
 // in part order, rounded once to bf16. Work items are (tile, 8-row slab);
 // thread t adds 8 columns of one row.
@@ -895,21 +920,34 @@ struct Ring {
     static constexpr int NST = split ? 3 : (BN == 256 ? 4 : 3);
 };
 
+// grid: the launch-order blocks of the tile map. Persistent kinds run
+// min(grid, CUs rounded down to a multiple of 8) workgroups over them.
 template <int KIND, bool DUAL, int BN, int NWM = 2>
 hipError_t launch_kind(const GemmParams& p, unsigned grid, hipStream_t s) {
     using R = Ring<KIND, BN>;
-    grouped_gemm_kernel<KIND, DUAL, R::BK, R::NST, BN, NWM><<<grid, 128 * NWM, 0, s>>>(p);
+    GemmParams q = p;
+    q.vblocks = (int)grid;
+    unsigned g = grid;
+    if constexpr (persistent_tiles<KIND, R::BK, BN, NWM>()) {
+        const unsigned cus = (unsigned)(cu_count() / 8 * 8);
+        if (cus >= 8 && g > cus) g = cus;
+    }
+    grouped_gemm_kernel<KIND, DUAL, R::BK, R::NST, BN, NWM><<<g, 128 * NWM, 0, s>>>(q);
     return hipGetLastError();
 }
 
 // Tile width per GEMM kind (BN 128 = two workgroups per CU). Measured in the
-// c3 step: UP, DOWN and DX run fastest on 256-column tiles with split rings
-// (UP 1.31 -> 1.26 ms against two 128-column workgroups per CU); DACT, whose
-// epilogue reads a U tile, keeps two 128-column workgroups per CU (1.33
-// against 1.39 ms). The weight-gradient GEMMs run 256-column tiles in
-// balanced 16-tile groups (4-6% faster than two 128-column workgroups).
+// c3 step: every GEMM runs fastest on 256-column tiles (UP, DOWN, DX and DACT
+// on split rings; UP 1.26 against 1.29 ms with two 128-column workgroups per
+// CU). DACT moved to 256 columns once its epilogue no longer evaluated
+// silu'(U) itself (1.22 against 1.24 ms, and the weight-gradient GEMMs after
+// it 0.02-0.04 ms faster); while it did, the co-resident second workgroup of
+// the 128-column tiles covered that VALU work and won. The weight-gradient
+// GEMMs run 256-column tiles in balanced 16-tile groups (4-6% faster than two
+// 128-column workgroups).
 int gemm_tile_n(GemmKind kind) {
-    return kind == GEMM_DACT ? 128 : 256;
+    (void)kind;
+    return 256;
 }
 
 hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn, hipStream_t s) {

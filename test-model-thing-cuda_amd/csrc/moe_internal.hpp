@@ -136,6 +136,9 @@ struct GemmParams {
     // wrote only the picks; workgroup (e, s) takes expert e's rows straight
     // from the [T][topk] pick table in idx (the grid is indexed by expert).
     int self_dispatch;
+    // Set by the launcher: launch-order blocks of the tile map (persistent
+    // grouped GEMMs loop over them).
+    int vblocks;
 };
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s);
 // Rows of an activation-GEMM tile, and the fp32 partial buffer the split-K
