@@ -795,7 +795,9 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
         }
         __syncthreads();
         if (kSplitK && part_unit >= 0) {
-            // split-K part: the fp32 partial tile [BM][BN], rows < mlim
+            // split-K part: the fp32 partial tile [BM][BN], rows < mlim, with
+            // plain stores (split_fixup_kernel reads it right after, from
+            // the caches; non-temporal stores measured 0.015 ms slower per GEMM)
             float* C = p.part + (int64_t)part_unit * BM * BN;
             const int cl = lane % FLPR;
 #pragma unroll 4
@@ -804,7 +806,7 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
                 const int n = nbase + cl * 4;
                 if (m >= mlim || n >= nlim) continue;
                 const f32x4 v = *reinterpret_cast<const f32x4*>(stage_f + rr * WTN + ((cl ^ (rr & (CH - 1))) * 4));
-                st16_nt(C + (int64_t)m * BN + n, v);
+                *reinterpret_cast<f32x4*>(C + (int64_t)m * BN + n) = v;
             }
         } else if constexpr (!Tr::group_k) {
             // LPR lanes per row (8 bf16 each), RPI rows per instruction
@@ -991,7 +993,8 @@ hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn,
                                            : launch_kind<GEMM_DX, false, 256>(p, g, s);
         if (err != hipSuccess) return err;
         static_assert(Ring<GEMM_DOWN, 256>::BK == Ring<GEMM_DX, 256>::BK, "one split plan for DOWN and DX");
-        split_fixup_kernel<Ring<GEMM_DOWN, 256>::BK, 256><<<p.resident, 256, 0, s>>>(p);
+        // 4 workgroups per CU: the (tile, 8-row slab) items are short and latency-bound
+        split_fixup_kernel<Ring<GEMM_DOWN, 256>::BK, 256><<<p.resident * 4, 256, 0, s>>>(p);
         return hipGetLastError();
     }
     switch (kind) {
