@@ -59,7 +59,8 @@ enum { TMT_MOE_WEIGHTS_BF16 = 0, TMT_MOE_WEIGHTS_MXFP4 = 1, TMT_MOE_WEIGHTS_MXFP
 
 typedef struct tmt_moe_desc {
     int32_t max_tokens;     /* T_max: largest T a call may pass */
-    int32_t d;              /* model width (multiple of 64) */
+    int32_t d;              /* model width, a multiple of 64 (TMT's config.h:46-52
+                               accepts any dim; other widths fail with EINVAL) */
     int32_t experts;        /* E, 1..64 */
     int32_t topk;           /* K, 1..min(E, 8) */
     int32_t hidden;         /* h (multiple of 64), or 0 for reference experts */
