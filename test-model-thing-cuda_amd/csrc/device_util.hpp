@@ -54,10 +54,13 @@ __device__ __forceinline__ float dsilu_fast(float x) {
 // Both from one sigmoid: the up GEMM's epilogue writes SiLU(U) for the down
 // GEMM and silu'(U) for the backward (GEMM_DACT multiplies by it), so the
 // exp / reciprocal pair runs once per element of U, in the forward.
+// silu'(x) = s(1 + x(1 - s)) = s + a(1 - s) with a = x s: one subtraction and
+// one fused multiply-add (the up GEMM's epilogue is bound by these VALU
+// instructions).
 __device__ __forceinline__ void silu_dsilu(float x, float& a, float& da) {
     const float s = sigmoid_fast(x);
     a = x * s;
-    da = s * (1.0f + x * (1.0f - s));
+    da = __builtin_fmaf(a, 1.0f - s, s);
 }
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }

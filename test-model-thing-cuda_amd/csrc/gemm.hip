@@ -813,6 +813,10 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
             uint16_t* C = reinterpret_cast<uint16_t*>(p.c);
             const int cl = lane % LPR;
             const int n = nbase + cl * 8;
+            // element offset of the lane's first row in this pass, advanced by
+            // RPI rows per store (no 64-bit multiply per store)
+            const int64_t off0 = (int64_t)(row0 + mbase + pass * EPR + lane / LPR) * p.ldc + nt * BN + n;
+            const int64_t rstep = (int64_t)RPI * p.ldc;
 #pragma unroll
             for (int k = 0; k < EPR / RPI; ++k) {
                 const int rr = lane / LPR + RPI * k;
@@ -822,7 +826,7 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
                 const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + (((2 * cl) ^ (rr & (CH - 1))) * 4));
                 const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + (((2 * cl + 1) ^ (rr & (CH - 1))) * 4));
                 float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                const int64_t off = (int64_t)(row0 + m) * p.ldc + nt * BN + n;
+                const int64_t off = off0 + k * rstep;
                 if constexpr (DUAL) {
                     // U itself is not kept: C = silu'(U) (skipped when C is
                     // null, for forward-only handles), c2 = SiLU(U)
