@@ -150,6 +150,7 @@ def test_c1_backward_against_oracle(orc):
     (300, 512, 64, 8, 128),    # widest router (64 experts), top-8
     (500, 1024, 32, 4, 256),   # the c5 router shape
     (129, 128, 3, 3, 128),     # E == K, odd expert count
+    (300, 64, 4, 2, 192),      # d = 64: one K = 64 tile in UP and DACT (the split ring's clamped reloads only)
     (333, 192, 5, 2, 320),     # d and h not multiples of the 256-wide GEMM tile
     (6, 256, 8, 2, 512),       # decode-sized: skinny expert GEMMs forward, tiled GEMMs backward
     (8, 1024, 16, 4, 4096),    # c3 weights at T = 8 (persistent skinny forward), forward + backward
