@@ -366,12 +366,12 @@ bool ln_in_router(int T, int E, int d) { return E > 1 && T > kSmallRouteTokens &
 int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* Wr, const float* bias,
           bool picks_only = false, const LnFuse* ln = nullptr) {
     const int E = m->desc.experts, K = m->desc.topk, d = m->desc.d;
+    if (ln && !ln_in_router(T, E, d)) return fail(TMT_MOE_EINVAL, "internal: LayerNorm not fusable into this router");
     if (E == 1) {
         LAUNCH(TMT_MOE_PH_PERMUTE, launch_dense_dispatch(T, m->perm, m->slot_of, m->gate, m->counts,
                                                         m->offsets, m->order, m->stats, s));
         return TMT_MOE_OK;
     }
-    if (ln && !ln_in_router(T, E, d)) return fail(TMT_MOE_EINVAL, "internal: LayerNorm not fusable into this router");
     if (T >= 1 && T <= kSmallRouteTokens) {
         const Route1 r = small_route_params(m, T, X, Wr, bias);
         LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(r.rp, r.sp, r.pp, picks_only ? nullptr : m->ticket, s));
