@@ -723,6 +723,190 @@ __global__ __launch_bounds__(kThreads) void scatter_rows_kernel(ScatterParams p,
         }
     }
 }
+// LayerNorm variant with two rows per wave in flight (rows r and r + 4 of
+// the wave's stride; K and the chunk count are template arguments so that
+// both rows' loads are issued unconditionally): each staged Wr chunk is
+// unpacked once for the two rows. Per row the arithmetic is scatter_kernel's
+// (picks j ascending, then experts e ascending; dgamma / dbeta partials over
+// the wave's rows in ascending order), so the results are bit-identical.
+template <int K, int NI, bool WLDS>
+__global__ __launch_bounds__(kThreads) void scatter_ln2_kernel(ScatterParams p, int rows_per_block) {
+    extern __shared__ uint4 smem_w[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d = p.d, E = p.E;
+    const int rbeg = blockIdx.x * rows_per_block;
+    const int rend = min(p.T, rbeg + rows_per_block);
+    float* s_dl = reinterpret_cast<float*>(smem_w + (WLDS ? E * d / 8 : 0));  // [rows_per_block][E]
+    const bool red_on_wr = WLDS && E >= kRedOnWrExperts;
+    float* s_red = red_on_wr ? reinterpret_cast<float*>(smem_w) : s_dl + rows_per_block * E;
+    if (WLDS) {
+        const uint4* src = reinterpret_cast<const uint4*>(p.Wr);
+        const int nvec = E * d / 8;
+        for (int i0 = threadIdx.x; i0 < nvec; i0 += 8 * kThreads) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = src[min(i0 + u * kThreads, nvec - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (i0 + u * kThreads < nvec) smem_w[i0 + u * kThreads] = v[u];
+        }
+    }
+    {
+        const int ndl = (rend - rbeg) * E;
+        for (int i = threadIdx.x; i < ndl; i += kThreads) s_dl[i] = p.dlogits[(int64_t)rbeg * E + i];
+    }
+    __syncthreads();
+    const uint16_t* wl = WLDS ? reinterpret_cast<const uint16_t*>(smem_w) : p.Wr;
+
+    float gam[NI][8], pg[NI][8], pb[NI][8];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int c0 = i * 512 + lane * 8;
+        f32x4 g0 = f32x4{0.f, 0.f, 0.f, 0.f}, g1 = g0;
+        if (c0 < d) {
+            g0 = *reinterpret_cast<const f32x4*>(p.ln_gamma + c0);
+            g1 = *reinterpret_cast<const f32x4*>(p.ln_gamma + c0 + 4);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            gam[i][t] = g0[t];
+            gam[i][t + 4] = g1[t];
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) pg[i][t] = pb[i][t] = 0.0f;
+    }
+
+    for (int r = rbeg + wave; r < rend; r += 8) {
+        const bool two = r + 4 < rend;  // wave-uniform
+        int row[2], pos[2][K];
+        row[0] = r;
+        row[1] = two ? r + 4 : r;  // clamped: the second row is loaded but not used
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int j = 0; j < K; ++j) pos[q][j] = p.slot_of[(int64_t)row[q] * K + j];
+        float mean[2], rstd[2];
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            mean[q] = p.ln_mean[row[q]];
+            rstd[q] = p.ln_rstd[row[q]];
+        }
+        float hv[2][NI][8], xs[2][NI][8];
+        float s1[2] = {0.0f, 0.0f}, s2[2] = {0.0f, 0.0f};
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int c0 = i * 512 + lane * 8;
+            if (c0 < d) {
+                uint4 xv[2][K], sv[2];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    sv[q] = *reinterpret_cast<const uint4*>(p.ln_S + (int64_t)row[q] * d + c0);
+#pragma unroll
+                    for (int j = 0; j < K; ++j) xv[q][j] = *reinterpret_cast<const uint4*>(p.dXg + (int64_t)pos[q][j] * d + c0);
+                }
+                float acc[2][8];
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) acc[q][t] = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < K; ++j) {
+                        float v[8];
+                        unpack8(xv[q][j], v);
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) acc[q][t] += v[t];
+                    }
+                }
+                const float* dl0 = s_dl + (row[0] - rbeg) * E;
+                const float* dl1 = s_dl + (row[1] - rbeg) * E;
+                for (int e = 0; e < E; ++e) {
+                    const float g0 = dl0[e], g1 = dl1[e];
+                    float w[8];
+                    unpack8(*reinterpret_cast<const uint4*>(wl + e * d + c0), w);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        acc[0][t] += g0 * w[t];
+                        acc[1][t] += g1 * w[t];
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 2; ++q) {
+                    unpack8(pack8(acc[q]), hv[q][i]);
+                    unpack8(sv[q], xs[q][i]);
+                    if (q == 0 || two) {
+#pragma unroll
+                        for (int t = 0; t < 8; ++t) {
+                            const float g = hv[q][i][t] * gam[i][t];
+                            const float xh = (xs[q][i][t] - mean[q]) * rstd[q];
+                            s1[q] += g;
+                            s2[q] += g * xh;
+                            pg[i][t] += hv[q][i][t] * xh;
+                            pb[i][t] += hv[q][i][t];
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            if (q == 1 && !two) break;  // wave-uniform
+            const float a = wave_sum(s1[q]) / (float)d, b = wave_sum(s2[q]) / (float)d;
+#pragma unroll
+            for (int i = 0; i < NI; ++i) {
+                const int c0 = i * 512 + lane * 8;
+                if (c0 < d) {
+                    float out[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const float g = hv[q][i][t] * gam[i][t];
+                        const float xh = (xs[q][i][t] - mean[q]) * rstd[q];
+                        out[t] = rstd[q] * ((g - a) - xh * b);
+                    }
+                    *reinterpret_cast<uint4*>(p.ln_dS + (int64_t)row[q] * d + c0) = pack8(out);
+                }
+            }
+        }
+    }
+
+    if (red_on_wr) __syncthreads();  // Wr reads done before it is overwritten
+    if (wave > 0) {
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int c0 = i * 512 + lane * 8;
+            if (c0 < d) {
+                float* dg = s_red + (int64_t)((wave - 1) * 2) * d + c0;
+                float* db = dg + d;
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    dg[t] = pg[i][t];
+                    db[t] = pb[i][t];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float* outg = p.ln_partial + (int64_t)blockIdx.x * 2 * d;
+        float* outb = outg + d;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            const int c0 = i * 512 + lane * 8;
+            if (c0 < d) {
+                float g[8], b[8];
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    g[t] = ((pg[i][t] + s_red[c0 + t]) + s_red[2 * d + c0 + t]) + s_red[4 * d + c0 + t];
+                    b[t] = ((pb[i][t] + s_red[d + c0 + t]) + s_red[3 * d + c0 + t]) + s_red[5 * d + c0 + t];
+                }
+                *reinterpret_cast<f32x4*>(outg + c0) = f32x4{g[0], g[1], g[2], g[3]};
+                *reinterpret_cast<f32x4*>(outg + c0 + 4) = f32x4{g[4], g[5], g[6], g[7]};
+                *reinterpret_cast<f32x4*>(outb + c0) = f32x4{b[0], b[1], b[2], b[3]};
+                *reinterpret_cast<f32x4*>(outb + c0 + 4) = f32x4{b[4], b[5], b[6], b[7]};
+            }
+        }
+    }
+}
+
 }  // namespace
 
 int scatter_blocks(int T) {
@@ -808,6 +992,19 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
         return hipGetLastError();
     }
     if (!router) return launch_scatter_ni<false, false>(p, ni, rows, lds, s);
+    if (p.K <= 4 && ni <= 2) {
+        // two rows per wave in flight (scatter_ln2_kernel)
+        const int grid = (p.T + rows - 1) / rows;
+#define TMT_LN2(KK, NN)                                                                                    \
+    if (p.K == KK && ni == NN) {                                                                          \
+        if (wlds) scatter_ln2_kernel<KK, NN, true><<<grid, kThreads, lds, s>>>(p, rows);                   \
+        else scatter_ln2_kernel<KK, NN, false><<<grid, kThreads, lds, s>>>(p, rows);                       \
+        return hipGetLastError();                                                                         \
+    }
+        TMT_LN2(1, 1) TMT_LN2(2, 1) TMT_LN2(3, 1) TMT_LN2(4, 1)
+        TMT_LN2(1, 2) TMT_LN2(2, 2) TMT_LN2(3, 2) TMT_LN2(4, 2)
+#undef TMT_LN2
+    }
     return wlds ? launch_scatter_ni<true, true>(p, ni, rows, lds, s)
                 : launch_scatter_ni<true, false>(p, ni, rows, lds, s);
 }
