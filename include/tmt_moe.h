@@ -17,8 +17,18 @@
  * Layout: all matrices row-major, weights [out][in] like nn.Linear
  * (linalg.cu:1-8). bf16 values are raw uint16 bit patterns. Per-expert
  * weights are passed as host arrays of E device pointers, the reference's
- * `bf16** Wexp` convention (moe.cu:374). All device pointers must be 16-byte
- * aligned. d and hidden must be multiples of 64.
+ * `bf16** Wexp` convention (moe.cu:374).
+ *
+ * Widths: any d >= 1 and hidden >= 0, as TMT's validate_cfg
+ * (config.h:46-52). When d and hidden are multiples of 64 the kernels read
+ * the caller's tensors directly and every device pointer must be 16-byte
+ * aligned. Other widths (TMT's own tests run dim 16 and 32) run on
+ * zero-padded copies at the widths rounded up to 64, kept in the handle's
+ * shared workspace: each call copies its operands in and its results out
+ * (a few extra small kernels), and pointers need only their natural
+ * alignment (2 bytes for bf16, 4 for fp32). Zero columns add exact zeros, so
+ * the routing is the same as at the caller's width. The MXFP4 formats keep
+ * d and hidden multiples of 64.
  *
  * Every function returns TMT_MOE_OK (0) or a negative error code and never
  * exits the process; tmt_moe_last_error() gives a thread-local message.
@@ -59,11 +69,10 @@ enum { TMT_MOE_WEIGHTS_BF16 = 0, TMT_MOE_WEIGHTS_MXFP4 = 1, TMT_MOE_WEIGHTS_MXFP
 
 typedef struct tmt_moe_desc {
     int32_t max_tokens;     /* T_max: largest T a call may pass */
-    int32_t d;              /* model width, a multiple of 64 (TMT's config.h:46-52
-                               accepts any dim; other widths fail with EINVAL) */
+    int32_t d;              /* model width, >= 1 (TMT's config.h:46-52) */
     int32_t experts;        /* E, 1..64 */
     int32_t topk;           /* K, 1..min(E, 8) */
-    int32_t hidden;         /* h (multiple of 64), or 0 for reference experts */
+    int32_t hidden;         /* h >= 1, or 0 for reference experts */
     int32_t weight_format;  /* TMT_MOE_WEIGHTS_* */
 } tmt_moe_desc;
 
@@ -231,9 +240,10 @@ int tmt_moe_read_routing(tmt_moe* moe, void* stream, float* logits,
  *   backward: from the bf16 gradient dH at H: dS [T][d] bf16, dGamma, dBeta
  *             [d] fp32 (overwritten, fixed-order sums over rows).
  * The backward needs `workspace` of at least tmt_moe_layernorm_workspace_size
- * bytes (device memory, 256-byte aligned); no call allocates. d must be a
- * multiple of 64, pointers 16-byte aligned. Calls that share a workspace
- * must be ordered by the caller.
+ * bytes (device memory, 256-byte aligned); no call allocates. Any d >= 1
+ * (rows whose width is not a multiple of 8 are read and written element by
+ * element, in the same summation order); pointers 16-byte aligned. Calls
+ * that share a workspace must be ordered by the caller.
  */
 int tmt_moe_layernorm_workspace_size(int32_t T, int32_t d, size_t* bytes);
 int tmt_moe_layernorm_forward(void* stream, int32_t T, int32_t d, const uint16_t* S,
@@ -247,15 +257,18 @@ int tmt_moe_layernorm_backward(void* stream, int32_t T, int32_t d, const uint16_
 /*
  * tmt_moe_layernorm_backward without the workspace argument, for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
- * serving loops, harnesses that forbid hipMalloc). No reference counterpart
- * (the reference's layernorm_bwd allocates nothing but also keeps no
- * workspace, norm.cu:102-106). The scratch is a 4 MiB device array inside
- * the library (one per GPU, held until the process ends): shapes whose
- * workspace (tmt_moe_layernorm_workspace_size) exceeds 4 MiB are rejected
- * with TMT_MOE_EINVAL, e.g. T = 32768 at d = 1024 uses 0.53 MiB. No call
+ * serving loops, harnesses that forbid hipMalloc). No reference counterpart.
+ * The scratch is a 4 MiB device array inside the library (one per GPU, held
+ * until the process ends): shapes whose workspace
+ * (tmt_moe_layernorm_workspace_size) exceeds 4 MiB are rejected with
+ * TMT_MOE_EINVAL, e.g. T = 32768 at d = 1024 uses 0.53 MiB. No call
  * allocates. Every call on one GPU uses that GPU's same scratch: calls that
  * overlap on one GPU (different streams, or threads, without ordering) race.
- * Same results, bit for bit, as tmt_moe_layernorm_backward.
+ * The first call on a device looks the scratch's address up and keeps it for
+ * the process: make that first call outside a graph capture, and do not use
+ * the entry point after hipDeviceReset. Later calls may be captured (the
+ * launches are plain kernels, no memset nodes). Same results, bit for bit,
+ * as tmt_moe_layernorm_backward.
  */
 int tmt_moe_layernorm_backward_noalloc(void* stream, int32_t T, int32_t d, const uint16_t* S,
                                        const uint16_t* dH, const float* gamma, const float* mean,

@@ -53,6 +53,7 @@ int fail(int code, const char* fmt, ...) {
     } while (0)
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned_to(const void* p, unsigned a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1u)) == 0; }
 
 // Device address of `scratch` on the current device, looked up on the first
 // call made with that device current and kept per device.
@@ -91,7 +92,20 @@ struct Layout {
 }  // namespace
 
 struct tmt_moe {
-    tmt_moe_desc desc;
+    tmt_moe_desc desc;  // the widths the kernels run at (d and hidden rounded up to 64)
+    tmt_moe_desc user;  // the caller's descriptor
+    // d or hidden not a multiple of 64: every call copies its operands into
+    // zero-padded internal buffers of the rounded-up widths and copies the
+    // results back (zero rows and columns contribute nothing to any product,
+    // so the routing and every result on the caller's columns are unchanged)
+    bool padded = false;
+    unsigned align_bf16 = 16, align_f32 = 16;  // pointer alignment the checks require
+    uint16_t *px = nullptr, *py = nullptr, *pdy = nullptr, *pdx = nullptr, *pwr = nullptr;
+    float* pdwr = nullptr;
+    uint16_t* pwu[kMaxExperts] = {};
+    uint16_t* pwd[kMaxExperts] = {};
+    float* pdwu[kMaxExperts] = {};
+    float* pdwd[kMaxExperts] = {};
     int hn = 0;        // width of the first expert GEMM (h, or d for h == 0)
     int nblk_max = 0;  // router blocks at the largest T
     int device = 0;
@@ -128,16 +142,35 @@ struct tmt_moe {
 
 namespace {
 
+int round64(int v) { return (v + 63) / 64 * 64; }
+
+// The widths the kernels run at: bf16 handles round d and hidden up to
+// multiples of 64 (the GEMM tiles' K step and the router's lane layout);
+// MXFP4 handles take them as given (validate_desc requires multiples of 64).
+tmt_moe_desc internal_desc(const tmt_moe_desc& u) {
+    tmt_moe_desc d = u;
+    if (u.weight_format == TMT_MOE_WEIGHTS_BF16) {
+        d.d = round64(u.d);
+        d.hidden = u.hidden > 0 ? round64(u.hidden) : 0;
+    }
+    return d;
+}
+bool is_padded(const tmt_moe_desc& u) {
+    const tmt_moe_desc d = internal_desc(u);
+    return d.d != u.d || d.hidden != u.hidden;
+}
+
 int validate_desc(const tmt_moe_desc* d) {
     if (!d) return fail(TMT_MOE_EINVAL, "descriptor is NULL");
     if (d->max_tokens < 1) return fail(TMT_MOE_EINVAL, "max_tokens must be >= 1");
-    if (d->d < 64 || d->d % 64 != 0) return fail(TMT_MOE_EINVAL, "d=%d must be a positive multiple of 64", d->d);
+    // any width, as TMT's validate_cfg (config.h:46-52): d >= 1
+    if (d->d < 1 || d->d > (1 << 20)) return fail(TMT_MOE_EINVAL, "d=%d must be in [1, 2^20]", d->d);
     if (d->experts < 1 || d->experts > kMaxExperts)
         return fail(TMT_MOE_EINVAL, "experts=%d must be in [1, %d]", d->experts, kMaxExperts);
     if (d->topk < 1 || d->topk > d->experts || d->topk > kMaxTopK)
         return fail(TMT_MOE_EINVAL, "require 1 <= topk <= min(experts, %d) (topk=%d)", kMaxTopK, d->topk);
-    if (d->hidden < 0 || d->hidden % 64 != 0)
-        return fail(TMT_MOE_EINVAL, "hidden=%d must be 0 or a multiple of 64", d->hidden);
+    if (d->hidden < 0 || d->hidden > (1 << 20))
+        return fail(TMT_MOE_EINVAL, "hidden=%d must be in [0, 2^20]", d->hidden);
     if ((int64_t)d->max_tokens * d->topk >= (1ll << 31))
         return fail(TMT_MOE_EINVAL, "max_tokens*topk must fit in int32");
     if (d->weight_format != TMT_MOE_WEIGHTS_BF16 && d->weight_format != TMT_MOE_WEIGHTS_MXFP4 &&
@@ -153,6 +186,13 @@ int validate_desc(const tmt_moe_desc* d) {
     }
     if (d->weight_format != TMT_MOE_WEIGHTS_BF16 && d->hidden == 0)
         return fail(TMT_MOE_EINVAL, "MXFP4 weights need hidden > 0");
+    // the MX blocks of 32 run along d and hidden, and the FP4 GEMMs step K by 64
+    if (d->weight_format != TMT_MOE_WEIGHTS_BF16 && (d->d % 64 != 0 || d->hidden % 64 != 0))
+        return fail(TMT_MOE_EINVAL, "MXFP4 weights need d and hidden multiples of 64 (d=%d, hidden=%d)", d->d,
+                    d->hidden);
+    const tmt_moe_desc in = internal_desc(*d);
+    if ((int64_t)d->max_tokens * in.d >= (int64_t(1) << 40) || (int64_t)in.hidden * in.d >= (int64_t(1) << 31))
+        return fail(TMT_MOE_EINVAL, "d=%d, hidden=%d too large", d->d, d->hidden);
     return TMT_MOE_OK;
 }
 
@@ -184,11 +224,13 @@ struct Sizes {
     size_t layer = 0, shared = 0;
 };
 
-Sizes plan(const tmt_moe_desc* d, tmt_moe* m) {
+Sizes plan(const tmt_moe_desc* user, tmt_moe* m) {
+    const tmt_moe_desc din = internal_desc(*user);
+    const tmt_moe_desc* d = &din;
     const int64_t T = d->max_tokens, E = d->experts, K = d->topk, D = d->d, h = d->hidden;
     const int64_t hn = h > 0 ? h : D;
     const int64_t TK = T * K;
-    const int rpb_min = 4 * router_rows_per_wave((int)E);
+    const int rpb_min = kRouterWaves * router_rows_per_wave((int)E);
     const int64_t nblk = (T + rpb_min - 1) / rpb_min;
     Layout L, W;
     size_t o_logits = L.add(T * E * 4), o_probs = L.add(T * E * 4), o_lse = L.add(T * 4);
@@ -230,6 +272,27 @@ Sizes plan(const tmt_moe_desc* d, tmt_moe* m) {
     const int64_t ln_rows = std::max(scatter_blocks((int)T), ln_chunks((int)T));
     size_t o_lnp = bwd ? W.add((size_t)ln_rows * 2 * D * 4) : 0;
     size_t o_lnp2 = bwd ? W.add((size_t)colsum_groups((int)ln_rows) * 2 * D * 4) : 0;
+    // zero-padded operand copies of a handle whose widths are not multiples
+    // of 64 (transient: every call fills the ones it reads)
+    const bool pad = is_padded(*user);
+    size_t o_px = 0, o_py = 0, o_pdy = 0, o_pdx = 0, o_pwr = 0, o_pdwr = 0;
+    size_t o_pwu[kMaxExperts] = {}, o_pwd[kMaxExperts] = {}, o_pdwu[kMaxExperts] = {}, o_pdwd[kMaxExperts] = {};
+    if (pad) {
+        o_px = W.add(T * D * 2);
+        o_py = W.add(T * D * 2);
+        o_pdy = W.add(T * D * 2);
+        o_pdx = W.add(T * D * 2);
+        o_pwr = W.add(E * D * 2);
+        o_pdwr = W.add(E * D * 4);
+        for (int64_t e = 0; e < E; ++e) {
+            o_pwu[e] = W.add(hn * D * 2);
+            o_pdwu[e] = W.add(hn * D * 4);
+            if (h > 0) {
+                o_pwd[e] = W.add(D * h * 2);
+                o_pdwd[e] = W.add(D * h * 4);
+            }
+        }
+    }
     if (m) {
         char* a = m->arena;
         char* w = m->ws;
@@ -271,6 +334,21 @@ Sizes plan(const tmt_moe_desc* d, tmt_moe* m) {
         m->ln_partial = bwd ? (float*)(w + o_lnp) : nullptr;
         m->ln_partial2 = bwd ? (float*)(w + o_lnp2) : nullptr;
         m->nblk_max = (int)nblk;
+        m->padded = pad;
+        if (pad) {
+            m->px = (uint16_t*)(w + o_px);
+            m->py = (uint16_t*)(w + o_py);
+            m->pdy = (uint16_t*)(w + o_pdy);
+            m->pdx = (uint16_t*)(w + o_pdx);
+            m->pwr = (uint16_t*)(w + o_pwr);
+            m->pdwr = (float*)(w + o_pdwr);
+            for (int64_t e = 0; e < E; ++e) {
+                m->pwu[e] = (uint16_t*)(w + o_pwu[e]);
+                m->pdwu[e] = (float*)(w + o_pdwu[e]);
+                m->pwd[e] = h > 0 ? (uint16_t*)(w + o_pwd[e]) : nullptr;
+                m->pdwd[e] = h > 0 ? (float*)(w + o_pdwd[e]) : nullptr;
+            }
+        }
     }
     return Sizes{L.total, W.total};
 }
@@ -406,11 +484,11 @@ int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* W
     return TMT_MOE_OK;
 }
 
-int check_ptrs(const void* const* tab, int n, const char* what) {
+int check_ptrs(const void* const* tab, int n, const char* what, unsigned align = 16) {
     if (!tab) return fail(TMT_MOE_EINVAL, "%s table is NULL", what);
     for (int e = 0; e < n; ++e) {
         if (!tab[e]) return fail(TMT_MOE_EINVAL, "%s[%d] is NULL", what, e);
-        if (!aligned16(tab[e])) return fail(TMT_MOE_EINVAL, "%s[%d] is not 16-byte aligned", what, e);
+        if (!aligned_to(tab[e], align)) return fail(TMT_MOE_EINVAL, "%s[%d] is not %u-byte aligned", what, e, align);
     }
     return TMT_MOE_OK;
 }
@@ -425,12 +503,14 @@ int check_forward(tmt_moe* m, int T, const uint16_t* X, const char* xname, const
         return fail(TMT_MOE_EINVAL, "handle expects MXFP4 weights: use tmt_moe_forward_mxfp4");
     if (T < 0 || T > ds.max_tokens) return fail(TMT_MOE_EINVAL, "T=%d outside [0, %d]", T, ds.max_tokens);
     if (T > 0 && (!X || !Y)) return fail(TMT_MOE_EINVAL, "%s and Y must be non-NULL", xname);
-    if (!aligned16(X) || !aligned16(Y)) return fail(TMT_MOE_EINVAL, "%s and Y must be 16-byte aligned", xname);
-    if (ds.experts > 1 && (!Wr || !aligned16(Wr)))
-        return fail(TMT_MOE_EINVAL, "Wr must be a 16-byte aligned pointer when experts > 1");
-    int rc = check_ptrs((const void* const*)W_up, ds.experts, "W_up");
+    const unsigned a = m->align_bf16;
+    if (!aligned_to(X, a) || !aligned_to(Y, a))
+        return fail(TMT_MOE_EINVAL, "%s and Y must be %u-byte aligned", xname, a);
+    if (ds.experts > 1 && (!Wr || !aligned_to(Wr, a)))
+        return fail(TMT_MOE_EINVAL, "Wr must be a %u-byte aligned pointer when experts > 1", a);
+    int rc = check_ptrs((const void* const*)W_up, ds.experts, "W_up", a);
     if (rc) return rc;
-    if (ds.hidden > 0 && (rc = check_ptrs((const void* const*)W_down, ds.experts, "W_down"))) return rc;
+    if (ds.hidden > 0 && (rc = check_ptrs((const void* const*)W_down, ds.experts, "W_down", a))) return rc;
     return check_device(m);
 }
 
@@ -531,17 +611,18 @@ int check_backward(tmt_moe* m, const uint16_t* dY, const uint16_t* X, const uint
     if (m->last_T < 0) return fail(TMT_MOE_ESTATE, "backward called without a successful forward");
     const int T = m->last_T, E = ds.experts, h = ds.hidden;
     if (T > 0 && (!dY || !X || !dX)) return fail(TMT_MOE_EINVAL, "dY, X and dX must be non-NULL");
-    if (!aligned16(dY) || !aligned16(X) || !aligned16(dX))
-        return fail(TMT_MOE_EINVAL, "dY, X and dX must be 16-byte aligned");
-    if (E > 1 && (!Wr || !dWr || !aligned16(Wr) || !aligned16(dWr)))
-        return fail(TMT_MOE_EINVAL, "Wr and dWr must be 16-byte aligned pointers when experts > 1");
-    if (!aligned16(dWr)) return fail(TMT_MOE_EINVAL, "dWr must be 16-byte aligned");
-    int rc = check_ptrs((const void* const*)W_up, E, "W_up");
+    const unsigned a = m->align_bf16, af = m->align_f32;
+    if (!aligned_to(dY, a) || !aligned_to(X, a) || !aligned_to(dX, a))
+        return fail(TMT_MOE_EINVAL, "dY, X and dX must be %u-byte aligned", a);
+    if (E > 1 && (!Wr || !dWr || !aligned_to(Wr, a) || !aligned_to(dWr, af)))
+        return fail(TMT_MOE_EINVAL, "Wr and dWr must be aligned pointers (%u / %u bytes) when experts > 1", a, af);
+    if (!aligned_to(dWr, af)) return fail(TMT_MOE_EINVAL, "dWr must be %u-byte aligned", af);
+    int rc = check_ptrs((const void* const*)W_up, E, "W_up", a);
     if (rc) return rc;
-    if ((rc = check_ptrs((const void* const*)dW_up, E, "dW_up"))) return rc;
+    if ((rc = check_ptrs((const void* const*)dW_up, E, "dW_up", af))) return rc;
     if (h > 0) {
-        if ((rc = check_ptrs((const void* const*)W_down, E, "W_down"))) return rc;
-        if ((rc = check_ptrs((const void* const*)dW_down, E, "dW_down"))) return rc;
+        if ((rc = check_ptrs((const void* const*)W_down, E, "W_down", a))) return rc;
+        if ((rc = check_ptrs((const void* const*)dW_down, E, "dW_down", af))) return rc;
     }
     return check_device(m);
 }
@@ -620,7 +701,9 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
         rw.nchunks = router_dw_chunks(T); rw.partial = m->dwr_partial; rw.dWr = dWr;
         LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_router_dw(rw, s));
     }
-    const bool ln_fused = ln != nullptr && d <= kLnFusedMaxD;
+    // the scatter's fused LayerNorm backward needs the row width of the
+    // LayerNorm itself (a padded handle runs the separate kernels)
+    const bool ln_fused = ln != nullptr && d <= kLnFusedMaxD && !m->padded;
     if (T > 0) {
         ScatterParams sc{};
         sc.dXg = m->dXg; sc.slot_of = m->slot_of; sc.dlogits = E > 1 ? m->dlogits : nullptr;
@@ -633,10 +716,13 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
     }
     if (ln_fused) {
         LAUNCH(TMT_MOE_PH_NORM_BWD, launch_colsum(m->ln_partial, T > 0 ? scatter_blocks(T) : 0, 2 * d,
-                                                  m->ln_partial2, d, ln->dGamma, ln->dBeta, s));
+                                                  m->ln_partial2, d, d, ln->dGamma, ln->dBeta, s));
     } else if (ln) {
+        // the caller's S / dS rows have the caller's width; dX (the gradient
+        // at H) has the internal one
         LayerNormParams lp{};
-        lp.S = ln->S; lp.gamma = ln->gamma; lp.T = T; lp.d = d;
+        lp.S = ln->S; lp.gamma = ln->gamma; lp.T = T; lp.d = m->user.d;
+        lp.lds = m->user.d; lp.ldh = d;
         lp.mean = m->ln_mean; lp.rstd = m->ln_rstd; lp.dH = dX; lp.dS = ln->dS;
         lp.partial = m->ln_partial; lp.partial2 = m->ln_partial2; lp.dgamma = ln->dGamma; lp.dbeta = ln->dBeta;
         LAUNCH(TMT_MOE_PH_NORM_BWD, launch_ln_bwd(lp, s));
@@ -646,17 +732,17 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
 
 int check_ln_shape(int32_t T, int32_t d) {
     if (T < 0) return fail(TMT_MOE_EINVAL, "T=%d must be >= 0", T);
-    if (d < 64 || d % 64 != 0) return fail(TMT_MOE_EINVAL, "d=%d must be a positive multiple of 64", d);
+    if (d < 1 || d > (1 << 20)) return fail(TMT_MOE_EINVAL, "d=%d must be in [1, 2^20]", d);
     return TMT_MOE_OK;
 }
 
 // Workspace of the standalone LayerNorm backward, in floats: chunk partials,
 // then (from *level1_off, 256-byte aligned) the level-1 column sums.
 size_t ln_workspace_floats(int32_t T, int32_t d, size_t* level1_off) {
-    const size_t nch = (size_t)ln_chunks(T);
-    const size_t off = (nch * 2 * d + 63) & ~size_t(63);
+    const size_t nch = (size_t)ln_chunks(T), pw = (size_t)ln_width4(d);
+    const size_t off = (nch * 2 * pw + 63) & ~size_t(63);
     *level1_off = off;
-    return off + (size_t)colsum_groups((int)nch) * 2 * d;
+    return off + (size_t)colsum_groups((int)nch) * 2 * pw;
 }
 
 int check_ln_backward_args(int32_t T, int32_t d, const uint16_t* S, const uint16_t* dH, const float* gamma,
@@ -680,12 +766,70 @@ int run_ln_backward(hipStream_t s, int32_t T, int32_t d, const uint16_t* S, cons
                     const float* gamma, const float* mean, const float* rstd, uint16_t* dS, float* dGamma,
                     float* dBeta, float* ws, size_t level1_off) {
     LayerNormParams p{};
-    p.S = S; p.gamma = gamma; p.T = T; p.d = d; p.mean = const_cast<float*>(mean);
+    p.S = S; p.gamma = gamma; p.T = T; p.d = d; p.lds = d; p.ldh = d; p.mean = const_cast<float*>(mean);
     p.rstd = const_cast<float*>(rstd); p.dH = dH; p.dS = dS;
     p.partial = ws;
     p.partial2 = ws + level1_off;
     p.dgamma = dGamma; p.dbeta = dBeta;
     HIP_TRY(launch_ln_bwd(p, s));
+    return TMT_MOE_OK;
+}
+
+// ---- padded handles (d or hidden not a multiple of 64) ----------------------
+// n matrices of rows_s x cols_s (contiguous rows) copied into rows_d x cols_d
+// ones: zero-filled when the destination is larger, cropped when smaller.
+int copy_mats(hipStream_t s, const void* const* src, void* const* dst, int n, int64_t rows_s, int64_t cols_s,
+              int64_t rows_d, int64_t cols_d, int elem_bytes) {
+    PadParams p{};
+    for (int i = 0; i < n; ++i) {
+        p.src[i] = src[i];
+        p.dst[i] = dst[i];
+    }
+    p.rows_s = rows_s; p.cols_s = cols_s; p.ld_s = cols_s;
+    p.rows_d = rows_d; p.cols_d = cols_d; p.ld_d = cols_d;
+    HIP_TRY(launch_pad_copy(p, n, elem_bytes, s));
+    return TMT_MOE_OK;
+}
+// [T][user d] bf16 rows to [T][d] and back.
+int pad_rows(const tmt_moe* m, hipStream_t s, int T, const uint16_t* src, uint16_t* dst) {
+    const void* a[1] = {src};
+    void* b[1] = {dst};
+    return copy_mats(s, a, b, 1, T, m->user.d, T, m->desc.d, 2);
+}
+int unpad_rows(const tmt_moe* m, hipStream_t s, int T, const uint16_t* src, uint16_t* dst) {
+    const void* a[1] = {src};
+    void* b[1] = {dst};
+    return copy_mats(s, a, b, 1, T, m->desc.d, T, m->user.d, 2);
+}
+// Router and expert weights into the handle's padded copies.
+int pad_weights(tmt_moe* m, hipStream_t s, const uint16_t* Wr, const uint16_t* const* W_up,
+                const uint16_t* const* W_down) {
+    const int E = m->desc.experts, du = m->user.d, dp = m->desc.d, hu = m->user.hidden, hp = m->desc.hidden;
+    const int hnu = hu > 0 ? hu : du;
+    int rc;
+    if (E > 1) {
+        const void* a[1] = {Wr};
+        void* b[1] = {m->pwr};
+        if ((rc = copy_mats(s, a, b, 1, E, du, E, dp, 2))) return rc;
+    }
+    if ((rc = copy_mats(s, (const void* const*)W_up, (void* const*)m->pwu, E, hnu, du, m->hn, dp, 2))) return rc;
+    if (hp > 0 && (rc = copy_mats(s, (const void* const*)W_down, (void* const*)m->pwd, E, du, hu, dp, hp, 2)))
+        return rc;
+    return TMT_MOE_OK;
+}
+// Gradients from the padded copies to the caller's (dWr may be NULL when E == 1).
+int unpad_grads(tmt_moe* m, hipStream_t s, float* dWr, float* const* dW_up, float* const* dW_down) {
+    const int E = m->desc.experts, du = m->user.d, dp = m->desc.d, hu = m->user.hidden, hp = m->desc.hidden;
+    const int hnu = hu > 0 ? hu : du;
+    int rc;
+    if (dWr) {
+        const void* a[1] = {m->pdwr};
+        void* b[1] = {dWr};
+        if ((rc = copy_mats(s, a, b, 1, E, dp, E, du, 4))) return rc;
+    }
+    if ((rc = copy_mats(s, (const void* const*)m->pdwu, (void* const*)dW_up, E, m->hn, dp, hnu, du, 4))) return rc;
+    if (hp > 0 && (rc = copy_mats(s, (const void* const*)m->pdwd, (void* const*)dW_down, E, dp, hp, du, hu, 4)))
+        return rc;
     return TMT_MOE_OK;
 }
 
@@ -731,8 +875,14 @@ int create_handle(const tmt_moe_desc* desc, void* workspace, size_t workspace_by
     }
     tmt_moe* m = new (std::nothrow) tmt_moe();
     if (!m) return fail(TMT_MOE_ENOMEM, "host allocation failed");
-    m->desc = *desc;
-    m->hn = desc->hidden > 0 ? desc->hidden : desc->d;
+    m->desc = internal_desc(*desc);
+    m->user = *desc;
+    m->hn = m->desc.hidden > 0 ? m->desc.hidden : m->desc.d;
+    if (is_padded(*desc)) {
+        // operands are read element by element into the padded copies
+        m->align_bf16 = 2;
+        m->align_f32 = 4;
+    }
     hipError_t err = hipGetDevice(&m->device);
     if (err != hipSuccess) {
         delete m;
@@ -791,7 +941,13 @@ int tmt_moe_forward(tmt_moe* m, void* stream, int32_t T, const uint16_t* X,
     int rc = check_forward(m, T, X, "X", Wr, W_up, W_down, Y);
     if (rc) return rc;
     m->last_ln = false;
-    return run_forward(m, (hipStream_t)stream, T, X, Wr, logit_bias, W_up, W_down, Y, beta);
+    hipStream_t s = (hipStream_t)stream;
+    if (!m->padded) return run_forward(m, s, T, X, Wr, logit_bias, W_up, W_down, Y, beta);
+    m->last_T = -1;
+    if ((rc = pad_weights(m, s, Wr, W_up, W_down)) || (rc = pad_rows(m, s, T, X, m->px))) return rc;
+    if (beta != 0.0f && (rc = pad_rows(m, s, T, Y, m->py))) return rc;  // beta == 0: Y is not read
+    if ((rc = run_forward(m, s, T, m->px, m->pwr, logit_bias, m->pwu, m->pwd, m->py, beta))) return rc;
+    return unpad_rows(m, s, T, m->py, Y);
 }
 
 int tmt_moe_forward_ln(tmt_moe* m, void* stream, int32_t T, const uint16_t* S,
@@ -806,16 +962,25 @@ int tmt_moe_forward_ln(tmt_moe* m, void* stream, int32_t T, const uint16_t* S,
     hipStream_t s = (hipStream_t)stream;
     m->last_T = -1;
     m->last_ln = false;
+    // H has the internal width (zeros in the padded columns of a padded handle)
     LayerNormParams ln{};
-    ln.S = S; ln.gamma = ln_gamma; ln.beta = ln_beta; ln.T = T; ln.d = m->desc.d;
+    ln.S = S; ln.gamma = ln_gamma; ln.beta = ln_beta; ln.T = T; ln.d = m->user.d;
+    ln.lds = m->user.d; ln.ldh = m->desc.d;
     ln.H = m->H; ln.mean = m->ln_mean; ln.rstd = m->ln_rstd;
     // Routed batches: the router normalises its rows itself (one read of S
     // instead of a LayerNorm pass and a read of H); otherwise the LayerNorm
     // runs first.
     const LnFuse fuse{S, ln_gamma, ln_beta};
-    const bool fused = ln_in_router(T, m->desc.experts, m->desc.d);
+    const bool fused = !m->padded && ln_in_router(T, m->desc.experts, m->desc.d);
     if (!fused) LAUNCH(TMT_MOE_PH_NORM, launch_ln_fwd(ln, s));
-    if ((rc = run_forward(m, s, T, m->H, Wr, logit_bias, W_up, W_down, Y, beta, fused ? &fuse : nullptr))) return rc;
+    if (m->padded) {
+        if ((rc = pad_weights(m, s, Wr, W_up, W_down))) return rc;
+        if (beta != 0.0f && (rc = pad_rows(m, s, T, Y, m->py))) return rc;
+        if ((rc = run_forward(m, s, T, m->H, m->pwr, logit_bias, m->pwu, m->pwd, m->py, beta))) return rc;
+        if ((rc = unpad_rows(m, s, T, m->py, Y))) return rc;
+    } else if ((rc = run_forward(m, s, T, m->H, Wr, logit_bias, W_up, W_down, Y, beta, fused ? &fuse : nullptr))) {
+        return rc;
+    }
     m->last_ln = true;
     return TMT_MOE_OK;
 }
@@ -902,8 +1067,18 @@ int tmt_moe_backward(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_
         return fail(TMT_MOE_ESTATE, "the last forward was tmt_moe_forward_ln: use tmt_moe_backward_ln");
     int rc = check_backward(m, dY, X, Wr, W_up, W_down, dX, dWr, dW_up, dW_down);
     if (rc) return rc;
-    return run_backward(m, (hipStream_t)stream, dY, X, Wr, W_up, W_down, aux_coef, z_coef, dX, dWr,
-                        dW_up, dW_down, nullptr);
+    hipStream_t s = (hipStream_t)stream;
+    if (!m->padded)
+        return run_backward(m, s, dY, X, Wr, W_up, W_down, aux_coef, z_coef, dX, dWr, dW_up, dW_down, nullptr);
+    const int T = m->last_T;
+    if ((rc = pad_weights(m, s, Wr, W_up, W_down)) || (rc = pad_rows(m, s, T, X, m->px)) ||
+        (rc = pad_rows(m, s, T, dY, m->pdy)))
+        return rc;
+    if ((rc = run_backward(m, s, m->pdy, m->px, m->pwr, m->pwu, m->pwd, aux_coef, z_coef, m->pdx,
+                           dWr ? m->pdwr : nullptr, m->pdwu, m->pdwd, nullptr)))
+        return rc;
+    if ((rc = unpad_rows(m, s, T, m->pdx, dX))) return rc;
+    return unpad_grads(m, s, dWr, dW_up, dW_down);
 }
 
 int tmt_moe_backward_ln(tmt_moe* m, void* stream, const uint16_t* dY, const uint16_t* S,
@@ -918,12 +1093,19 @@ int tmt_moe_backward_ln(tmt_moe* m, void* stream, const uint16_t* dY, const uint
     if (rc) return rc;
     const int T = m->last_T;
     if (T > 0 && (!S || !dS)) return fail(TMT_MOE_EINVAL, "S and dS must be non-NULL");
-    if (!aligned16(S) || !aligned16(dS)) return fail(TMT_MOE_EINVAL, "S and dS must be 16-byte aligned");
+    if (!aligned_to(S, m->align_bf16) || !aligned_to(dS, m->align_bf16))
+        return fail(TMT_MOE_EINVAL, "S and dS must be %u-byte aligned", m->align_bf16);
     if (!ln_gamma || !dGamma || !dBeta || !aligned16(ln_gamma) || !aligned16(dGamma) || !aligned16(dBeta))
         return fail(TMT_MOE_EINVAL, "ln_gamma, dGamma and dBeta must be 16-byte aligned device pointers");
     const LnGrad lg{S, ln_gamma, dS, dGamma, dBeta};
-    return run_backward(m, (hipStream_t)stream, dY, m->H, Wr, W_up, W_down, aux_coef, z_coef, m->dH, dWr,
-                        dW_up, dW_down, &lg);
+    hipStream_t s = (hipStream_t)stream;
+    if (!m->padded)
+        return run_backward(m, s, dY, m->H, Wr, W_up, W_down, aux_coef, z_coef, m->dH, dWr, dW_up, dW_down, &lg);
+    if ((rc = pad_weights(m, s, Wr, W_up, W_down)) || (rc = pad_rows(m, s, T, dY, m->pdy))) return rc;
+    if ((rc = run_backward(m, s, m->pdy, m->H, m->pwr, m->pwu, m->pwd, aux_coef, z_coef, m->dH,
+                           dWr ? m->pdwr : nullptr, m->pdwu, m->pdwd, &lg)))
+        return rc;
+    return unpad_grads(m, s, dWr, dW_up, dW_down);
 }
 
 int tmt_moe_read_stats(tmt_moe* m, void* stream, float* aux, float* z, int32_t* counts) {
@@ -1027,7 +1209,8 @@ int tmt_moe_layernorm_forward(void* stream, int32_t T, int32_t d, const uint16_t
     if (!aligned16(S) || !aligned16(H) || !aligned16(gamma) || !aligned16(beta))
         return fail(TMT_MOE_EINVAL, "S, H, gamma and beta must be 16-byte aligned");
     LayerNormParams p{};
-    p.S = S; p.gamma = gamma; p.beta = beta; p.T = T; p.d = d; p.H = H; p.mean = mean; p.rstd = rstd;
+    p.S = S; p.gamma = gamma; p.beta = beta; p.T = T; p.d = d; p.lds = d; p.ldh = d;
+    p.H = H; p.mean = mean; p.rstd = rstd;
     HIP_TRY(launch_ln_fwd(p, (hipStream_t)stream));
     return TMT_MOE_OK;
 }
@@ -1076,8 +1259,8 @@ int tmt_moe_read_norm(tmt_moe* m, void* stream, uint16_t* H, float* mean, float*
     int rc = check_device(m);
     if (rc) return rc;
     HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
-    const int64_t T = m->last_T, d = m->desc.d;
-    if (H && T) HIP_TRY(hipMemcpy(H, m->H, T * d * 2, hipMemcpyDeviceToHost));
+    const int64_t T = m->last_T, du = m->user.d, dp = m->desc.d;
+    if (H && T) HIP_TRY(hipMemcpy2D(H, du * 2, m->H, dp * 2, du * 2, T, hipMemcpyDeviceToHost));
     if (mean && T) HIP_TRY(hipMemcpy(mean, m->ln_mean, T * 4, hipMemcpyDeviceToHost));
     if (rstd && T) HIP_TRY(hipMemcpy(rstd, m->ln_rstd, T * 4, hipMemcpyDeviceToHost));
     return TMT_MOE_OK;

@@ -328,29 +328,46 @@ hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStre
 
 // ------------------------------------------------------------------ norm --
 struct LayerNormParams {
-    const uint16_t* S;       // [T][d] bf16 LayerNorm input
+    const uint16_t* S;       // [T][lds] bf16 LayerNorm input (d columns used)
     const float* gamma;      // [d]
     const float* beta;       // [d] (forward)
-    int T, d;
-    uint16_t* H;             // [T][d] bf16 output (forward)
+    int T, d;                // rows, row width (the statistics divide by d)
+    int lds, ldh;            // row strides of S / dS and of H / dH (>= d); H's
+                             // columns [d, ldh) are written as zeros
+    uint16_t* H;             // [T][ldh] bf16 output (forward)
     float* mean;             // [T] (written by forward, read by backward)
     float* rstd;             // [T]
-    const uint16_t* dH;      // [T][d] bf16 gradient at H (backward)
-    uint16_t* dS;            // [T][d] bf16 (backward)
-    float* partial;          // [ln_chunks(T)][2][d] dgamma / dbeta chunk sums
-    float* partial2;         // [colsum_groups(ln_chunks(T))][2][d] (level-1 sums)
+    const uint16_t* dH;      // [T][ldh] bf16 gradient at H (backward)
+    uint16_t* dS;            // [T][lds] bf16 (backward)
+    float* partial;          // [ln_chunks(T)][2][ln_width4(d)] dgamma / dbeta chunk sums
+    float* partial2;         // [colsum_groups(ln_chunks(T))][2][ln_width4(d)] (level-1 sums)
     float* dgamma;           // [d]
     float* dbeta;            // [d]
 };
 int ln_chunks(int T);
+// Row stride of the dgamma / dbeta partials: d rounded up to a multiple of 4.
+__host__ __device__ inline int ln_width4(int d) { return (d + 3) & ~3; }
 hipError_t launch_ln_fwd(const LayerNormParams& p, hipStream_t s);
 hipError_t launch_ln_bwd(const LayerNormParams& p, hipStream_t s);
 // Fixed-order column sums of in [nrows][ncols] (ncols % 4 == 0): columns
-// [0, split) to out_lo, [split, ncols) to out_hi; scratch holds
+// [0, split) to out_lo, [split, ncols) to out_hi, each of which receives its
+// first `width` columns (width <= split, ncols - split); scratch holds
 // [colsum_groups(nrows)][ncols] level-1 sums.
 int colsum_groups(int nrows);
-hipError_t launch_colsum(const float* in, int nrows, int ncols, float* scratch, int split, float* out_lo,
-                         float* out_hi, hipStream_t s);
+hipError_t launch_colsum(const float* in, int nrows, int ncols, float* scratch, int split, int width,
+                         float* out_lo, float* out_hi, hipStream_t s);
+
+// Zero-padded copies between a caller's matrices and the internal ones of a
+// handle whose width is not a multiple of 64: dst[r][c] = src[r][c] for
+// r < rows_s and c < cols_s, else 0, over rows_d x cols_d (one launch copies
+// up to kMaxExperts matrices of one shape; blockIdx.y picks the matrix).
+struct PadParams {
+    const void* src[kMaxExperts];
+    void* dst[kMaxExperts];
+    int64_t rows_s, cols_s, ld_s;
+    int64_t rows_d, cols_d, ld_d;
+};
+hipError_t launch_pad_copy(const PadParams& p, int nmat, int elem_bytes, hipStream_t s);
 
 // ----------------------------------------------------------------- adamw --
 constexpr int kAdamChunk = 8192;      // elements per chunk (one workgroup)

@@ -949,6 +949,34 @@ hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStre
     return hipGetLastError();
 }
 
+namespace {
+// One thread per destination element (these copies serve widths that are not
+// a multiple of 64, where speed is not the point).
+template <typename V>
+__global__ __launch_bounds__(kThreads) void pad_copy_kernel(PadParams p) {
+    const V* src = static_cast<const V*>(p.src[blockIdx.y]);
+    V* dst = static_cast<V*>(p.dst[blockIdx.y]);
+    const int64_t n = p.rows_d * p.cols_d;
+    for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < n; i += (int64_t)gridDim.x * kThreads) {
+        const int64_t r = i / p.cols_d, c = i - r * p.cols_d;
+        V v = 0;
+        if (r < p.rows_s && c < p.cols_s) v = src[r * p.ld_s + c];
+        dst[r * p.ld_d + c] = v;
+    }
+}
+}  // namespace
+
+hipError_t launch_pad_copy(const PadParams& p, int nmat, int elem_bytes, hipStream_t s) {
+    if (nmat < 0 || nmat > kMaxExperts || p.cols_s > p.ld_s || p.cols_d > p.ld_d) return hipErrorInvalidValue;
+    const int64_t n = p.rows_d * p.cols_d;
+    if (nmat == 0 || n <= 0) return hipSuccess;
+    const unsigned blocks = (unsigned)std::min<int64_t>((n + kThreads - 1) / kThreads, 2048);
+    if (elem_bytes == 2) pad_copy_kernel<uint16_t><<<dim3(blocks, nmat), kThreads, 0, s>>>(p);
+    else if (elem_bytes == 4) pad_copy_kernel<float><<<dim3(blocks, nmat), kThreads, 0, s>>>(p);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     const int64_t blocks = std::min<int64_t>((n + kThreads - 1) / kThreads, 1024);

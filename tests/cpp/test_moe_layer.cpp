@@ -104,7 +104,7 @@ static std::vector<uint16_t> uniform_bf16(std::mt19937& g, size_t n, float a) {
 // upstream gradient so only the regulariser reaches the router; checked
 // through dWrouter = dlogits^T X and the router part of dX = dlogits Wr.
 static void test_router() {
-    constexpr int N = 5, E = 4, K = 2, D = 64;
+    constexpr int N = 5, E = 4, K = 2, D = 16;  // small_config's dim (architecture_test.cu:88-89)
     std::mt19937 g(1234);
     auto X = normal_bf16(g, (size_t)N * D, 1.f), Wr = normal_bf16(g, (size_t)E * D, 0.125f);
     std::vector<std::vector<uint16_t>> We(E);
@@ -179,11 +179,12 @@ static void test_router() {
 
 // Two experts with identical weights, both selected (renormalised weights sum
 // to 1), compute exactly the dense layer: forward, summed expert gradients
-// and the input gradient must match the E=1 path (as test_moe_backward).
-static void identical_experts(int hidden) {
-    constexpr int N = 14, D = 64;  // batch 2 x seqlen 7
+// and the input gradient must match the E=1 path (as test_moe_backward, which
+// runs small_config: dim 16, batch 2 x seqlen 7, architecture_test.cu:88-89).
+static void identical_experts(int D, int hidden) {
+    constexpr int N = 14;  // batch 2 x seqlen 7
     const int hn = hidden > 0 ? hidden : D;
-    std::mt19937 g(99 + hidden);
+    std::mt19937 g(99 + hidden + D);
     auto X = normal_bf16(g, (size_t)N * D, 1.f), Y0 = normal_bf16(g, (size_t)N * D, 1.f);
     auto dYh = normal_bf16(g, (size_t)N * D, 1.f), Wr = normal_bf16(g, (size_t)2 * D, 0.02f);
     auto Wu = uniform_bf16(g, (size_t)hn * D, std::sqrt(1.f / D));
@@ -239,9 +240,13 @@ static void identical_experts(int hidden) {
     near(rel_l2(dx[1], dx[0]), 0, 0.03, 0, "input gradient through MoE differs from dense");
 }
 static void test_moe_backward() {
-    identical_experts(0);
-    std::puts("PASS MoE backward: identical experts reproduce dense expert and input gradients");
-    identical_experts(128);
+    identical_experts(16, 0);
+    std::puts("PASS MoE backward: identical experts reproduce dense expert and input gradients (dim 16)");
+    identical_experts(64, 0);
+    std::puts("PASS MoE backward: identical experts reproduce dense expert and input gradients (dim 64)");
+    identical_experts(16, 40);
+    std::puts("PASS MoE backward (up/SiLU/down experts, dim 16, hidden 40): identical experts reproduce the dense layer");
+    identical_experts(64, 128);
     std::puts("PASS MoE backward (up/SiLU/down experts): identical experts reproduce the dense layer");
 }
 

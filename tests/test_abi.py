@@ -58,20 +58,41 @@ def test_shared_workspace_split():
 
 
 @pytest.mark.parametrize("desc,msg", [
-    ((16, 100, 4, 2, 0), "multiple of 64"),
+    ((16, 0, 4, 2, 0), "d=0"),
+    ((16, -3, 4, 2, 0), "d=-3"),
     ((16, 128, 0, 1, 0), "experts"),
     ((16, 128, 65, 1, 0), "experts"),
     ((16, 128, 4, 5, 0), "topk"),
     ((16, 128, 16, 9, 0), "topk"),
-    ((16, 128, 4, 2, 100), "hidden"),
+    ((16, 128, 4, 2, -64), "hidden"),
     ((0, 128, 4, 2, 0), "max_tokens"),
-    ((16, 1000, 16, 2, 0), "multiple of 64"),  # contract difference: TMT accepts any dim
+    # the MXFP4 formats keep whole 64-wide K steps (blocks of 32 along d and h)
+    ((16, 100, 4, 2, 256, tmt_moe.WEIGHTS_MXFP4), "multiples of 64"),
+    ((16, 256, 4, 2, 100, tmt_moe.WEIGHTS_MXFP4_MX), "multiples of 64"),
 ])
 def test_invalid_descriptors_are_rejected(desc, msg):
     with pytest.raises(tmt_moe.MoeError) as ei:
         tmt_moe.workspace_size(*desc)
     assert ei.value.code == -1
     assert msg in str(ei.value)
+
+
+@pytest.mark.parametrize("desc", [
+    (14, 16, 1, 1, 0),      # TMT's small_config (architecture_test.cu:88-89): dense, dim 16
+    (14, 16, 2, 2, 0),      # ... with two experts, top-2 (test_moe_backward)
+    (64, 32, 4, 2, 0),      # tests/zig.sh:49 runs dim 32
+    (1000, 100, 4, 2, 0),
+    (1000, 100, 4, 2, 70),  # hidden not a multiple of 64 either
+    (16, 1000, 16, 2, 0),
+])
+def test_any_width_is_accepted(desc):
+    """TMT's validate_cfg takes any dim > 0 (tmt-cuda/src/config.h:46-52). The
+    library runs such a layer on zero-padded internal copies of width
+    ceil(d / 64) * 64 (and of hidden likewise), which the workspace holds."""
+    T, d, E, K, h = desc
+    size = tmt_moe.workspace_size(*desc)
+    dp, hp = -(-d // 64) * 64, (-(-h // 64) * 64 if h else 0)
+    assert size > tmt_moe.workspace_size(T, dp, E, K, hp)  # the padded copies come on top
 
 
 @pytest.mark.parametrize("desc", [
@@ -82,7 +103,7 @@ def test_invalid_descriptors_are_rejected(desc, msg):
 ])
 def test_reference_dims_are_accepted(desc):
     """TMT accepts experts <= 16 with any dim (tmt-cuda/src/config.h:46-52);
-    the library takes E up to 64 with any d that is a multiple of 64."""
+    the library takes E up to 64 with any d."""
     assert tmt_moe.workspace_size(*desc) > 0
 
 
@@ -91,13 +112,15 @@ def test_layernorm_workspace_and_argument_checks():
     nch = 32768 // 512
     assert tmt_moe.layernorm_workspace_size(32768, 1024) == (nch * 2 * 1024 + 1 * 2 * 1024) * 4
     assert tmt_moe.layernorm_workspace_size(0, 64) == (2 * 64 + 2 * 64) * 4
-    with pytest.raises(tmt_moe.MoeError, match="multiple of 64"):
-        tmt_moe.layernorm_workspace_size(16, 100)
+    # any width: partial rows of d rounded up to a multiple of 4
+    assert tmt_moe.layernorm_workspace_size(16, 100) == (256 + 2 * 100) * 4
+    with pytest.raises(tmt_moe.MoeError, match="d=0"):
+        tmt_moe.layernorm_workspace_size(16, 0)
     lib = tmt_moe.load_library()
     f = ctypes.c_void_p
     # argument checks run before any device work
-    assert lib.tmt_moe_layernorm_forward(None, 4, 96, None, None, None, None, None, None) == -1
-    assert "multiple of 64" in tmt_moe.last_error()
+    assert lib.tmt_moe_layernorm_forward(None, 4, 0, None, None, None, None, None, None) == -1
+    assert "d=0" in tmt_moe.last_error()
     assert lib.tmt_moe_layernorm_forward(None, 4, 128, None, None, None, None, None, None) == -1
     assert "non-NULL" in tmt_moe.last_error()
     fake = f(256)  # 256-byte aligned, never dereferenced: the size check fails first
