@@ -253,14 +253,24 @@ def bench_h0(name, steps=50, warmup=10):
         e1.record(stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
+        # per-kernel breakdown from the handle's per-launch events (a separate
+        # pass: the events add a little host time per launch)
+        m.set_profiling(True)
+        m.profile(reset=True)
+        for _ in range(steps):
+            step()
+        prof = m.profile(reset=True)
+        m.set_profiling(False)
     finally:
         m.close()
+    phase_us = {k: round(v[0] / steps * 1e3, 2) for k, v in prof.items() if v[1] > 0}
     fwd = 2.0 * T * d * E + 2.0 * T * K * d * d
     flops = fwd * 3.2  # profile.cu's model: bwd = 2.2 x fwd
     tf = flops / (ms / 1e3) / 1e12
     return {"workload": f"{name}: fwd+bwd T={T} d={d} E={E} top-{K} h=0 (aux {cfg['aux']}, z {cfg['z']})",
             "ms_per_step": round(ms, 4), "tokens_per_s": round(T / (ms / 1e3), 1),
             "tflops_profile_model": round(tf, 2), "mfma_frac_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+            "phase_us": phase_us,
             "reference_published": "about 50% of a 49 TFLOP/s roof at N=2048 E=8 K=2 D=1280 "
                                    "(CHANGES.md:35,46), i.e. about 24.5 TFLOP/s, other hardware"}
 
@@ -583,6 +593,8 @@ def main():
                     help="only the c5 MXFP4 forward measurement (both weight formats)")
     ap.add_argument("--no-h0", action="store_true",
                     help="skip the reference-expert (h = 0) fwd+bwd measurements")
+    ap.add_argument("--h0-only", action="store_true",
+                    help="only the reference-expert (h = 0) fwd+bwd measurements, with per-kernel times")
     ap.add_argument("--source-digest", action="store_true",
                     help="print the digest of the kernel sources the profiles are tagged with")
     args = ap.parse_args()
@@ -607,6 +619,10 @@ def main():
     if args.fp4_only:
         torch.cuda.set_device(0)
         print(json.dumps(bench_mxfp4(torch.cuda.current_stream())))
+        return
+    if args.h0_only:
+        torch.cuda.set_device(0)
+        print(json.dumps({name: bench_h0(name) for name in H0_SHAPES}))
         return
 
     import tmt_moe

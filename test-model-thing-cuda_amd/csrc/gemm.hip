@@ -47,7 +47,7 @@
 namespace tmt {
 namespace {
 
-constexpr int BM = kGemmTileRows;
+constexpr int BM = kGemmTileRows;  // tile rows of the large-problem kernels (TBM: the tile's own)
 
 // Tile geometry. BK_ is the K depth of one LDS stage (32 or 64), NST the
 // number of stages in the ring, BN_ the tile width and NWM_ the waves along
@@ -57,8 +57,9 @@ constexpr int BM = kGemmTileRows;
 //                  waves per SIMD on the same operand tiles);
 //   BN 128, NWM 2: two 4-wave workgroups per CU, 128 x 64 wave tiles, so one
 //                  workgroup's waits and epilogue overlap the other's MFMAs.
-template <int BK_, int NST, int BN_, int NWM_ = 2>
+template <int BK_, int NST, int BN_, int NWM_ = 2, int BM_ = 256>
 struct Geo {
+    static constexpr int BM = BM_;
     static constexpr int BK = BK_;
     static constexpr int NSTAGE = NST;
     static constexpr int BN = BN_;
@@ -75,7 +76,7 @@ struct Geo {
     static constexpr int DMA_PER_TILE = DMA_A + DMA_B;
     static constexpr int KC_ROWS = 1024 / (2 * BK);    // K-contiguous rows per wave load
     static constexpr int STEPS = BK / 16;              // MFMA k16 steps per stage
-    static constexpr int WGS = BN == 256 ? 1 : 2;      // workgroups per CU
+    static constexpr int WGS = BN == 256 && BM == 256 ? 1 : 2;  // workgroups per CU
     // the epilogue's fp32 staging ([EPR][WTN] per wave); the kernel sizes the
     // ring (single or split) and checks the total
     static constexpr int EPI = NW * EPR * WTN * 4;
@@ -193,9 +194,10 @@ __device__ __forceinline__ void wait_vm() {
 struct SplitPlan {
     int cut = 0, F = 0, R = 0, S = 1, chunk = 0;  // chunk: reduction length of a part
 };
+template <int TBM = BM>
 __device__ __forceinline__ int act_mtiles(const GemmParams& p) {
     int mt = 0;
-    for (int ee = 0; ee < p.E; ++ee) mt += (p.offsets[ee + 1] - p.offsets[ee] + BM - 1) / BM;
+    for (int ee = 0; ee < p.E; ++ee) mt += (p.offsets[ee + 1] - p.offsets[ee] + TBM - 1) / TBM;
     return mt;
 }
 template <int BK>
@@ -217,17 +219,19 @@ __device__ __forceinline__ SplitPlan split_plan(const GemmParams& p, int ntn, in
     sp.chunk = ((nk + S - 1) / S) * BK;
     return sp;
 }
-// Expert segment of activation M tile mt: expert, first slot, rows (e < 0: none).
+// Expert segment of activation M tile mt (TBM rows per tile): expert, first
+// slot, rows (e < 0: none).
+template <int TBM = BM>
 __device__ __forceinline__ void act_tile(const GemmParams& p, int mt, int& e, int& row0, int& rows) {
     e = -1;
     int t0 = 0;
     for (int ee = 0; ee < p.E; ++ee) {
         const int beg = p.offsets[ee], end = p.offsets[ee + 1];
-        const int tiles = (end - beg + BM - 1) / BM;
+        const int tiles = (end - beg + TBM - 1) / TBM;
         if (mt < t0 + tiles) {
             e = ee;
-            row0 = beg + (mt - t0) * BM;
-            rows = min(BM, end - row0);
+            row0 = beg + (mt - t0) * TBM;
+            rows = min(TBM, end - row0);
             return;
         }
         t0 += tiles;
@@ -236,9 +240,9 @@ __device__ __forceinline__ void act_tile(const GemmParams& p, int mt, int& e, in
 
 // Split rings (A in NST slots, B in NST - 1) for K = 64 tiles of the
 // activation GEMMs on 256 x 256 tiles.
-template <int KIND, int BK, int BN, int NWM>
+template <int KIND, int BK, int BN, int NWM, int TBM = BM>
 constexpr bool split_ring() {
-    return BK == 64 && BN == 256 && NWM == 2 && !Traits<KIND>::group_k;
+    return BK == 64 && BN == 256 && NWM == 2 && TBM == 256 && !Traits<KIND>::group_k;
 }
 
 // Persistent kernels: the split-ring GEMMs (every tile of a launch has the
@@ -249,23 +253,25 @@ constexpr bool split_ring() {
 // instead of once per tile. vb keeps the launch-order meaning of blockIdx.x
 // (gridDim.x is a multiple of 8 whenever it is below the tile count, so vb
 // runs on XCD vb % 8 as the tile map assumes).
-template <int KIND, int BK, int BN, int NWM>
+template <int KIND, int BK, int BN, int NWM, int TBM = BM>
 constexpr bool persistent_tiles() {
-    return split_ring<KIND, BK, BN, NWM>();
+    return split_ring<KIND, BK, BN, NWM, TBM>();
 }
 
 // One output tile (or split-K part) of the grouped GEMM: launch-order block
 // index vb; returns without touching memory when vb maps to no tile.
-template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2>
+template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2, int BM_ = 256>
 __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int vb) {
     using Tr = Traits<KIND>;
-    using Gm = Geo<BK_, NST, BN_, NWM_>;
+    using Gm = Geo<BK_, NST, BN_, NWM_, BM_>;
+    constexpr int BM = Gm::BM;
     constexpr int BK = Gm::BK, NSTAGE = Gm::NSTAGE, BN = Gm::BN, WTN = Gm::WTN, NJ = Gm::NJ;
     constexpr int WTM = Gm::WTM, MI = Gm::MI, NT = Gm::NT, EPR = Gm::EPR;
     constexpr int OPND_A = Gm::OPND_A, OPND_B = Gm::OPND_B;
     constexpr int DMA_A = Gm::DMA_A, DMA_B = Gm::DMA_B;
-    constexpr bool kSplit = split_ring<KIND, BK_, BN_, NWM_>();
+    constexpr bool kSplit = split_ring<KIND, BK_, BN_, NWM_, BM_>();
     static_assert(!kSplit || NST == 3, "split rings: 3 A slots and 2 B slots");
+    static_assert(BM == 256 || (BN == 128 && NWM_ == 2 && !Tr::b_fp4), "128-row tiles: 128 columns, 4 waves, bf16");
     // MXFP4 B operand per tile: 256 rows x BK/2 bytes of codes, then one 1 KiB
     // copy per wave of the tile's row scales (one 32-block at BK = 32, two at
     // BK = 64: lanes 16-31 load the second block's).
@@ -304,16 +310,28 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
     int row0 = 0, rows = 0;   // activation GEMMs: slot range of this tile
     int kbeg = 0, kend = 0;   // reduction range (slots for dW GEMMs)
     int mlim = 0;             // valid output rows in this tile
-    constexpr bool kSplitK = KIND == GEMM_DOWN || KIND == GEMM_DX;
+    constexpr bool kSplitK = (KIND == GEMM_DOWN || KIND == GEMM_DX) && BM == 256;
     int part_unit = -1;  // split-K tail: index of this workgroup's partial tile
     if constexpr (!Tr::group_k) {
         kbeg = 0;
         kend = p.K;
         SplitPlan sp;
         if constexpr (kSplitK) {
-            if (p.part != nullptr) sp = split_plan<BK>(p, ntn, act_mtiles(p));
+            if (p.part != nullptr) sp = split_plan<BK>(p, ntn, act_mtiles<BM>(p));
         }
-        if (sp.S >= 2 && vb >= sp.F) {
+        if (p.xcd_runs) {
+            // Launches whose tiles all run at once: the tiles in (mt, nt)
+            // order, nt fastest, cut into 8 runs of `per`; workgroup vb runs
+            // on XCD vb % 8 and takes tile vb / 8 of that XCD's run. Every
+            // XCD gets the same number of tiles, and a run covers whole rows
+            // of tiles of one or two experts, whose weights its L2 keeps.
+            const int R = act_mtiles<BM>(p) * ntn;
+            const int per = (R + 7) / 8;
+            const int j = (vb & 7) * per + (vb >> 3);
+            if ((vb >> 3) >= per || j >= R) return;
+            mt = j / ntn;
+            nt = j - mt * ntn;
+        } else if (sp.S >= 2 && vb >= sp.F) {
             const int u = vb - sp.F;
             if (u >= sp.R * sp.S) return;
             const int j = u / sp.S, q = u - j * sp.S;
@@ -328,7 +346,7 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
             nt = (G % ngn) * gn + gi / gm;
             if (nt >= ntn) return;
         }
-        act_tile(p, mt, e, row0, rows);
+        act_tile<BM>(p, mt, e, row0, rows);
         if (e < 0) return;  // beyond the last tile of the last expert
         mlim = rows;
     } else {
@@ -387,8 +405,9 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
             a_ptr[i] = p.a + (int64_t)src * p.lda + c * 8;
             a_k[i] = 0;
         } else {
-            const int k = 2 * q + (lane >> 5);
-            const int c = (lane & 31) ^ Gm::mc_swz(k);
+            constexpr int C = BM / 8;  // 16-byte chunks per k row
+            const int k = (64 / C) * q + lane / C;
+            const int c = (lane % C) ^ Gm::mc_swz(k);
             a_ptr[i] = p.a + min(mt * BM + c * 8, p.M - 8);
             a_k[i] = k;
         }
@@ -862,13 +881,13 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
     }
 }
 
-template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2>
-__global__ __launch_bounds__(128 * NWM_, (BN_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
-    if constexpr (persistent_tiles<KIND, BK_, BN_, NWM_>()) {
+template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2, int BM_ = 256>
+__global__ __launch_bounds__(128 * NWM_, (BN_ == 256 && BM_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
+    if constexpr (persistent_tiles<KIND, BK_, BN_, NWM_, BM_>()) {
         for (int vb = blockIdx.x; vb < p.vblocks; vb += gridDim.x)
-            grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_>(p, vb);
+            grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_, BM_>(p, vb);
     } else {
-        grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_>(p, blockIdx.x);
+        grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_, BM_>(p, blockIdx.x);
     }
 }
 
@@ -919,26 +938,28 @@ __global__ __launch_bounds__(256) void split_fixup_kernel(GemmParams p) {
 // Tile depth and ring per kind and tile width: split rings of K = 64 for the
 // activation GEMMs on 256 columns; K = 32 rings otherwise (4 stages of 32 KiB
 // at 256 columns, 3 of 24 KiB at 128 columns with two workgroups per CU).
-template <int KIND, int BN>
+// 128 x 128 tiles: 4 stages of K = 32 (64 KiB, the size of the epilogue's
+// staging anyway), two workgroups per CU.
+template <int KIND, int BN, int TBM = BM>
 struct Ring {
-    static constexpr bool split = split_ring<KIND, 64, BN, 2>();
+    static constexpr bool split = split_ring<KIND, 64, BN, 2, TBM>();
     static constexpr int BK = split ? 64 : 32;
-    static constexpr int NST = split ? 3 : (BN == 256 ? 4 : 3);
+    static constexpr int NST = split ? 3 : (BN == 256 || TBM == 128 ? 4 : 3);
 };
 
 // grid: the launch-order blocks of the tile map. Persistent kinds run
 // min(grid, CUs rounded down to a multiple of 8) workgroups over them.
-template <int KIND, bool DUAL, int BN, int NWM = 2>
+template <int KIND, bool DUAL, int BN, int NWM = 2, int TBM = BM>
 hipError_t launch_kind(const GemmParams& p, unsigned grid, hipStream_t s) {
-    using R = Ring<KIND, BN>;
+    using R = Ring<KIND, BN, TBM>;
     GemmParams q = p;
     q.vblocks = (int)grid;
     unsigned g = grid;
-    if constexpr (persistent_tiles<KIND, R::BK, BN, NWM>()) {
+    if constexpr (persistent_tiles<KIND, R::BK, BN, NWM, TBM>()) {
         const unsigned cus = (unsigned)(cu_count() / 8 * 8);
         if (cus >= 8 && g > cus) g = cus;
     }
-    grouped_gemm_kernel<KIND, DUAL, R::BK, R::NST, BN, NWM><<<g, 128 * NWM, 0, s>>>(q);
+    grouped_gemm_kernel<KIND, DUAL, R::BK, R::NST, BN, NWM, TBM><<<g, 128 * NWM, 0, s>>>(q);
     return hipGetLastError();
 }
 
@@ -951,17 +972,32 @@ hipError_t launch_kind(const GemmParams& p, unsigned grid, hipStream_t s) {
 // the 128-column tiles covered that VALU work and won. The weight-gradient
 // GEMMs run 256-column tiles in balanced 16-tile groups (4-6% faster than two
 // 128-column workgroups).
-int gemm_tile_n(GemmKind kind) {
-    (void)kind;
-    return 256;
+// Small problems: a launch whose 256 x 256 tiles would leave most CUs idle
+// runs 128 x 128 tiles (four times the tiles, two workgroups per CU). At
+// the reference's profile shape (4096 slots, d = 1280, h = 0) the up GEMM
+// took 30 us on 128 x 128 tiles against 29 us on 256 x 128 and 35 us on
+// 256 x 256 (all with the XCD runs of launch_gemm_tile); at TMT's default
+// width (2048 slots, d = 256) 9 against 12 and 16 us.
+static int64_t tiles_256(GemmKind kind, const GemmParams& p) {
+    const int64_t ntn = (p.N + 255) / 256;
+    if (kind == GEMM_DW_DOWN || kind == GEMM_DW_UP) return (int64_t)p.E * ((p.M + BM - 1) / BM) * ntn;
+    return ((int64_t)p.slots + BM - 1) / BM * ntn;  // lower bound (experts' partial tiles aside)
 }
 
-hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn, hipStream_t s) {
+GemmTile gemm_tile(GemmKind kind, const GemmParams& p) {
+    if (kind == GEMM_UP_FP4 || kind == GEMM_DOWN_FP4) return GemmTile{256, 256};
+    if (2 * tiles_256(kind, p) < cu_count()) return GemmTile{128, 128};
+    return GemmTile{256, 256};
+}
+
+hipError_t launch_gemm_tile(GemmKind kind, bool dual, const GemmParams& p, GemmTile tile, hipStream_t s) {
+    const int bn = tile.n, bm = tile.m;
     if (p.N % 8 != 0 || p.N <= 0) return hipErrorInvalidValue;
     if (bn != 256 && bn != 128) return hipErrorInvalidValue;
+    if (bm != 256 && !(bm == 128 && bn == 128)) return hipErrorInvalidValue;
     const bool group_k = kind == GEMM_DW_DOWN || kind == GEMM_DW_UP;
     const bool fp4 = kind == GEMM_UP_FP4 || kind == GEMM_DOWN_FP4;
-    if (fp4 && (p.K % 64 != 0 || bn != 256)) return hipErrorInvalidValue;
+    if (fp4 && (p.K % 64 != 0 || bn != 256 || bm != 256)) return hipErrorInvalidValue;
     const int64_t ntn = (p.N + bn - 1) / bn;
     const int64_t gn = ntn < 8 ? ntn : 8, gm = 32 / gn;
     const int64_t ngn = (ntn + gn - 1) / gn;
@@ -969,36 +1005,51 @@ hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn,
     int64_t gsz = 32;  // tiles per group (weight-gradient GEMMs on 256 columns: 16)
     if (group_k) {
         if (p.M % 8 != 0 || p.M <= 0) return hipErrorInvalidValue;
-        const int64_t ntm = (p.M + BM - 1) / BM;
+        const int64_t ntm = (p.M + bm - 1) / bm;
         if (bn == 256) gsz = 16;
         const int64_t gmk = gsz / gn;
         groups = (int64_t)p.E * ((ntm + gmk - 1) / gmk) * ngn;
     } else {
         if (p.K % (bn == 256 && !fp4 ? 64 : 32) != 0) return hipErrorInvalidValue;
-        // sum_e ceil(cnt_e / BM) <= ceil(slots / BM) + E - 1
-        const int64_t mtiles = (int64_t)(p.slots + BM - 1) / BM + p.E;
+        // sum_e ceil(cnt_e / bm) <= ceil(slots / bm) + E - 1
+        const int64_t mtiles = (int64_t)(p.slots + bm - 1) / bm + p.E;
         groups = ((mtiles + gm - 1) / gm) * ngn;
     }
     // whole rounds of 8 XCDs x 32 workgroups keep the block -> tile map a bijection
     int64_t grid = (groups * gsz + 255) / 256 * 256;
+    GemmParams q = p;
+    q.xcd_runs = 0;
+    if (!group_k && !fp4) {
+        // every tile resident at once (two workgroups per CU below 256 x 256):
+        // 8 equal runs of tiles, one per XCD (at most 8 * ceil(tiles / 8) blocks)
+        const int64_t mt_max = (int64_t)(p.slots + bm - 1) / bm + p.E;
+        const int64_t tiles = mt_max * ntn;
+        const int64_t slots_resident = (int64_t)cu_count() * (bn == 256 && bm == 256 ? 1 : 2);
+        if (tiles <= slots_resident) {
+            q.xcd_runs = 1;
+            grid = (tiles + 7) / 8 * 8;
+        }
+    }
     // split-K tail (GEMM_DOWN / GEMM_DX on 256-column tiles): its parts are
     // the workgroups after the whole rounds, at most `resident` of them.
-    const bool split = (kind == GEMM_DOWN || kind == GEMM_DX) && bn == 256 && p.part != nullptr &&
+    const bool split = (kind == GEMM_DOWN || kind == GEMM_DX) && bn == 256 && bm == 256 && p.part != nullptr && !q.xcd_runs &&
                        p.resident > 0 && p.resident % 256 == 0;
     if (split) grid += p.resident;
     if (grid <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     const unsigned g = (unsigned)grid;
-#define TMT_BN(KIND_, DUAL_) \
-    (bn == 256 ? launch_kind<KIND_, DUAL_, 256>(p, g, s) : launch_kind<KIND_, DUAL_, 128>(p, g, s))
+#define TMT_BN(KIND_, DUAL_)                                    \
+    (bn == 256 ? launch_kind<KIND_, DUAL_, 256>(q, g, s)        \
+     : bm == 256 ? launch_kind<KIND_, DUAL_, 128>(q, g, s)      \
+                 : launch_kind<KIND_, DUAL_, 128, 2, 128>(q, g, s))
     if (split) {
         // bn == 256 here, so launch_kind runs the 256-column kernel
-        hipError_t err = kind == GEMM_DOWN ? launch_kind<GEMM_DOWN, false, 256>(p, g, s)
-                                           : launch_kind<GEMM_DX, false, 256>(p, g, s);
+        hipError_t err = kind == GEMM_DOWN ? launch_kind<GEMM_DOWN, false, 256>(q, g, s)
+                                           : launch_kind<GEMM_DX, false, 256>(q, g, s);
         if (err != hipSuccess) return err;
         static_assert(Ring<GEMM_DOWN, 256>::BK == Ring<GEMM_DX, 256>::BK, "one split plan for DOWN and DX");
         // 4 workgroups per CU: the (tile, 8-row slab) items are short and latency-bound
-        split_fixup_kernel<Ring<GEMM_DOWN, 256>::BK, 256><<<p.resident * 4, 256, 0, s>>>(p);
+        split_fixup_kernel<Ring<GEMM_DOWN, 256>::BK, 256><<<p.resident * 4, 256, 0, s>>>(q);
         return hipGetLastError();
     }
     switch (kind) {
@@ -1009,15 +1060,15 @@ hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn,
         case GEMM_DW_DOWN: return TMT_BN(GEMM_DW_DOWN, false);
         case GEMM_DW_UP: return TMT_BN(GEMM_DW_UP, false);
         case GEMM_UP_FP4:
-            return dual ? launch_kind<GEMM_UP_FP4, true, 256>(p, g, s) : launch_kind<GEMM_UP_FP4, false, 256>(p, g, s);
-        case GEMM_DOWN_FP4: return launch_kind<GEMM_DOWN_FP4, false, 256>(p, g, s);
+            return dual ? launch_kind<GEMM_UP_FP4, true, 256>(q, g, s) : launch_kind<GEMM_UP_FP4, false, 256>(q, g, s);
+        case GEMM_DOWN_FP4: return launch_kind<GEMM_DOWN_FP4, false, 256>(q, g, s);
         default: return hipErrorInvalidValue;
     }
 #undef TMT_BN
 }
 
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s) {
-    return launch_gemm_bn(kind, dual, p, gemm_tile_n(kind), s);
+    return launch_gemm_tile(kind, dual, p, gemm_tile(kind, p), s);
 }
 
 }  // namespace tmt

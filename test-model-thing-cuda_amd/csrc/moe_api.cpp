@@ -258,7 +258,7 @@ Sizes plan(const tmt_moe_desc* user, tmt_moe* m) {
     size_t o_dXg = bwd ? W.add(TK * D * 2) : 0;
     size_t o_Xg = bwd ? W.add(TK * D * 2) : 0;
     size_t o_dl = bwd ? W.add(T * E * 4) : 0;
-    size_t o_dwr = bwd ? W.add((size_t)router_dw_chunks((int)T) * E * D * 4) : 0;
+    size_t o_dwr = bwd ? W.add((size_t)router_dw_chunks_max((int)T, (int)E, (int)D) * E * D * 4) : 0;
     size_t o_dH = bwd ? W.add(T * D * 2) : 0;
     // Split-K tail of the tiled GEMM_DOWN / GEMM_DX (decode-sized handles never tile).
     const bool split = d->weight_format == TMT_MOE_WEIGHTS_BF16 && T > kSkinnyMaxTokens;
@@ -698,7 +698,7 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
         // With T == 0 the partial pass sums no rows and writes zeros.
         RouterDwParams rw{};
         rw.dlogits = m->dlogits; rw.X = X; rw.T = T; rw.d = d; rw.E = E;
-        rw.nchunks = router_dw_chunks(T); rw.partial = m->dwr_partial; rw.dWr = dWr;
+        rw.nchunks = router_dw_chunks(T, E, d); rw.partial = m->dwr_partial; rw.dWr = dWr;
         LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_router_dw(rw, s));
     }
     // the scatter's fused LayerNorm backward needs the row width of the

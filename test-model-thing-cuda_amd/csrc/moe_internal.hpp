@@ -139,6 +139,9 @@ struct GemmParams {
     // Set by the launcher: launch-order blocks of the tile map (persistent
     // grouped GEMMs loop over them).
     int vblocks;
+    // Set by the launcher for activation GEMMs whose tiles all run at once:
+    // the (M tile, N tile) list is cut into 8 equal runs, one per XCD.
+    int xcd_runs;
 };
 hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_t s);
 // Rows of an activation-GEMM tile, and the fp32 partial buffer the split-K
@@ -146,8 +149,13 @@ hipError_t launch_gemm(GemmKind kind, bool dual, const GemmParams& p, hipStream_
 constexpr int kGemmTileRows = 256;
 inline size_t gemm_split_floats(int resident) { return (size_t)resident * kGemmTileRows * 256; }
 int cu_count();  // compute units of the current device (cached per device)
-// Same with an explicit tile width (256, or 128 = two workgroups per CU).
-hipError_t launch_gemm_bn(GemmKind kind, bool dual, const GemmParams& p, int bn, hipStream_t s);
+// Same with an explicit tile shape: 256 x 256 (one workgroup per CU),
+// 256 x 128 or 128 x 128 (two workgroups per CU; bf16 kinds only).
+struct GemmTile {
+    int m, n;
+};
+GemmTile gemm_tile(GemmKind kind, const GemmParams& p);  // the shape launch_gemm picks
+hipError_t launch_gemm_tile(GemmKind kind, bool dual, const GemmParams& p, GemmTile tile, hipStream_t s);
 
 // Decode-sized forward GEMMs (GEMM_UP / GEMM_DOWN, bf16 weights) for
 // T <= kSkinnyMaxTokens tokens: every expert then owns at most T rows.
@@ -297,7 +305,8 @@ struct RouterDwParams {
     float* partial;          // [nchunks][E][d]
     float* dWr;              // [E][d]
 };
-int router_dw_chunks(int T);
+int router_dw_chunks(int T, int E, int d);
+int router_dw_chunks_max(int max_tokens, int E, int d);
 hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s);
 
 struct ScatterParams {

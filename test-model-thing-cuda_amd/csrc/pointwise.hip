@@ -623,13 +623,31 @@ hipError_t launch_combine_bwd(const CombineBwdParams& p, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Chunks of at most kDwRows rows (the LDS-staged dlogits block).
-int router_dw_chunks(int T) {
-    const int c = (T + kDwRows - 1) / kDwRows;
-    return c < 1 ? 1 : c;
+// Row chunks of pass 1: at most kDwRows rows each (the LDS-staged dlogits
+// block), and, where T is small, enough chunks that the pass has about
+// kDwMinBlocks workgroups (chunks of at least kDwMinRows rows).
+constexpr int kDwMinBlocks = 512, kDwMinRows = 16;
+static int router_dw_blocks_per_chunk(int E, int d) {
+    return ((d + kDwCols - 1) / kDwCols) * ((E + kDwExperts - 1) / kDwExperts);
+}
+int router_dw_chunks(int T, int E, int d) {
+    if (T <= 0) return 1;
+    const int want = (kDwMinBlocks + router_dw_blocks_per_chunk(E, d) - 1) / router_dw_blocks_per_chunk(E, d);
+    int rows = (T + want - 1) / want;
+    rows = rows < kDwMinRows ? kDwMinRows : rows > kDwRows ? kDwRows : rows;
+    return (T + rows - 1) / rows;
+}
+// router_dw_chunks(T, E, d) <= this for every T <= max_tokens: chunks of
+// fewer than kDwRows rows number at most `want`, full-size chunks at most
+// ceil(max_tokens / kDwRows).
+int router_dw_chunks_max(int max_tokens, int E, int d) {
+    const int want = (kDwMinBlocks + router_dw_blocks_per_chunk(E, d) - 1) / router_dw_blocks_per_chunk(E, d);
+    const int c = (max_tokens + kDwRows - 1) / kDwRows;
+    return std::max(1, std::max(c, want));
 }
 
 hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s) {
+    if (p.nchunks < 1 || (int64_t)p.nchunks * kDwRows < p.T) return hipErrorInvalidValue;
     dim3 grid1(p.nchunks, (p.d + kDwCols - 1) / kDwCols, (p.E + kDwExperts - 1) / kDwExperts);
     router_dw_partial_kernel<<<grid1, kThreads, 0, s>>>(p);
     const int64_t n = (int64_t)p.E * p.d;
@@ -648,6 +666,7 @@ constexpr int kScatterRowsPerWave = 4;
 // Rows per workgroup of the router variant: 32 gives 1024 workgroups at
 // T = 32768, four per CU (LDS: E*d*2 bytes of Wr + 32*E*4 of dlogits).
 constexpr int kScatterRowsRouter = 32;
+constexpr int kScatterRowsRouterMin = 8;
 template <bool ROUTER, int K, bool WLDS>
 __global__ __launch_bounds__(kThreads) void scatter_rows_kernel(ScatterParams p, int rows_per_block) {
     extern __shared__ uint4 smem_w[];
@@ -996,7 +1015,11 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
     if (ln && !(wlds && p.E >= kRedOnWrExperts)) lds += (size_t)3 * 2 * p.d * 4;
     const int ni = ln ? (p.d + 511) / 512 : 0;
     if (ni == 0) {
-        const int rrows = router ? kScatterRowsRouter : 4 * kScatterRowsPerWave;
+        // router variant: fewer rows per workgroup while that keeps the grid
+        // under 512 workgroups (small T: each wave's chain of chunk loads is
+        // the time, so more, shorter workgroups finish sooner)
+        int rrows = router ? kScatterRowsRouter : 4 * kScatterRowsPerWave;
+        while (router && rrows > kScatterRowsRouterMin && (p.T + rrows - 1) / rrows < 512) rrows /= 2;
         const int grid = (p.T + rrows - 1) / rrows;
         const size_t rlds = router ? wr_lds + (size_t)rrows * p.E * 4 : 0;
         switch (p.K * 2 + (router ? 1 : 0)) {

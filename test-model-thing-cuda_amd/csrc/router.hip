@@ -331,8 +331,9 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanParams p) {
     const int tid = threadIdx.x;
     const int E = p.E, nblk = p.nblk;
 
-    // 1) per (segment, expert) sums of the block histograms
-    const int S = 1024 / E;
+    // 1) per (segment, expert) sums of the block histograms (no more
+    // segments than blocks: the serial scans of step 2 walk every segment)
+    const int S = max(1, min(1024 / E, nblk));
     const int chunk = (nblk + S - 1) / S;
     // (Loads in batches of 8 at clamped addresses, added in ascending order:
     // one memory round trip per batch instead of one per block.)
@@ -351,7 +352,7 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanParams p) {
     }
     // 1b) per (segment, statistic) sums of the block statistics
     const int E1 = E + 1;
-    const int S2 = 1024 / E1;
+    const int S2 = max(1, min(1024 / E1, nblk));
     const int chunk2 = (nblk + S2 - 1) / S2;
     if (tid < S2 * E1) {
         const int q = tid % E1, seg = tid / E1;
