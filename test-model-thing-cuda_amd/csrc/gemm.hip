@@ -938,20 +938,24 @@ __global__ __launch_bounds__(256) void split_fixup_kernel(GemmParams p) {
 // Tile depth and ring per kind and tile width: split rings of K = 64 for the
 // activation GEMMs on 256 columns; K = 32 rings otherwise (4 stages of 32 KiB
 // at 256 columns, 3 of 24 KiB at 128 columns with two workgroups per CU).
-// 128 x 128 tiles: 4 stages of K = 32 (64 KiB, the size of the epilogue's
-// staging anyway), two workgroups per CU.
-template <int KIND, int BN, int TBM = BM>
+// 128 x 128 tiles (two workgroups per CU, 64 KiB each, the size of the
+// epilogue's staging anyway): 4 stages of K = 32, or with K64 2 stages of
+// K = 64, whose 128-byte row segments the CU's load path takes at twice the
+// rate of 64-byte ones (reference profile shape, K = 1280: up GEMM 25
+// against 30 us; at K = 256 the deeper K = 32 ring is as fast or faster).
+template <int KIND, int BN, int TBM = BM, bool K64 = false>
 struct Ring {
     static constexpr bool split = split_ring<KIND, 64, BN, 2, TBM>();
-    static constexpr int BK = split ? 64 : 32;
-    static constexpr int NST = split ? 3 : (BN == 256 || TBM == 128 ? 4 : 3);
+    static constexpr bool k64 = K64 && TBM == 128;
+    static constexpr int BK = split || k64 ? 64 : 32;
+    static constexpr int NST = split ? 3 : k64 ? 2 : (BN == 256 || TBM == 128 ? 4 : 3);
 };
 
 // grid: the launch-order blocks of the tile map. Persistent kinds run
 // min(grid, CUs rounded down to a multiple of 8) workgroups over them.
-template <int KIND, bool DUAL, int BN, int NWM = 2, int TBM = BM>
+template <int KIND, bool DUAL, int BN, int NWM = 2, int TBM = BM, bool K64 = false>
 hipError_t launch_kind(const GemmParams& p, unsigned grid, hipStream_t s) {
-    using R = Ring<KIND, BN, TBM>;
+    using R = Ring<KIND, BN, TBM, K64>;
     GemmParams q = p;
     q.vblocks = (int)grid;
     unsigned g = grid;
@@ -986,7 +990,10 @@ static int64_t tiles_256(GemmKind kind, const GemmParams& p) {
 
 GemmTile gemm_tile(GemmKind kind, const GemmParams& p) {
     if (kind == GEMM_UP_FP4 || kind == GEMM_DOWN_FP4) return GemmTile{256, 256};
-    if (2 * tiles_256(kind, p) < cu_count()) return GemmTile{128, 128};
+    if (2 * tiles_256(kind, p) < cu_count()) {
+        const bool group_k = kind == GEMM_DW_DOWN || kind == GEMM_DW_UP;
+        return GemmTile{128, 128, !group_k && p.K % 64 == 0 && p.K >= 512};
+    }
     return GemmTile{256, 256};
 }
 
@@ -995,6 +1002,8 @@ hipError_t launch_gemm_tile(GemmKind kind, bool dual, const GemmParams& p, GemmT
     if (p.N % 8 != 0 || p.N <= 0) return hipErrorInvalidValue;
     if (bn != 256 && bn != 128) return hipErrorInvalidValue;
     if (bm != 256 && !(bm == 128 && bn == 128)) return hipErrorInvalidValue;
+    if (tile.k64 && (bm != 128 || p.K % 64 != 0 || kind == GEMM_DW_DOWN || kind == GEMM_DW_UP))
+        return hipErrorInvalidValue;
     const bool group_k = kind == GEMM_DW_DOWN || kind == GEMM_DW_UP;
     const bool fp4 = kind == GEMM_UP_FP4 || kind == GEMM_DOWN_FP4;
     if (fp4 && (p.K % 64 != 0 || bn != 256 || bm != 256)) return hipErrorInvalidValue;
@@ -1038,10 +1047,11 @@ hipError_t launch_gemm_tile(GemmKind kind, bool dual, const GemmParams& p, GemmT
     if (grid <= 0) return hipSuccess;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
     const unsigned g = (unsigned)grid;
-#define TMT_BN(KIND_, DUAL_)                                    \
-    (bn == 256 ? launch_kind<KIND_, DUAL_, 256>(q, g, s)        \
-     : bm == 256 ? launch_kind<KIND_, DUAL_, 128>(q, g, s)      \
-                 : launch_kind<KIND_, DUAL_, 128, 2, 128>(q, g, s))
+#define TMT_BN(KIND_, DUAL_)                                      \
+    (bn == 256     ? launch_kind<KIND_, DUAL_, 256>(q, g, s)      \
+     : bm == 256   ? launch_kind<KIND_, DUAL_, 128>(q, g, s)      \
+     : !tile.k64   ? launch_kind<KIND_, DUAL_, 128, 2, 128>(q, g, s) \
+                   : launch_kind<KIND_, DUAL_, 128, 2, 128, true>(q, g, s))
     if (split) {
         // bn == 256 here, so launch_kind runs the 256-column kernel
         hipError_t err = kind == GEMM_DOWN ? launch_kind<GEMM_DOWN, false, 256>(q, g, s)

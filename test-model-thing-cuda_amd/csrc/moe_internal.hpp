@@ -153,6 +153,7 @@ int cu_count();  // compute units of the current device (cached per device)
 // 256 x 128 or 128 x 128 (two workgroups per CU; bf16 kinds only).
 struct GemmTile {
     int m, n;
+    bool k64 = false;  // 128 x 128 tiles: 2 stages of K = 64 instead of 4 of K = 32
 };
 GemmTile gemm_tile(GemmKind kind, const GemmParams& p);  // the shape launch_gemm picks
 hipError_t launch_gemm_tile(GemmKind kind, bool dual, const GemmParams& p, GemmTile tile, hipStream_t s);
