@@ -474,13 +474,16 @@ int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* W
     sp.blkcnt = m->blkcnt; sp.blkstat = m->blkstat; sp.nblk = nblk; sp.T = T; sp.E = E; sp.K = K;
     sp.counts = m->counts; sp.offsets = m->offsets; sp.blkbase = m->blkbase; sp.order = m->order;
     sp.stats = m->stats;
-    LAUNCH(TMT_MOE_PH_SCAN, launch_scan(sp, s));
-    if (nblk > 0) {
-        PermuteParams pp{};
-        pp.idx = m->idx; pp.blkbase = m->blkbase; pp.T = T; pp.E = E; pp.K = K;
-        pp.rows_per_block = rpb; pp.perm = m->perm; pp.slot_of = m->slot_of;
-        LAUNCH(TMT_MOE_PH_PERMUTE, launch_permute(pp, nblk, s));
+    PermuteParams pp{};
+    pp.idx = m->idx; pp.blkbase = m->blkbase; pp.T = T; pp.E = E; pp.K = K;
+    pp.rows_per_block = rpb; pp.perm = m->perm; pp.slot_of = m->slot_of;
+    if (nblk > 0 && nblk <= kFusedScanBlocks) {
+        // few router blocks: the permutation kernel does the scan itself
+        LAUNCH(TMT_MOE_PH_PERMUTE, launch_permute_scan(pp, sp, nblk, s));
+        return TMT_MOE_OK;
     }
+    LAUNCH(TMT_MOE_PH_SCAN, launch_scan(sp, s));
+    if (nblk > 0) LAUNCH(TMT_MOE_PH_PERMUTE, launch_permute(pp, nblk, s));
     return TMT_MOE_OK;
 }
 

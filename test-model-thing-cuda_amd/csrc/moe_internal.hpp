@@ -75,6 +75,10 @@ struct PermuteParams {
     int32_t* slot_of;        // [T][K] (token, j) -> slot
 };
 hipError_t launch_permute(const PermuteParams& p, int nblk, hipStream_t s);
+// scan + permute in one launch for nblk <= kFusedScanBlocks router blocks
+// (blkbase is not written).
+constexpr int kFusedScanBlocks = 64;
+hipError_t launch_permute_scan(const PermuteParams& p, const ScanParams& sp, int nblk, hipStream_t s);
 
 // T <= kSmallRouteTokens: router + scan + permute in one launch, one block
 // per token row; with several rows the last block to finish (atomic

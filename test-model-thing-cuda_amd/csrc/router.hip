@@ -319,6 +319,41 @@ hipError_t launch_router(const RouterParams& p, int nblk, hipStream_t s) {
     return hipGetLastError();
 }
 
+// From the per-expert totals s_cnt and the summed block statistics s_fsum
+// (E probability sums, then the lse^2 sum): the exclusive offsets into s_off
+// and, with `stats`, the switch aux (moe.cu:456-465) and z-loss mean
+// (moe.cu:268-278). One thread.
+__device__ __forceinline__ void scan_offsets_stats(const ScanParams& p, const int* s_cnt, const float* s_fsum,
+                                                   int* s_off, bool stats) {
+    const int E = p.E;
+    int run = 0;
+    for (int e = 0; e < E; ++e) {
+        s_off[e] = run;
+        run += s_cnt[e];
+    }
+    s_off[E] = run;
+    if (!stats) return;
+    float aux = 0.0f, z = 0.0f;
+    if (p.T > 0) {
+        const float inv_t = 1.0f / (float)p.T;
+        const float inv_tk = 1.0f / ((float)p.T * (float)p.K);
+        for (int e = 0; e < E; ++e) aux += (s_fsum[e] * inv_t) * ((float)s_cnt[e] * inv_tk);
+        aux *= (float)E;
+        z = s_fsum[E] * inv_t;
+    }
+    p.stats[0] = aux;
+    p.stats[1] = z;
+}
+// Expert e's count (in counts and stats) and its place in the descending-
+// count order (ties to the lower index).
+__device__ __forceinline__ void scan_write_expert(const ScanParams& p, const int* s_cnt, int e) {
+    p.counts[e] = s_cnt[e];
+    reinterpret_cast<int32_t*>(p.stats + 2)[e] = s_cnt[e];
+    int rank = 0;
+    for (int q = 0; q < p.E; ++q) rank += (s_cnt[q] > s_cnt[e]) || (s_cnt[q] == s_cnt[e] && q < e);
+    p.order[rank] = e;
+}
+
 // Single workgroup: per-expert totals, exclusive offsets, per-block bases,
 // the aux / z statistics and the descending-count expert order. Every sum is
 // taken in a fixed order, so the statistics are run-to-run deterministic.
@@ -399,35 +434,10 @@ __global__ __launch_bounds__(1024) void scan_kernel(ScanParams p) {
         s_fsum[tid] = run;
     }
     __syncthreads();
-    if (tid == 0) {
-        int run = 0;
-        for (int e = 0; e < E; ++e) {
-            s_off[e] = run;
-            run += s_cnt[e];
-        }
-        s_off[E] = run;
-        // Switch aux (moe.cu:456-465) and z-loss mean (moe.cu:268-278).
-        float aux = 0.0f, z = 0.0f;
-        if (p.T > 0) {
-            const float inv_t = 1.0f / (float)p.T;
-            const float inv_tk = 1.0f / ((float)p.T * (float)p.K);
-            for (int e = 0; e < E; ++e) aux += (s_fsum[e] * inv_t) * ((float)s_cnt[e] * inv_tk);
-            aux *= (float)E;
-            z = s_fsum[E] * inv_t;
-        }
-        p.stats[0] = aux;
-        p.stats[1] = z;
-    }
+    if (tid == 0) scan_offsets_stats(p, s_cnt, s_fsum, s_off, true);
     __syncthreads();
     if (tid <= E) p.offsets[tid] = s_off[tid];
-    if (tid < E) {
-        p.counts[tid] = s_cnt[tid];
-        reinterpret_cast<int32_t*>(p.stats + 2)[tid] = s_cnt[tid];
-        int rank = 0;
-        for (int e = 0; e < E; ++e)
-            rank += (s_cnt[e] > s_cnt[tid]) || (s_cnt[e] == s_cnt[tid] && e < tid);
-        p.order[rank] = tid;
-    }
+    if (tid < E) scan_write_expert(p, s_cnt, tid);
     // 3) per-block bases
     if (tid < S * E) {
         const int e = tid % E, seg = tid / E;
@@ -506,6 +516,109 @@ __global__ __launch_bounds__(kThreads) void permute_kernel(PermuteParams p) {
             p.slot_of[(int64_t)row * K + j] = pos;
         }
     }
+}
+
+// The permutation with the scan folded in, for grids of at most
+// kFusedScanBlocks router blocks: every block adds the block histograms
+// itself (the totals, and the counts of the blocks before it, in ascending
+// block order) to find its own bases, and block 0 writes the counts,
+// offsets, order and statistics (block statistics added in ascending block
+// order). One launch fewer where the scan's single workgroup was mostly
+// launch latency. Slots are the same as scan_kernel + permute_kernel give.
+__global__ __launch_bounds__(kThreads) void permute_scan_kernel(PermuteParams p, ScanParams sp) {
+    __shared__ int s_g[kMaxGroups][kMaxExperts];
+    __shared__ int s_tot[kMaxExperts];
+    __shared__ int s_base[kMaxExperts];
+    __shared__ int s_off[kMaxExperts + 1];
+    __shared__ float s_fsum[kMaxExperts + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = p.K, E = p.E, nblk = sp.nblk, b = blockIdx.x;
+    if (tid < E) {
+        int tot = 0, before = 0;
+        for (int b0 = 0; b0 < nblk; b0 += 8) {
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = sp.blkcnt[(int64_t)min(b0 + u, nblk - 1) * E + tid];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int c = b0 + u < nblk ? v[u] : 0;
+                tot += c;
+                before += b0 + u < b ? c : 0;
+            }
+        }
+        s_tot[tid] = tot;
+        s_base[tid] = before;
+    } else if (b == 0 && tid >= 64 && tid - 64 <= E) {
+        const int q = tid - 64;
+        float run = 0.0f;
+        for (int b0 = 0; b0 < nblk; b0 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = sp.blkstat[(int64_t)min(b0 + u, nblk - 1) * (E + 1) + q];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (b0 + u < nblk) run += v[u];
+        }
+        s_fsum[q] = run;
+    }
+    __syncthreads();
+    if (tid == 0) scan_offsets_stats(sp, s_tot, s_fsum, s_off, b == 0);
+    __syncthreads();
+    if (tid < E) {
+        s_base[tid] += s_off[tid];
+        if (b == 0) scan_write_expert(sp, s_tot, tid);
+    }
+    if (b == 0 && tid <= E) sp.offsets[tid] = s_off[tid];
+    // the permutation (permute_kernel with the block bases from s_base)
+    const int RG = 64 / K;
+    const int pairs = RG * K;
+    const int row_begin = b * p.rows_per_block;
+    const int row_end = min(p.T, row_begin + p.rows_per_block);
+    const int G = (row_end - row_begin + RG - 1) / RG;
+    const int rr = lane / K, j = lane % K;
+    const uint64_t lt_mask = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    for (int g = wave; g < G; g += 4) {
+        const int row = row_begin + g * RG + rr;
+        const bool valid = lane < pairs && row < row_end;
+        const int e = valid ? p.idx[(int64_t)row * K + j] : -1;
+        for (int ee = 0; ee < E; ++ee) {
+            const uint64_t m = __ballot(e == ee);
+            if (lane == ee) s_g[g][ee] = __popcll(m);
+        }
+    }
+    __syncthreads();
+    if (tid < E) {
+        int run = s_base[tid];
+        for (int g = 0; g < G; ++g) {
+            const int c = s_g[g][tid];
+            s_g[g][tid] = run;
+            run += c;
+        }
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += 4) {
+        const int row = row_begin + g * RG + rr;
+        const bool valid = lane < pairs && row < row_end;
+        const int e = valid ? p.idx[(int64_t)row * K + j] : -1;
+        int rank = 0;
+        for (int ee = 0; ee < E; ++ee) {
+            const uint64_t m = __ballot(e == ee);
+            if (e == ee) rank = __popcll(m & lt_mask);
+        }
+        if (valid) {
+            const int pos = s_g[g][e] + rank;
+            p.perm[pos] = row;
+            p.slot_of[(int64_t)row * K + j] = pos;
+        }
+    }
+}
+
+hipError_t launch_permute_scan(const PermuteParams& p, const ScanParams& sp, int nblk, hipStream_t s) {
+    const int RG = 64 / p.K;
+    if ((p.rows_per_block + RG - 1) / RG > kMaxGroups || nblk < 1 || nblk > kFusedScanBlocks || p.E > kMaxExperts)
+        return hipErrorInvalidValue;
+    permute_scan_kernel<<<nblk, kThreads, 0, s>>>(p, sp);
+    return hipGetLastError();
 }
 
 hipError_t launch_permute(const PermuteParams& p, int nblk, hipStream_t s) {
