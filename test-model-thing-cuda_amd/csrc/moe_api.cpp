@@ -697,12 +697,15 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
         // reference's (moe.cu:486-487).
         LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_zero_f32(dWr, d, s));
     }
+    // Without the LayerNorm the scatter's launch also runs the router weight
+    // gradient's second pass (one launch fewer).
+    RouterDwParams rw{};
+    const bool dw_in_scatter = E > 1 && T > 0 && ln == nullptr;
     if (E > 1) {
         // With T == 0 the partial pass sums no rows and writes zeros.
-        RouterDwParams rw{};
         rw.dlogits = m->dlogits; rw.X = X; rw.T = T; rw.d = d; rw.E = E;
         rw.nchunks = router_dw_chunks(T, E, d); rw.partial = m->dwr_partial; rw.dWr = dWr;
-        LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_router_dw(rw, s));
+        LAUNCH(TMT_MOE_PH_ROUTER_DW, launch_router_dw(rw, s, !dw_in_scatter));
     }
     // the scatter's fused LayerNorm backward needs the row width of the
     // LayerNorm itself (a padded handle runs the separate kernels)
@@ -711,6 +714,7 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
         ScatterParams sc{};
         sc.dXg = m->dXg; sc.slot_of = m->slot_of; sc.dlogits = E > 1 ? m->dlogits : nullptr;
         sc.Wr = Wr; sc.T = T; sc.d = d; sc.E = E; sc.K = K; sc.dX = dX;
+        if (dw_in_scatter) sc.dw = rw;
         if (ln_fused) {
             sc.ln_S = ln->S; sc.ln_gamma = ln->gamma; sc.ln_mean = m->ln_mean; sc.ln_rstd = m->ln_rstd;
             sc.ln_dS = ln->dS; sc.ln_partial = m->ln_partial;

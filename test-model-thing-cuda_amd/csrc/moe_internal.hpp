@@ -312,7 +312,9 @@ struct RouterDwParams {
 };
 int router_dw_chunks(int T, int E, int d);
 int router_dw_chunks_max(int max_tokens, int E, int d);
-hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s);
+// reduce = false: pass 1 only; the scatter's launch then runs pass 2
+// (ScatterParams::dw).
+hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s, bool reduce = true);
 
 struct ScatterParams {
     const uint16_t* dXg;     // [TK][d]
@@ -329,6 +331,11 @@ struct ScatterParams {
     const float* ln_rstd;    // [T]
     uint16_t* ln_dS;         // [T][d]
     float* ln_partial;       // [scatter_blocks(T)][2][d] per-block dgamma / dbeta sums
+    // Pass 2 of the router weight gradient (the per-output sum over pass 1's
+    // chunks) run by extra workgroups of the same launch (dw.partial !=
+    // nullptr; only without the LayerNorm): the two are independent, and
+    // one launch fewer shortens a small backward.
+    RouterDwParams dw;
 };
 constexpr int kLnFusedMaxD = 2048;
 constexpr int kScatterRows = 64;  // rows per scatter workgroup (router or LayerNorm variants)

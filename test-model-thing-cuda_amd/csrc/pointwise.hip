@@ -348,10 +348,11 @@ __global__ __launch_bounds__(kThreads) void router_dw_partial_kernel(RouterDwPar
 }
 
 // Pass 2: dWr[e][k] = sum over chunks in ascending order; each thread owns
-// one output and keeps 16 chunk loads in flight.
-__global__ __launch_bounds__(kThreads) void router_dw_reduce_kernel(RouterDwParams p) {
+// one output and keeps 16 chunk loads in flight. Block b of the pass covers
+// outputs [b * kThreads, (b + 1) * kThreads).
+__device__ __forceinline__ void router_dw_reduce_block(const RouterDwParams& p, int b) {
     const int64_t n = (int64_t)p.E * p.d;
-    const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const int64_t i = (int64_t)b * kThreads + threadIdx.x;
     if (i >= n) return;
     float s = 0.0f;
     int c = 0;
@@ -364,6 +365,12 @@ __global__ __launch_bounds__(kThreads) void router_dw_reduce_kernel(RouterDwPara
     }
     for (; c < p.nchunks; ++c) s += p.partial[(int64_t)c * n + i];
     p.dWr[i] = s;
+}
+__global__ __launch_bounds__(kThreads) void router_dw_reduce_kernel(RouterDwParams p) {
+    router_dw_reduce_block(p, blockIdx.x);
+}
+int router_dw_reduce_blocks(const RouterDwParams& p) {
+    return (int)(((int64_t)p.E * p.d + kThreads - 1) / kThreads);
 }
 
 // Gradient of one token row over the lane's 8 columns at c0: the K expert
@@ -649,12 +656,11 @@ int router_dw_chunks_max(int max_tokens, int E, int d) {
     return std::max(1, std::max(c, want));
 }
 
-hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s) {
+hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s, bool reduce) {
     if (p.nchunks < 1 || (int64_t)p.nchunks * kDwRows < p.T) return hipErrorInvalidValue;
     dim3 grid1(p.nchunks, (p.d + kDwCols - 1) / kDwCols, (p.E + kDwExperts - 1) / kDwExperts);
     router_dw_partial_kernel<<<grid1, kThreads, 0, s>>>(p);
-    const int64_t n = (int64_t)p.E * p.d;
-    router_dw_reduce_kernel<<<(unsigned)((n + kThreads - 1) / kThreads), kThreads, 0, s>>>(p);
+    if (reduce) router_dw_reduce_kernel<<<(unsigned)router_dw_reduce_blocks(p), kThreads, 0, s>>>(p);
     return hipGetLastError();
 }
 
@@ -677,6 +683,11 @@ __global__ __launch_bounds__(kThreads) void scatter_rows_kernel(ScatterParams p,
     constexpr bool STAGE = ROUTER && WLDS;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d = p.d, E = p.E;
+    const int nrow_blocks = (p.T + rows_per_block - 1) / rows_per_block;
+    if ((int)blockIdx.x >= nrow_blocks) {  // the router weight gradient's pass 2
+        router_dw_reduce_block(p.dw, blockIdx.x - nrow_blocks);
+        return;
+    }
     const int rbeg = blockIdx.x * rows_per_block;
     const int rend = min(p.T, rbeg + rows_per_block);
     float* s_dl = reinterpret_cast<float*>(smem_w + (STAGE ? E * d / 8 : 0));  // [rows_per_block][E]
@@ -1008,6 +1019,7 @@ hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t s) {
 
 hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
+    if (p.dw.partial != nullptr && (p.ln_S != nullptr || p.dw.nchunks < 1)) return hipErrorInvalidValue;
     const bool router = p.dlogits != nullptr && p.E > 1;
     const bool ln = p.ln_S != nullptr;
     if (ln && p.d > kLnFusedMaxD) return hipErrorInvalidValue;
@@ -1023,7 +1035,8 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s) {
         // the time, so more, shorter workgroups finish sooner)
         int rrows = router ? kScatterRowsRouter : 4 * kScatterRowsPerWave;
         while (router && rrows > kScatterRowsRouterMin && (p.T + rrows - 1) / rrows < 512) rrows /= 2;
-        const int grid = (p.T + rrows - 1) / rrows;
+        // pass 2 of the router weight gradient rides along (extra workgroups)
+        const int grid = (p.T + rrows - 1) / rrows + (p.dw.partial != nullptr ? router_dw_reduce_blocks(p.dw) : 0);
         const size_t rlds = router ? wr_lds + (size_t)rrows * p.E * 4 : 0;
         switch (p.K * 2 + (router ? 1 : 0)) {
 #define TMT_SCATTER_ROWS(KK)                                                                   \
