@@ -124,6 +124,7 @@ struct tmt_moe {
     // activations (U: the single linear's output when hidden = 0, silu'(U)
     // when hidden > 0)
     uint16_t *U, *Aact, *O, *dO, *dU, *dXg, *Xg;
+    uint16_t* wt = nullptr;  // W_up transposed ([E][d][hn]) for the backward's GEMM_DX (nullptr: none)
     // MX handles: activations of the two expert GEMMs as two MXFP6 terms
     uint8_t *xq = nullptr, *xq_scales = nullptr, *aq = nullptr, *aq_scales = nullptr;
     float *dlogits, *dwr_partial;
@@ -256,6 +257,11 @@ Sizes plan(const tmt_moe_desc* user, tmt_moe* m) {
     size_t o_dO = bwd ? W.add(TK * D * 2) : 0;
     size_t o_dU = bwd && h > 0 ? W.add(TK * h * 2) : 0;
     size_t o_dXg = bwd ? W.add(TK * D * 2) : 0;
+    // W_up transposed to [E][d][hn] for GEMM_DX on 256 x 256 tiles (handles
+    // whose largest batch runs it there): the GEMM then reads both operands
+    // K-contiguous, as GEMM_DOWN does
+    const bool wt = bwd && 2 * ((TK + 255) / 256) * ((D + 255) / 256) >= cu_count();
+    size_t o_wt = wt ? W.add(E * hn * D * 2) : 0;
     size_t o_Xg = bwd ? W.add(TK * D * 2) : 0;
     size_t o_dl = bwd ? W.add(T * E * 4) : 0;
     size_t o_dwr = bwd ? W.add((size_t)router_dw_chunks_max((int)T, (int)E, (int)D) * E * D * 4) : 0;
@@ -324,6 +330,7 @@ Sizes plan(const tmt_moe_desc* user, tmt_moe* m) {
         m->dO = bwd ? (uint16_t*)(w + o_dO) : nullptr;
         m->dU = bwd ? (h > 0 ? (uint16_t*)(w + o_dU) : m->dO) : nullptr;  // h == 0: combine_bwd writes dU
         m->dXg = bwd ? (uint16_t*)(w + o_dXg) : nullptr;
+        m->wt = wt ? (uint16_t*)(w + o_wt) : nullptr;
         m->Xg = bwd ? (uint16_t*)(w + o_Xg) : nullptr;
         m->dlogits = bwd ? (float*)(w + o_dl) : nullptr;
         m->dwr_partial = bwd ? (float*)(w + o_dwr) : nullptr;
@@ -690,7 +697,22 @@ int run_backward(tmt_moe* m, hipStream_t s, const uint16_t* dY, const uint16_t* 
         for (int e = 0; e < E; ++e) dx.w[e] = W_up[e];
         dx.ldb = d;
         dx.part = m->split; dx.resident = m->resident;
-        LAUNCH(TMT_MOE_PH_GEMM_DX, launch_gemm(GEMM_DX, false, dx, s));
+        if (m->wt != nullptr && gemm_tile(GEMM_DX, dx).m == 256) {
+            // dXg = dU W_up as GEMM_DOWN over W_up^T: a transpose of the
+            // weights (E * hn * d * 2 bytes each way) buys K-contiguous B
+            // tiles for the GEMM (ds_read_b128 instead of the transposing
+            // 8-byte reads, half the LDS read instructions)
+            TransposeParams tp{};
+            for (int e = 0; e < E; ++e) tp.src[e] = W_up[e];
+            tp.ld_src = d; tp.rows = hn; tp.cols = d; tp.dst = m->wt;
+            LAUNCH(TMT_MOE_PH_GEMM_DX, launch_transpose_bf16(tp, E, s));
+            GemmParams dt = dx;
+            for (int e = 0; e < E; ++e) dt.w[e] = m->wt + (int64_t)e * d * hn;
+            dt.ldb = hn;
+            LAUNCH(TMT_MOE_PH_GEMM_DX, launch_gemm(GEMM_DOWN, false, dt, s));
+        } else {
+            LAUNCH(TMT_MOE_PH_GEMM_DX, launch_gemm(GEMM_DX, false, dx, s));
+        }
     }
     if (E == 1 && dWr) {
         // The dense path has no router; its gradient slot is zeroed like the

@@ -346,6 +346,15 @@ hipError_t launch_scatter(const ScatterParams& p, hipStream_t s);
 hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t s);
 // out = bf16(in), round to nearest even.
 hipError_t launch_f32_to_bf16(const float* in, uint16_t* out, int64_t n, hipStream_t s);
+// dst + e * rows * cols = src[e]^T ([rows][cols] bf16, row stride ld_src ->
+// [cols][rows]); rows and cols multiples of 64.
+struct TransposeParams {
+    const uint16_t* src[kMaxExperts];
+    int64_t ld_src;
+    int rows, cols;
+    uint16_t* dst;
+};
+hipError_t launch_transpose_bf16(const TransposeParams& p, int nmat, hipStream_t s);
 
 // ------------------------------------------------------------------ norm --
 struct LayerNormParams {

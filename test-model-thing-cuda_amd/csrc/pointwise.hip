@@ -1010,6 +1010,55 @@ hipError_t launch_pad_copy(const PadParams& p, int nmat, int elem_bytes, hipStre
     return hipGetLastError();
 }
 
+namespace {
+// dst[e] = src[e]^T for bf16 matrices [rows][cols] -> [cols][rows], through
+// 64 x 64 LDS tiles: 16-byte loads along the source rows, 16-byte stores
+// along the destination rows (both coalesced), one tile per workgroup.
+__global__ __launch_bounds__(kThreads) void transpose_bf16_kernel(TransposeParams p) {
+    __shared__ uint16_t t[64][64 + 2];
+    const int e = blockIdx.z;
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+    const uint16_t* src = p.src[e];
+    uint16_t* dst = p.dst + (int64_t)e * p.rows * p.cols;
+    const int tx = threadIdx.x & 7, ty = threadIdx.x >> 3;  // 8 lanes x 16 bytes per 64-element row
+    uint4 v[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = r0 + ty + 32 * i;
+        v[i] = r < p.rows ? *reinterpret_cast<const uint4*>(src + (int64_t)r * p.ld_src + c0 + tx * 8) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            t[ty + 32 * i][tx * 8 + 2 * q] = (uint16_t)(w[q] & 0xffff);
+            t[ty + 32 * i][tx * 8 + 2 * q + 1] = (uint16_t)(w[q] >> 16);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = ty + 32 * i;  // destination row (source column c0 + c)
+        uint32_t w[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            w[q] = (uint32_t)t[tx * 8 + 2 * q][c] | ((uint32_t)t[tx * 8 + 2 * q + 1][c] << 16);
+        const int rr = r0 + tx * 8;  // destination columns rr .. rr + 7
+        if (c0 + c < p.cols && rr < p.rows)
+            *reinterpret_cast<uint4*>(dst + (int64_t)(c0 + c) * p.rows + rr) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+}  // namespace
+
+hipError_t launch_transpose_bf16(const TransposeParams& p, int nmat, hipStream_t s) {
+    if (nmat < 0 || nmat > kMaxExperts || p.rows % 64 != 0 || p.cols % 64 != 0 || p.ld_src < p.cols)
+        return hipErrorInvalidValue;
+    if (nmat == 0 || p.rows == 0 || p.cols == 0) return hipSuccess;
+    transpose_bf16_kernel<<<dim3(p.cols / 64, p.rows / 64, nmat), kThreads, 0, s>>>(p);
+    return hipGetLastError();
+}
+
 hipError_t launch_zero_f32(float* p, int64_t n, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     const int64_t blocks = std::min<int64_t>((n + kThreads - 1) / kThreads, 1024);
