@@ -462,7 +462,10 @@ int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* W
         LAUNCH(TMT_MOE_PH_ROUTER, launch_route_small(r.rp, r.sp, r.pp, picks_only ? nullptr : m->ticket, s));
         return TMT_MOE_OK;
     }
-    const int rpb = router_rows_per_block(T, E, K);
+    // without the LayerNorm the logits come from the matrix cores (with the
+    // canonical order for rows whose ranking that could change)
+    const bool mfma = ln == nullptr && router_mfma_fits(T, E, K, d);
+    const int rpb = mfma ? kMfmaRouterRows : router_rows_per_block(T, E, K);
     const int nblk = T > 0 ? (T + rpb - 1) / rpb : 0;
     if (nblk > m->nblk_max) return fail(TMT_MOE_EINVAL, "internal: router block count %d > %d", nblk, m->nblk_max);
     if (nblk > 0) {
@@ -475,7 +478,7 @@ int route(tmt_moe* m, hipStream_t s, int T, const uint16_t* X, const uint16_t* W
             rp.X = ln->S; rp.ln_gamma = ln->gamma; rp.ln_beta = ln->beta;
             rp.ln_H = m->H; rp.ln_mean = m->ln_mean; rp.ln_rstd = m->ln_rstd;
         }
-        LAUNCH(TMT_MOE_PH_ROUTER, launch_router(rp, nblk, s));
+        LAUNCH(TMT_MOE_PH_ROUTER, mfma ? launch_router_mfma(rp, nblk, s) : launch_router(rp, nblk, s));
     }
     ScanParams sp{};
     sp.blkcnt = m->blkcnt; sp.blkstat = m->blkstat; sp.nblk = nblk; sp.T = T; sp.E = E; sp.K = K;

@@ -54,6 +54,13 @@ constexpr size_t kRouterWrLdsBytes = 65536;
 inline bool router_wr_in_lds(int E, int d) { return (size_t)E * (size_t)d * 2 <= kRouterWrLdsBytes; }
 int router_rows_per_wave(int E);
 hipError_t launch_router(const RouterParams& p, int nblk, hipStream_t s);
+// Large routed batches without the LayerNorm (router_mfma_fits): logits on
+// the matrix cores, rows whose top-k ranking the MFMA rounding could change
+// recomputed in the canonical order (picks bit-exact; logits within a few
+// ulp elsewhere). rows_per_block must be kMfmaRouterRows.
+constexpr int kMfmaRouterRows = 128;
+bool router_mfma_fits(int T, int E, int K, int d);
+hipError_t launch_router_mfma(const RouterParams& p, int nblk, hipStream_t s);
 
 struct ScanParams {
     const int32_t* blkcnt;   // [nblk][E]

@@ -279,6 +279,404 @@ __global__ __launch_bounds__(64 * NW) void router_kernel(RouterParams p) {
     }
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// ---- router logits on the matrix cores -----------------------------------
+// Large routed batches without the LayerNorm (E <= 32): wave w of a 4-wave
+// block takes rows 32w .. 32w + 31 of the block's kMfmaRouterRows and
+// computes their logits with v_mfma_f32_32x32x16_bf16 (X rows as the A
+// operand, Wr rows as B, fp32 accumulation), together with
+// A = sum_k |x_k w_k| from a second MFMA over the operands with their sign
+// bits cleared. Wr sits in LDS for the block (rows padded by 16 bytes); X
+// streams through a per-wave LDS buffer in 128-element chunks, loaded as
+// 4 rows x 256 bytes per instruction (the MFMA's own layout, 32 rows x 32
+// bytes per instruction, kept the CU's load path busy for 37 us per block
+// at c3) and one chunk ahead in registers.
+// The MFMA sums the same exact bf16 products as the canonical order does,
+// only in another order, so a logit differs from the canonical one by at
+// most
+//   delta = (4 (5d/64 + 24) A + 8 (|logit| + |bias|)) u,  u = 2^-24,
+// for every expert of the row: the canonical order rounds each product at
+// most d/64 + 6 times before the bias, the MFMA path at most d/16 + 16
+// times even with truncating arithmetic (twice the error per rounding),
+// and the factor 4 covers both with room. Where the MFMA logits of the
+// top K + 1 picks are more than 2 delta apart, the canonical logits rank the
+// experts the same way, so the picks, their order and everything built from
+// them (counts, offsets, permutation) are exactly the canonical router's;
+// the row keeps the MFMA logits, and probabilities, lse and gates computed
+// from them (within a few ulp of the canonical ones). A row with a closer
+// pair, or with a non-finite value, is flagged and recomputed in the
+// canonical order (the lane partials and full butterfly of token_logits,
+// then softmax_topk): bit for bit what router_kernel writes. Flagged rows
+// go to the waves in ascending row order, so the block statistics are
+// deterministic.
+// One wave-wide 16-byte-per-lane load from global memory into LDS at
+// lds_base + 16 * lane (lds_base wave-uniform); M0 is declared clobbered.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_lds(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "m0", "memory");
+}
+#pragma clang diagnostic pop
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+template <int EP>
+__global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
+    extern __shared__ uint4 smem_rm[];
+    __shared__ int s_cnt[kMaxExperts];
+    __shared__ float s_stat[4][kMaxExperts + 1];
+    __shared__ float s_fl[4][kMaxExperts + 1];
+    __shared__ uint32_t s_flag[4];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int E = p.E, d = p.d, K = p.K;
+    const int wpitch = d + 8;  // bf16 elements per staged Wr row
+    uint16_t* sw = reinterpret_cast<uint16_t*>(smem_rm);  // [32][wpitch]
+    // this wave's two X buffers, [32 rows][128] bf16 each: 16-byte chunk q of
+    // row r sits at chunk q ^ (r & 15), so the 32 rows that one fragment read
+    // touches spread over the banks
+    uint16_t* sx = sw + 32 * wpitch + wave * 2 * 32 * 128;
+    if (tid < kMaxExperts) s_cnt[tid] = 0;
+    {
+        // Wr's E rows (rows E .. 31 zero: their columns are unused). Each
+        // block starts at its own offset into the rows, so that the blocks,
+        // which all read the same few KiB at kernel start, do not all ask
+        // the same L2 lines for them at once.
+        const int vpr = d / 8;  // 16-byte vectors per row
+        const int nv = E * vpr;
+        const int rot = (int)((blockIdx.x * 97u) % (unsigned)nv);
+        for (int i0 = tid; i0 < nv; i0 += 8 * 256) {
+            uint4 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                int i = min(i0 + u * 256, nv - 1) + rot;
+                i = i >= nv ? i - nv : i;
+                v[u] = *reinterpret_cast<const uint4*>(p.Wr + (int64_t)i * 8);  // row i / vpr, vector i % vpr
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (i0 + u * 256 < nv) {
+                    int i = i0 + u * 256 + rot;
+                    i = i >= nv ? i - nv : i;
+                    const int n = i / vpr, c = i - n * vpr;
+                    *reinterpret_cast<uint4*>(sw + n * wpitch + 8 * c) = v[u];
+                }
+            }
+        }
+        for (int i = tid; i < (32 - E) * vpr; i += 256) {
+            const int n = E + i / vpr, c = i % vpr;
+            *reinterpret_cast<uint4*>(sw + n * wpitch + 8 * c) = make_uint4(0, 0, 0, 0);
+        }
+    }
+    const int row_begin = blockIdx.x * kMfmaRouterRows;
+    const int row_end = min(p.T, row_begin + kMfmaRouterRows);
+    const int rl = lane & 31, hi = lane >> 5;
+    const int row = row_begin + wave * 32 + rl;
+    const bool rvalid = row < row_end;
+    // X loads: load i of a chunk fills rows 4i .. 4i + 3 of the wave's 32
+    // (lane -> row 4i + lane / 16, physical chunk lane % 16, which holds the
+    // row's logical chunk (lane % 16) ^ (row & 15)): 4 rows x 256 bytes per
+    // load instead of the MFMA layout's 32 rows x 32 bytes
+    const uint16_t* xsrc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int r = 4 * i + (lane >> 4);
+        const int rr = row_begin + wave * 32 + r < row_end ? row_begin + wave * 32 + r : row_begin;  // clamped
+        xsrc[i] = p.X + (int64_t)rr * d + 8 * ((lane & 15) ^ (r & 15));
+    }
+    const uint32_t sx0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)sx;
+    auto dma_chunk = [&](int c, int buf) {
+        const int k0 = min(c, d / 128 - 1) * 128;  // clamped: a chunk past the end reloads the last
+#pragma unroll
+        for (int i = 0; i < 8; ++i) dma16_lds(xsrc[i] + k0, sx0 + (uint32_t)(buf * 32 * 128 * 2 + i * 1024));
+    };
+    f32x16 acc, aab;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = aab[r] = 0.0f;
+    const uint4 absm = make_uint4(0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu);
+    const int nch = d / 128;  // d % 128 == 0 (launch check)
+    // chunks 0 and 1 in flight; every later chunk is requested into the
+    // buffer its predecessor's predecessor used, once the wave's reads of
+    // that buffer are done (8 loads per chunk: waiting for all but the last
+    // 8 leaves the current chunk in LDS)
+    dma_chunk(0, 0);
+    dma_chunk(1, 1);
+    __syncthreads();  // Wr staged
+    for (int c = 0; c < nch; ++c) {
+        wait_vmcnt<8>();
+        const uint16_t* xb_ = sx + (c & 1) * 32 * 128;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            const int q = (2 * s + hi) ^ (rl & 15);
+            const uint4 xa = *reinterpret_cast<const uint4*>(xb_ + rl * 128 + 8 * q);
+            const uint4 wa = *reinterpret_cast<const uint4*>(sw + rl * wpitch + c * 128 + 16 * s + 8 * hi);
+            const uint4 xb = make_uint4(xa.x & absm.x, xa.y & absm.y, xa.z & absm.z, xa.w & absm.w);
+            const uint4 wb = make_uint4(wa.x & absm.x, wa.y & absm.y, wa.z & absm.z, wa.w & absm.w);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wa),
+                                                           __builtin_bit_cast(bf16x8, xa), acc, 0, 0, 0);
+            aab = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wb),
+                                                           __builtin_bit_cast(bf16x8, xb), aab, 0, 0, 0);
+        }
+        wait_lgkm0();  // this buffer's reads are done before the next load overwrites it
+        dma_chunk(c + 2, c & 1);
+    }
+    wait_vmcnt<0>();  // the clamped extra loads, before the buffers go away
+
+    // ---- softmax, top K + 1, the separation test (lanes l and l ^ 32 share a
+    // row; register r holds expert 8 (r / 4) + 4 (l / 32) + r % 4) ---------
+    auto expert_of = [&](int r) { return 8 * (r >> 2) + 4 * hi + (r & 3); };
+    float v[16];
+    float vmax = -INFINITY, vabs = 0.0f, amax = 0.0f, babs = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int n = expert_of(r);
+        const bool ev = n < E;
+        const float bias = (p.bias != nullptr && ev) ? p.bias[n] : 0.0f;
+        v[r] = p.bias != nullptr ? acc[r] + bias : acc[r];
+        if (ev) {
+            vmax = fmaxf(vmax, v[r]);
+            vabs = fmaxf(vabs, fabsf(v[r]));
+            amax = fmaxf(amax, aab[r]);
+            babs = fmaxf(babs, fabsf(bias));
+        }
+    }
+    vmax = fmaxf(vmax, xor_lane<32>(vmax));
+    vabs = fmaxf(vabs, xor_lane<32>(vabs));
+    amax = fmaxf(amax, xor_lane<32>(amax));
+    babs = fmaxf(babs, xor_lane<32>(babs));
+    float ex[16];
+    float se = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        ex[r] = expert_of(r) < E ? __expf(v[r] - vmax) : 0.0f;
+        se += ex[r];
+    }
+    se += xor_lane<32>(se);  // own + partner: both lanes of the row get the same bits
+    const float lse = vmax + __logf(se);
+    const int rounds = min(K + 1, E);
+    float topv[kMaxTopK + 1];
+    int tope[kMaxTopK + 1];
+    uint32_t selm = 0u;
+#pragma unroll
+    for (int j = 0; j <= kMaxTopK; ++j) {
+        topv[j] = -INFINITY;
+        tope[j] = 0;
+        if (j < rounds) {
+            float bv = -INFINITY;
+            int be = 1 << 20;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int n = expert_of(r);
+                const bool in = n < E && !((selm >> r) & 1u);
+                if (in && (v[r] > bv || (v[r] == bv && n < be))) {
+                    bv = v[r];
+                    be = n;
+                }
+            }
+            const float ov = xor_lane<32>(bv);
+            const int oe = xor_lane<32>(be);
+            if (ov > bv || (ov == bv && oe < be)) {
+                bv = ov;
+                be = oe;
+            }
+            topv[j] = bv;
+            tope[j] = be;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                if (expert_of(r) == be) selm |= 1u << r;
+        }
+    }
+    const float u = 5.9604644775390625e-08f;  // 2^-24
+    const float delta =
+        (4.0f * (5.0f * (float)d / 64.0f + 24.0f) * 1.001f * amax + 8.0f * (vabs + babs)) * u + 1e-30f;
+    bool flag = !(vabs < INFINITY) || !(amax < INFINITY) || !(se > 0.0f);
+#pragma unroll
+    for (int j = 0; j < kMaxTopK; ++j)
+        if (j + 1 < rounds && !(topv[j] - topv[j + 1] > 2.0f * delta)) flag = true;
+    const bool clean = rvalid && !flag;
+
+    // ---- outputs of the rows that keep the MFMA logits -------------------
+    float psum[16];
+    float lsum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) psum[r] = (clean && expert_of(r) < E) ? ex[r] / se : 0.0f;
+    if (clean) {
+        // register r holds expert 8 (r / 4) + 4 hi + r % 4: four consecutive
+        // experts per group of four registers, one 16-byte store each where
+        // E is a multiple of 4 (rows then start 16-byte aligned)
+        float* lrow = p.logits + (int64_t)row * E;
+        float* prow = p.probs + (int64_t)row * E;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int n0 = 8 * q + 4 * hi;
+            if ((E & 3) == 0 && n0 < E) {
+                *reinterpret_cast<f32x4*>(lrow + n0) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+                *reinterpret_cast<f32x4*>(prow + n0) =
+                    f32x4{psum[4 * q], psum[4 * q + 1], psum[4 * q + 2], psum[4 * q + 3]};
+            } else if ((E & 3) != 0) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    if (n0 + t < E) {
+                        lrow[n0 + t] = v[4 * q + t];
+                        prow[n0 + t] = psum[4 * q + t];
+                    }
+            }
+        }
+    }
+    if (clean && hi == 0) {
+        float zsum = 0.0f, pj[kMaxTopK];
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j) {
+            pj[j] = 0.0f;
+            if (j < K) {
+                pj[j] = __expf(topv[j] - vmax) / se;
+                zsum += pj[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kMaxTopK; ++j)
+            if (j < K) {
+                p.idx[(int64_t)row * K + j] = tope[j];
+                p.gate[(int64_t)row * K + j] = pj[j] / zsum;
+                atomicAdd(&s_cnt[tope[j]], 1);
+            }
+        p.lse[row] = lse;
+        lsum = lse * lse;
+    }
+    const uint64_t fm = __ballot(rvalid && flag && hi == 0);
+    if (lane == 0) s_flag[wave] = (uint32_t)fm;
+    // per-wave statistics over the wave's rows, in a fixed order
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        float t = psum[r];
+        t += xor_lane<16>(t);
+        t += xor_lane<8>(t);
+        t += xor_lane<4>(t);
+        t += xor_lane<2>(t);
+        t += xor_lane<1>(t);
+        const int n = expert_of(r);
+        if (rl == 0 && n < E) s_stat[wave][n] = t;
+    }
+    lsum += xor_lane<16>(lsum);
+    lsum += xor_lane<8>(lsum);
+    lsum += xor_lane<4>(lsum);
+    lsum += xor_lane<2>(lsum);
+    lsum += xor_lane<1>(lsum);
+    if (lane == 0) s_stat[wave][kMaxExperts] = lsum;
+    __syncthreads();
+
+    // ---- flagged rows in the canonical order: the block's i-th flagged row
+    // (ascending) goes to wave i % 4 -------------------------------------
+    float fps = 0.0f, fls = 0.0f;  // lane e: expert e's probability sum; lane 0: lse^2 sum
+    int fi = 0;
+    for (int w = 0; w < 4; ++w) {
+        uint32_t m = s_flag[w];
+        while (m != 0u) {
+            const int bit = __builtin_ctz(m);
+            m &= m - 1u;
+            if ((fi++ & 3) != wave) continue;
+            const int frow = row_begin + w * 32 + bit;
+            // lane partials over the lane's elements c * 512 + 8 lane + t,
+            // fmaf in ascending k, then the full xor butterfly
+            float pa[EP];
+#pragma unroll
+            for (int e = 0; e < EP; ++e) pa[e] = 0.0f;
+            for (int c0 = 0; c0 < d; c0 += 512) {
+                const int k = c0 + 8 * lane;
+                if (k < d) {
+                    float xf[8];
+                    unpack8(*reinterpret_cast<const uint4*>(p.X + (int64_t)frow * d + k), xf);
+#pragma unroll
+                    for (int e = 0; e < EP; ++e) {
+                        if (e < E) {
+                            float wf[8];
+                            unpack8(*reinterpret_cast<const uint4*>(sw + e * wpitch + k), wf);
+                            float a = pa[e];
+#pragma unroll
+                            for (int t = 0; t < 8; ++t) a = __builtin_fmaf(xf[t], wf[t], a);
+                            pa[e] = a;
+                        }
+                    }
+                }
+            }
+            float logit = 0.0f;
+#pragma unroll
+            for (int e = 0; e < EP; ++e) {
+                if (e < E) {
+                    float t = pa[e];
+                    t += xor_lane<32>(t);
+                    t += xor_lane<16>(t);
+                    t += xor_lane<8>(t);
+                    t += xor_lane<4>(t);
+                    t += xor_lane<2>(t);
+                    t += xor_lane<1>(t);
+                    if (lane % EP == e) logit = p.bias != nullptr ? t + p.bias[e] : t;
+                }
+            }
+            const int e_mine = lane % EP;
+            const bool e_valid = lane < EP && e_mine < E;
+            const RowPick pk = softmax_topk<EP>(logit, e_valid, e_mine, K);
+            if (lane < EP) {
+                if (e_valid) {
+                    p.logits[(int64_t)frow * E + e_mine] = logit;
+                    p.probs[(int64_t)frow * E + e_mine] = pk.prob;
+                    fps += pk.prob;
+                    if (pk.sel) atomicAdd(&s_cnt[e_mine], 1);
+                }
+                if (e_mine < K) {
+                    p.idx[(int64_t)frow * K + e_mine] = pk.idx;
+                    p.gate[(int64_t)frow * K + e_mine] = pk.gate;
+                }
+                if (e_mine == 0) {
+                    p.lse[frow] = pk.lse;
+                    fls += pk.lse * pk.lse;
+                }
+            }
+        }
+    }
+    if (lane < E) s_fl[wave][lane] = fps;
+    if (lane == 0) s_fl[wave][kMaxExperts] = fls;
+    __syncthreads();
+    const int blk = blockIdx.x;
+    if (tid <= E) {
+        const int col = tid < E ? tid : kMaxExperts;
+        float t = s_stat[0][col];
+        t += s_stat[1][col];
+        t += s_stat[2][col];
+        t += s_stat[3][col];
+        t += s_fl[0][col];
+        t += s_fl[1][col];
+        t += s_fl[2][col];
+        t += s_fl[3][col];
+        p.blkstat[(int64_t)blk * (E + 1) + tid] = t;
+        if (tid < E) p.blkcnt[(int64_t)blk * E + tid] = s_cnt[tid];
+    }
+}
+
+static size_t router_mfma_lds(int d) { return ((size_t)32 * (d + 8) + (size_t)4 * 2 * 32 * 128) * 2; }
+
+bool router_mfma_fits(int T, int E, int K, int d) {
+    return E >= 2 && E <= 32 && K <= E && K <= kMaxTopK && d % 128 == 0 && d >= 128 &&
+           router_mfma_lds(d) <= 140 * 1024 && (T + kMfmaRouterRows - 1) / kMfmaRouterRows >= cu_count();
+}
+
+hipError_t launch_router_mfma(const RouterParams& p, int nblk, hipStream_t s) {
+    if (p.rows_per_block != kMfmaRouterRows || p.ln_H != nullptr || !router_mfma_fits(nblk * kMfmaRouterRows, p.E, p.K, p.d))
+        return hipErrorInvalidValue;
+    const size_t lds = router_mfma_lds(p.d);
+    switch (router_ep(p.E)) {
+        case 8: router_mfma_kernel<8><<<nblk, 256, lds, s>>>(p); break;
+        case 16: router_mfma_kernel<16><<<nblk, 256, lds, s>>>(p); break;
+        case 32: router_mfma_kernel<32><<<nblk, 256, lds, s>>>(p); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // LayerNorm chunks of the fused router: 512-element chunks rounded up to 1, 2
 // or 4; a wave holds R = 64 / EP rows of them in registers (R * NCH <= 16;
 // with 64 expert lanes, whose 64 partials per lane leave less room, NCH <= 2).
