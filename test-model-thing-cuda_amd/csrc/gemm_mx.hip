@@ -380,11 +380,65 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
 
     // ---- epilogue -----------------------------------------------------------
     // acc[i][j][r] = C[m][n] with m = wm*128 + 32i + (lane&31) and
-    // n = wn*128 + 32j + 8(r>>2) + 4(lane>>5) + (r&3); staged per wave as fp32
-    // rows [EPR][WTN] (16-byte chunks swizzled by row), two passes.
+    // n = wn*128 + 32j + 8(r>>2) + 4(lane>>5) + (r&3).
+    const int mbase = wm * 128, nbase = wn * 128;
+    if constexpr (QUANT_OUT) {
+        // SiLU and the two-term MX6 quantisation straight from the
+        // accumulators: lanes l and l ^ 32 hold the two halves of each
+        // 32-column block of row l % 32, and one v_permlane32_swap per register
+        // pair (blocks 0 and 2, blocks 1 and 3) gives the lower half-wave all
+        // of blocks 0 and 1 and the upper all of blocks 2 and 3: in both, the
+        // first result of register r is element 8 (r / 4) + r % 4 of the block
+        // and the second element 8 (r / 4) + 4 + r % 4. Each lane then owns
+        // one (row, 64-column group) per row block, with no LDS staging.
+        const int hi = lane >> 5;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // keep the row blocks not yet converted in the accumulator
+            // registers: without this the allocator copies them all into
+            // VGPRs at the loop exit and spills
+#pragma unroll
+            for (int i2 = i; i2 < 4; ++i2)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i2][j]));
+            const int m = mbase + 32 * i + (lane & 31);
+            const int n = nbase + 64 * hi;
+            const bool in = m < mlim && n < nlim;
+            const int slot = row0 + m;
+            const int col = nt * BN + n;  // multiple of 64
+            uint4* codes = reinterpret_cast<uint4*>(p.q_codes + (int64_t)slot * (p.N / 32 * 48) + (col / 32) * 48);
+            uint32_t sc = 0;
+#pragma unroll
+            for (int b = 0; b < 2; ++b) {  // one 32-column block at a time
+                float x[32];
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int e = 8 * (r >> 2) + (r & 3);
+                    const u32x2_t sw = __builtin_amdgcn_permlane32_swap(
+                        __float_as_uint(acc[i][b][r]), __float_as_uint(acc[i][b + 2][r]), false, false);
+                    x[e] = silu_fast(__uint_as_float(sw[0]));
+                    x[e + 4] = silu_fast(__uint_as_float(sw[1]));
+                }
+                u32x6 t0, t1;
+                uint32_t s0, s1;
+                quant_block2(x, t0, t1, s0, s1);
+                sc |= (s0 | (s1 << 8)) << (16 * b);
+                if (in) {  // the block's 48 code bytes: t0 then t1
+                    codes[3 * b + 0] = make_uint4(t0[0], t0[1], t0[2], t0[3]);
+                    codes[3 * b + 1] = make_uint4(t0[4], t0[5], t1[0], t1[1]);
+                    codes[3 * b + 2] = make_uint4(t1[2], t1[3], t1[4], t1[5]);
+                }
+            }
+            if (in) *reinterpret_cast<uint32_t*>(p.q_scales + ((int64_t)(col / 64) * p.q_srows + slot) * 4) = sc;
+            __builtin_amdgcn_sched_barrier(0);  // one row block's values live at a time
+        }
+        return;
+    }
+    // bf16 C: staged per wave as fp32 rows [EPR][WTN] (16-byte chunks
+    // swizzled by row), two passes.
     constexpr int CH = WTN / 4;
     float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (EPR * WTN);
-    const int mbase = wm * 128, nbase = wn * 128;
 #pragma unroll
     for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
@@ -401,34 +455,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
                 }
         }
         __syncthreads();
-        if constexpr (QUANT_OUT) {
-            // lane -> (row rr, 64-column group g): two items per lane and pass
-#pragma unroll 1
-            for (int it = 0; it < 2; ++it) {
-                const int item = it * 64 + lane;
-                const int rr = item >> 1, g = item & 1;
-                const int m = mbase + pass * EPR + rr;
-                const int n = nbase + g * 64;
-                if (m < mlim && n < nlim) {
-                    float x[64];
-                    const float* src = stage_f + rr * WTN;
-#pragma unroll
-                    for (int c = 0; c < 16; ++c) {
-                        const f32x4 v = *reinterpret_cast<const f32x4*>(src + (((g * 16 + c) ^ (rr & (CH - 1))) * 4));
-#pragma unroll
-                        for (int u = 0; u < 4; ++u) x[4 * c + u] = silu_fast(v[u]);
-                    }
-                    u32x6 t[4];
-                    uint32_t s[4];
-                    quant_block2(x, t[0], t[1], s[0], s[1]);
-                    quant_block2(x + 32, t[2], t[3], s[2], s[3]);
-                    const int slot = row0 + m;
-                    const int col = nt * BN + n;  // multiple of 64
-                    store_group(p.q_codes + (int64_t)slot * (p.N / 32 * 48) + (col / 32) * 48,
-                                p.q_scales + ((int64_t)(col / 64) * p.q_srows + slot) * 4, t, s);
-                }
-            }
-        } else {
+        {
             constexpr int LPR = WTN / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
             uint16_t* C = p.c;
             const int cl = lane % LPR;
