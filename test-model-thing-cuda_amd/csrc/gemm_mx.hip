@@ -15,12 +15,16 @@
 // FP6 x FP4 products issue at the 8-pass rate, so the two terms together take
 // half the MFMA time of one bf16 product over the same K.
 //
-// Activation tensors ("MX6x2") in slot order, rows R, length K (K % 64 == 0):
-//   codes  [R][K/32][48] bytes: per 32-block, term 0 (24 bytes, element i at
-//          bits 6i..6i+5, little-endian) then term 1;
-//   scales [K/64][srows][4] bytes: per row and 64-column pair of blocks
-//          (block 2c term 0, block 2c term 1, block 2c+1 term 0, block 2c+1
-//          term 1); srows >= R + 256 so whole-tile loads stay in bounds.
+// Activation tensors ("MX6x2"), rows R, length K (K % 64 == 0), in planes of
+// 64 columns so that the 256 rows of a tile's K step are one contiguous
+// 24 KiB block (rows R apart at a large stride put a K step's loads on a few
+// L2 channels: at c5 the down GEMM ran 1.64 ms that way, 1.33 ms in planes):
+//   codes  [K/64][srows][96] bytes: per row, block 2c then block 2c+1 of
+//          plane c, each term 0 (24 bytes, element i at bits 6i..6i+5,
+//          little-endian) then term 1;
+//   scales [K/64][srows][4] bytes: per row and plane (block 2c term 0,
+//          block 2c term 1, block 2c+1 term 0, block 2c+1 term 1);
+//   srows >= R + 256 so whole-tile loads stay in bounds.
 //
 // Lane layout of the scaled MFMA (checked on the GPU against a host model):
 // lane l supplies row l % 32, K elements 32 * (l / 32) .. + 31 of each
@@ -154,12 +158,13 @@ __device__ __forceinline__ void store_group(uint8_t* codes, uint8_t* scales, con
 }
 
 // bf16 rows (gathered through perm when given) to MX6x2: one thread per
-// (row, 64-column group).
+// (row, 64-column plane), rows fastest so that a wave writes 64 consecutive
+// rows of one plane.
 __global__ __launch_bounds__(kThreads) void mx_quant_rows_kernel(MxQuantParams p) {
     const int groups = p.K / 64;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (idx >= (int64_t)p.rows * groups) return;
-    const int r = (int)(idx / groups), c = (int)(idx % groups);
+    const int c = (int)(idx / p.rows), r = (int)(idx % p.rows);
     const int src = p.perm ? p.perm[r] : r;
     const uint4* x = reinterpret_cast<const uint4*>(p.X + (int64_t)src * p.ldx + c * 64);
     uint4 v[8];
@@ -172,7 +177,7 @@ __global__ __launch_bounds__(kThreads) void mx_quant_rows_kernel(MxQuantParams p
     uint32_t s[4];
     quant_block2(f, t[0], t[1], s[0], s[1]);
     quant_block2(f + 32, t[2], t[3], s[2], s[3]);
-    store_group(p.codes + (int64_t)r * (p.K / 32 * 48) + c * 96, p.scales + ((int64_t)c * p.srows + r) * 4, t, s);
+    store_group(p.codes + ((int64_t)c * p.srows + r) * 96, p.scales + ((int64_t)c * p.srows + r) * 4, t, s);
 }
 
 // Expert segment of activation M tile mt: expert, first slot, rows (e < 0: none).
@@ -217,27 +222,24 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     if (e < 0) return;
     const int mlim = rows, nlim = min(BN, p.N - nt * BN);
     const int nk = p.K / 64;
-    const int64_t a_row_bytes = (int64_t)(p.K / 32) * 48;
+    const int64_t a_plane = p.a_srows * 96;  // bytes per 64-column plane of the activation codes
 
     // ---- DMA addressing: wave-uniform bases, 32-bit lane offsets ------------
     // (the host keeps every offset below 2^31)
-    // Activation row of tile row r: slot row0 + r (clamped to the last slot),
-    // or the token that slot gathers (a_perm).
-    auto a_src = [&](int r) {
-        const int slot = min(row0 + r, p.slots - 1);
-        return p.a_perm ? p.a_perm[slot] : slot;
-    };
+    // Activation row of tile row r: slot row0 + r, clamped to the last slot.
+    auto a_src = [&](int r) { return min(row0 + r, p.slots - 1); };
     // Activation codes: six consecutive 16-byte slots hold one row's 96 bytes
-    // of the stage (both 32-blocks, contiguous in memory), so a wave load
-    // covers ~11 rows x 96 bytes. The row's two 48-byte halves are swapped in
-    // LDS when bit 3 of the row is set (conflict-free fragment reads).
+    // of the stage (its row of the K step's plane), so a wave load covers ~11
+    // rows x 96 bytes, contiguous when the rows are. The row's two 48-byte
+    // halves are swapped in LDS when bit 3 of the row is set (conflict-free
+    // fragment reads).
     uint32_t a_off[A_LOADS];
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
         const int s = (wave * A_LOADS + i) * 64 + lane;  // 16-byte slot of the A region
         const int row = s / 6, part = s % 6;
         const int kb = (part / 3) ^ ((row >> 3) & 1), c = part % 3;
-        a_off[i] = (uint32_t)(a_src(row) * a_row_bytes + kb * 48 + c * 16);
+        a_off[i] = (uint32_t)(a_src(row) * 96 + kb * 48 + c * 16);
     }
     // Weight codes: lane pair (2m, 2m+1) loads the 32 contiguous bytes (both
     // 32-blocks) of row m, so a wave load covers 32 rows x 32 bytes rather
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     const uint8_t* wq = p.wq[e];
     const uint8_t* wsc = p.wsc[e];
     // scales: wave w loads the activation scales of tile rows 64w .. 64w+63
-    // (4 bytes per row and lane, rows gathered like the codes); every wave
+    // (4 bytes per row and lane, clamped like the codes); every wave
     // loads the tile's weight scales (the same bytes to the same place)
     const uint32_t as_off = (uint32_t)a_src(64 * wave + lane) * 4u;
     const uint32_t as_lds = A_BYTES + B_BYTES + 256u * (uint32_t)wave;
@@ -264,7 +266,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     auto dma_tile = [&](int t) {
         const int kt = min(t, nk - 1);
         const uint32_t sb = lds0 + (uint32_t)((t % NST) * STAGE);
-        const uint8_t* ab = p.a_codes + (int64_t)kt * 96;
+        const uint8_t* ab = p.a_codes + (int64_t)kt * a_plane;
         const uint8_t* bb = wq + (int64_t)kt * 32;
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) dma16(ab, a_off[i], sb + (uint32_t)(wave * A_LOADS + i) * 1024u);
@@ -329,16 +331,26 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
                                                                        (int)bsc[B][j], 1, (int)asc[i]); \
         }                                                                                             \
     } while (0)
+    // Until at most n (0..3) k64 tiles of this wave's DMA are in flight.
+    auto wait_tiles = [&](int n) {
+        if (n >= 3) wait_vm<3 * DMA_PER_TILE>();
+        else if (n == 2) wait_vm<2 * DMA_PER_TILE>();
+        else if (n == 1) wait_vm<DMA_PER_TILE>();
+        else wait_vm<0>();
+    };
     // One k64 tile t (stage S = t % NST, register set B = t % 2): wait for
-    // tile t+1, request tile t+NST-1, read tile t+1's weight fragments, and
+    // tile t+1, request tile t+NST into slot S (tile t's fragments are in
+    // registers since step t-1, and the barrier's LDS wait means every wave
+    // has finished reading them), read tile t+1's weight fragments, and
     // refill each activation row block with tile t+1's right after its MFMAs.
+    // Tiles t+2 .. t+NST stay in flight: every slot but the one being read.
 #define MX_STEP(S, B)                                                                                 \
     do {                                                                                              \
         const int t_ = kt + (S);                                                                      \
         if (t_ < nk) {                                                                                \
-            wait_vm<DMA_PER_TILE>();                                                                  \
+            wait_tiles(min(NST - 2, nk - 2 - t_));                                                    \
             __syncthreads();                                                                          \
-            dma_tile(t_ + NST - 1);                                                                   \
+            if (t_ + NST < nk) dma_tile(t_ + NST);                                                    \
             const int sn_ = t_ + 1 < nk ? ((S) + 1) % NST : (S);                                      \
             MX_LOAD_B((B) ^ 1, sn_);                                                                  \
             MX_MMA_ROW(0, B);                                                                         \
@@ -356,8 +368,9 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     // a compile-time constant --------------------------------------------------
     if (nk > 0) {
 #pragma unroll
-        for (int t = 0; t < NST - 1; ++t) dma_tile(t);
-        wait_vm<(NST - 2) * DMA_PER_TILE>();
+        for (int t = 0; t < NST; ++t)
+            if (t < nk) dma_tile(t);
+        wait_tiles(min(NST, nk) - 1);
         __syncthreads();
         MX_LOAD_B(0, 0);
         MX_LOAD_A(0, 0);
@@ -407,7 +420,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
             const bool in = m < mlim && n < nlim;
             const int slot = row0 + m;
             const int col = nt * BN + n;  // multiple of 64
-            uint4* codes = reinterpret_cast<uint4*>(p.q_codes + (int64_t)slot * (p.N / 32 * 48) + (col / 32) * 48);
+            uint4* codes = reinterpret_cast<uint4*>(p.q_codes + ((int64_t)(col / 64) * p.q_srows + slot) * 96);
             uint32_t sc = 0;
 #pragma unroll
             for (int b = 0; b < 2; ++b) {  // one 32-column block at a time
@@ -489,6 +502,8 @@ hipError_t launch_mx_quant_rows(const MxQuantParams& p, hipStream_t s) {
 hipError_t launch_mx_gemm(bool quant_out, const MxGemmParams& p, hipStream_t s) {
     if (p.slots <= 0) return hipSuccess;
     if (p.K % 64 != 0 || p.N % 64 != 0 || p.N <= 0) return hipErrorInvalidValue;
+    // lane offsets into one activation plane and into the weights are 32-bit
+    if (p.a_srows * 96 > 0x7fffffffLL || (int64_t)p.N * (p.K / 2) > 0x7fffffffLL) return hipErrorInvalidValue;
     const int64_t ntn = (p.N + BN - 1) / BN;
     const int64_t gn = ntn < 8 ? ntn : 8, gm = 32 / gn;
     const int64_t ngn = (ntn + gn - 1) / gn;

@@ -1044,15 +1044,15 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
     if (T > 0 && ds.weight_format == TMT_MOE_WEIGHTS_MXFP4_MX) {
         const int TK = T * K;
         const int64_t srows = (int64_t)ds.max_tokens * K + kMxScalePadRows;
-        // X is rounded once per token; the up GEMM gathers the rows of its slots.
+        // X is rounded per slot, in slot order (each token's row K times), so
+        // that every up-GEMM tile reads one contiguous block per K step.
         MxQuantParams qp{};
-        qp.X = X; qp.ldx = d; qp.perm = nullptr; qp.rows = T; qp.K = d;
+        qp.X = X; qp.ldx = d; qp.perm = E > 1 ? m->perm : nullptr; qp.rows = TK; qp.K = d;
         qp.codes = m->xq; qp.scales = m->xq_scales; qp.srows = srows;
         LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_quant_rows(qp, s));
         MxGemmParams up{};
         up.offsets = m->offsets; up.E = E; up.N = h; up.K = d; up.slots = TK;
         up.a_codes = m->xq; up.a_scales = m->xq_scales; up.a_srows = srows;
-        up.a_perm = E > 1 ? m->perm : nullptr;
         for (int e = 0; e < E; ++e) { up.wq[e] = W_up[e]; up.wsc[e] = W_up_scale[e]; }
         up.q_codes = m->aq; up.q_scales = m->aq_scales; up.q_srows = srows;
         LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_gemm(true, up, s));

@@ -215,11 +215,13 @@ bool skinny_self_dispatch(int T, int E, int K, int d, int h, int hn);
 
 // ------------------------------------------------------------- gemm_mx ----
 // MXFP4 weights times activations held as two MXFP6 terms, on the scaled
-// MFMA (layouts in gemm_mx.hip). Activation tensors ("MX6x2"): codes
-// [rows][K/32][48] bytes, scales [K/64][srows][4] bytes with srows >= rows +
-// kMxScalePadRows.
+// MFMA (layouts in gemm_mx.hip). Activation tensors ("MX6x2") are held in
+// K planes of 64: codes [K/64][srows][96] bytes, scales [K/64][srows][4]
+// bytes, srows >= rows + kMxScalePadRows.
 constexpr int kMxScalePadRows = 256;
-inline size_t mx_codes_bytes(int64_t rows, int64_t K) { return (size_t)rows * (size_t)(K / 32) * 48; }
+inline size_t mx_codes_bytes(int64_t rows, int64_t K) {
+    return (size_t)(K / 64) * (size_t)(rows + kMxScalePadRows) * 96;
+}
 inline size_t mx_scales_bytes(int64_t rows, int64_t K) {
     return (size_t)(K / 64) * (size_t)(rows + kMxScalePadRows) * 4;
 }
@@ -228,7 +230,7 @@ struct MxQuantParams {
     int64_t ldx;
     const int32_t* perm;     // row r reads X row perm[r] (nullptr: row r)
     int rows, K;
-    uint8_t* codes;          // [rows][K/32][48]
+    uint8_t* codes;          // [K/64][srows][96]
     uint8_t* scales;         // [K/64][srows][4]
     int64_t srows;
 };
@@ -237,15 +239,14 @@ struct MxGemmParams {
     const int32_t* offsets;  // [E+1] expert segments (slot space)
     int E;
     int N, K, slots;         // output columns, reduction length, routed rows
-    const uint8_t* a_codes;  // activations, MX6x2 [rows][K]: slot order, or
-    const uint8_t* a_scales; // token order gathered through a_perm
+    const uint8_t* a_codes;  // activations, MX6x2 planes in slot order (srows = a_srows)
+    const uint8_t* a_scales;
     int64_t a_srows;
-    const int32_t* a_perm;   // [slots] slot -> activation row (nullptr: the slot)
     const uint8_t* wq[kMaxExperts];   // e2m1 codes [N][K/2] per expert
     const uint8_t* wsc[kMaxExperts];  // e8m0 scales [K/32][N] per expert
     uint16_t* c;             // bf16 output [slots][ldc] (quant_out == false)
     int64_t ldc;
-    uint8_t* q_codes;        // SiLU(output) as MX6x2 [slots][N] (quant_out == true)
+    uint8_t* q_codes;        // SiLU(output) as MX6x2 planes, slot order (quant_out == true)
     uint8_t* q_scales;
     int64_t q_srows;
 };
