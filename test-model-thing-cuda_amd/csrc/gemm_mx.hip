@@ -180,100 +180,132 @@ __global__ __launch_bounds__(kThreads) void mx_quant_rows_kernel(MxQuantParams p
     store_group(p.codes + ((int64_t)c * p.srows + r) * 96, p.scales + ((int64_t)c * p.srows + r) * 4, t, s);
 }
 
-// Expert segment of activation M tile mt: expert, first slot, rows (e < 0: none).
-__device__ __forceinline__ void act_tile(const MxGemmParams& p, int mt, int& e, int& row0, int& rows) {
-    e = -1;
-    int t0 = 0;
-    for (int ee = 0; ee < p.E; ++ee) {
-        const int beg = p.offsets[ee], end = p.offsets[ee + 1];
-        const int tiles = (end - beg + BM - 1) / BM;
-        if (mt < t0 + tiles) {
-            e = ee;
-            row0 = beg + (mt - t0) * BM;
-            rows = min(BM, end - row0);
-            return;
-        }
-        t0 += tiles;
+// The activation M tiles of the experts, one expert per lane (E <= 64):
+// lane e holds expert e's first tile, tile count and slot range, so finding
+// a tile's expert is one ballot rather than a walk over the offsets.
+struct TileMap {
+    int first, tiles, beg, end;
+};
+__device__ __forceinline__ TileMap tile_map(const MxGemmParams& p, int lane) {
+    TileMap m{0, 0, 0, 0};
+    if (lane < p.E) {
+        m.beg = p.offsets[lane];
+        m.end = p.offsets[lane + 1];
+        m.tiles = (m.end - m.beg + BM - 1) / BM;
     }
+    int incl = m.tiles;  // inclusive prefix over the lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+    }
+    m.first = incl - m.tiles;
+    return m;
+}
+// Expert segment of activation M tile mt (wave-uniform): expert, first slot,
+// rows; false when mt is past the last tile.
+__device__ __forceinline__ bool act_tile(const TileMap& m, int mt, int& e, int& row0, int& rows) {
+    const uint64_t hit = __ballot(m.tiles > 0 && m.first <= mt && mt < m.first + m.tiles);
+    if (hit == 0) return false;
+    e = __builtin_ctzll(hit);
+    const int first = __builtin_amdgcn_readlane(m.first, e);
+    row0 = __builtin_amdgcn_readlane(m.beg, e) + (mt - first) * BM;
+    rows = min(BM, __builtin_amdgcn_readlane(m.end, e) - row0);
+    return true;
 }
 
 // QUANT_OUT: the output is SiLU(C) in MX6x2 (the next GEMM's activation);
-// otherwise C in bf16.
+// otherwise C in bf16. nvb virtual blocks map to tiles; a workgroup takes
+// vb = blockIdx.x, blockIdx.x + gridDim.x, ... (one each when the grid holds
+// all of them). With QUANT_OUT the epilogue uses no LDS, so the next tile's
+// first NST K steps are requested before it and land while it runs.
 template <bool QUANT_OUT>
-__global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
+__global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb) {
     __shared__ uint4 lds_raw[LDS_BYTES / 16];
     uint8_t* lds = reinterpret_cast<uint8_t*>(lds_raw);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int ntn = (p.N + BN - 1) / BN;
-
-    // ---- tile coordinates: XCD-aware groups of 32 tiles, as in gemm.hip ----
-    const int lid = ((((int)blockIdx.x >> 8) << 3) + ((int)blockIdx.x & 7)) * 32 + (((int)blockIdx.x >> 3) & 31);
-    const int G = lid >> 5, gi = lid & 31;
-    const int gn = min(ntn, 8), gm = 32 / gn;
-    const int ngn = (ntn + gn - 1) / gn;
-    if (gi >= gm * gn) return;
-    const int mt = (G / ngn) * gm + gi % gm;
-    const int nt = (G % ngn) * gn + gi / gm;
-    if (nt >= ntn) return;
-    int e, row0 = 0, rows = 0;
-    act_tile(p, mt, e, row0, rows);
-    if (e < 0) return;
-    const int mlim = rows, nlim = min(BN, p.N - nt * BN);
     const int nk = p.K / 64;
     const int64_t a_plane = p.a_srows * 96;  // bytes per 64-column plane of the activation codes
 
+    // ---- tiles: XCD-aware groups of 32 tiles, as in gemm.hip. Virtual block
+    // vb runs on XCD vb % 8, and gridDim.x is a multiple of 8, so a workgroup
+    // stays on the XCD of its groups. Blocks that hold no tile are skipped.
+    const int gn = min(ntn, 8), gm = 32 / gn;
+    const int ngn = (ntn + gn - 1) / gn;
+    const TileMap tmap = tile_map(p, lane);
+    auto find_tile = [&](int& vb, int& nt, int& e, int& row0, int& rows) {
+        for (; vb < nvb; vb += (int)gridDim.x) {
+            const int lid = (((vb >> 8) << 3) + (vb & 7)) * 32 + ((vb >> 3) & 31);
+            const int G = lid >> 5, gi = lid & 31;
+            if (gi >= gm * gn) continue;
+            const int mt = (G / ngn) * gm + gi % gm;
+            nt = (G % ngn) * gn + gi / gm;
+            if (nt >= ntn) continue;
+            if (act_tile(tmap, mt, e, row0, rows)) return true;
+        }
+        return false;
+    };
+    int vb = blockIdx.x, nt = 0, e = -1, row0 = 0, rows = 0;
+    if (!find_tile(vb, nt, e, row0, rows)) return;
+
     // ---- DMA addressing: wave-uniform bases, 32-bit lane offsets ------------
-    // (the host keeps every offset below 2^31)
-    // Activation row of tile row r: slot row0 + r, clamped to the last slot.
-    auto a_src = [&](int r) { return min(row0 + r, p.slots - 1); };
-    // Activation codes: six consecutive 16-byte slots hold one row's 96 bytes
-    // of the stage (its row of the K step's plane), so a wave load covers ~11
-    // rows x 96 bytes, contiguous when the rows are. The row's two 48-byte
-    // halves are swapped in LDS when bit 3 of the row is set (conflict-free
-    // fragment reads).
+    // (the host keeps every offset below 2^31). Activation codes: six
+    // consecutive 16-byte slots hold one row's 96 bytes of the stage (its row
+    // of the K step's plane), so the tile's 256 rows are one contiguous 24 KiB
+    // block; rows row0 .. row0 + 255 are in bounds for every tile (srows >=
+    // slots + 256), so these offsets do not depend on the tile. The row's two
+    // 48-byte halves are swapped in LDS when bit 3 of the row is set
+    // (conflict-free fragment reads).
     uint32_t a_off[A_LOADS];
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
         const int s = (wave * A_LOADS + i) * 64 + lane;  // 16-byte slot of the A region
         const int row = s / 6, part = s % 6;
         const int kb = (part / 3) ^ ((row >> 3) & 1), c = part % 3;
-        a_off[i] = (uint32_t)(a_src(row) * 96 + kb * 48 + c * 16);
+        a_off[i] = (uint32_t)(row * 96 + kb * 48 + c * 16);
     }
-    // Weight codes: lane pair (2m, 2m+1) loads the 32 contiguous bytes (both
-    // 32-blocks) of row m, so a wave load covers 32 rows x 32 bytes rather
-    // than 64 rows x 16 bytes. In LDS the row's two 16-byte halves are swapped
-    // when bit 3 of the row is set, which keeps the fragment reads (16 rows
-    // at a 32-byte stride) free of bank conflicts.
-    uint32_t b_off[B_LOADS];
-#pragma unroll
-    for (int i = 0; i < B_LOADS; ++i) {
-        const int s = (wave * B_LOADS + i) * 64 + lane;  // 16-byte slot of the B region: row s/2, half s%2
-        const int n = s >> 1, kb = (s & 1) ^ ((n >> 3) & 1);
-        b_off[i] = (uint32_t)(min(nt * BN + n, p.N - 1) * (int64_t)(p.K / 2) + kb * 16);
-    }
-    const uint8_t* wq = p.wq[e];
-    const uint8_t* wsc = p.wsc[e];
     // scales: wave w loads the activation scales of tile rows 64w .. 64w+63
-    // (4 bytes per row and lane, clamped like the codes); every wave
-    // loads the tile's weight scales (the same bytes to the same place)
-    const uint32_t as_off = (uint32_t)a_src(64 * wave + lane) * 4u;
+    // (4 bytes per row and lane); every wave loads the tile's weight scales
+    // (the same bytes to the same place)
+    const uint32_t as_off = (uint32_t)(64 * wave + lane) * 4u;
     const uint32_t as_lds = A_BYTES + B_BYTES + 256u * (uint32_t)wave;
-    const uint32_t ws_off = (uint32_t)(((lane >> 4) & 1) * p.N + min(nt * BN + (lane & 15) * 16, p.N - 16));
     constexpr uint32_t ws_lds = A_BYTES + B_BYTES + AS_BYTES;
+    // Per tile: the bases, and the weight offsets. Weight codes: lane pair
+    // (2m, 2m+1) loads the 32 contiguous bytes (both 32-blocks) of row m, so a
+    // wave load covers 32 rows x 32 bytes rather than 64 rows x 16 bytes. In
+    // LDS the row's two 16-byte halves are swapped when bit 3 of the row is
+    // set, which keeps the fragment reads (16 rows at a 32-byte stride) free
+    // of bank conflicts. Rows past N are clamped to N - 1.
+    const uint8_t *a_base = nullptr, *as_base = nullptr, *wq = nullptr, *wsc = nullptr;
+    uint32_t b_off[B_LOADS], ws_off = 0;
+    auto set_tile = [&](int t_nt, int t_e, int t_row0) {
+        a_base = p.a_codes + (int64_t)t_row0 * 96;
+        as_base = p.a_scales + (int64_t)t_row0 * 4;
+        wq = p.wq[t_e];
+        wsc = p.wsc[t_e];
+#pragma unroll
+        for (int i = 0; i < B_LOADS; ++i) {
+            const int s = (wave * B_LOADS + i) * 64 + lane;  // 16-byte slot of the B region: row s/2, half s%2
+            const int n = s >> 1, kb = (s & 1) ^ ((n >> 3) & 1);
+            b_off[i] = (uint32_t)(min(t_nt * BN + n, p.N - 1) * (int64_t)(p.K / 2) + kb * 16);
+        }
+        ws_off = (uint32_t)(((lane >> 4) & 1) * p.N + min(t_nt * BN + (lane & 15) * 16, p.N - 16));
+    };
     const uint32_t lds0 = lds_addr(lds);
+    // K step t (< nk) of the current addressing into ring slot t % NST.
     auto dma_tile = [&](int t) {
-        const int kt = min(t, nk - 1);
         const uint32_t sb = lds0 + (uint32_t)((t % NST) * STAGE);
-        const uint8_t* ab = p.a_codes + (int64_t)kt * a_plane;
-        const uint8_t* bb = wq + (int64_t)kt * 32;
+        const uint8_t* ab = a_base + (int64_t)t * a_plane;
+        const uint8_t* bb = wq + (int64_t)t * 32;
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) dma16(ab, a_off[i], sb + (uint32_t)(wave * A_LOADS + i) * 1024u);
 #pragma unroll
         for (int i = 0; i < B_LOADS; ++i) dma16(bb, b_off[i], sb + A_BYTES + (uint32_t)(wave * B_LOADS + i) * 1024u);
-        dma4(p.a_scales + (int64_t)kt * p.a_srows * 4, as_off, sb + as_lds);
-        dma16(wsc + (int64_t)kt * 2 * p.N, ws_off, sb + ws_lds);
+        dma4(as_base + (int64_t)t * p.a_srows * 4, as_off, sb + as_lds);
+        dma16(wsc + (int64_t)t * 2 * p.N, ws_off, sb + ws_lds);
     };
 
     // ---- fragments ----------------------------------------------------------
@@ -291,12 +323,6 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
     i32x8 a0[4], a1[4];
     uint32_t asc[4];
     f32x16 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
     // B fragments of the tile in stage `sg` into register set `B`.
 #define MX_LOAD_B(B, sg)                                                                              \
     do {                                                                                              \
@@ -364,13 +390,127 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
         }                                                                                             \
     } while (0)
 
-    // ---- main loop, unrolled by the ring depth so that every stage index is
-    // a compile-time constant --------------------------------------------------
-    if (nk > 0) {
+    // ---- epilogue -----------------------------------------------------------
+    // acc[i][j][r] = C[m][n] with m = wm*128 + 32i + (lane&31) and
+    // n = wn*128 + 32j + 8(r>>2) + 4(lane>>5) + (r&3).
+    const int mbase = wm * 128, nbase = wn * 128;
+    // after_block(i) runs after row block i of the MX epilogue
+    auto epilogue = [&](int t_row0, int t_rows, int t_nt, auto after_block) __attribute__((always_inline)) {
+        const int nlim = min(BN, p.N - t_nt * BN);
+        if constexpr (QUANT_OUT) {
+            // SiLU and the two-term MX6 quantisation straight from the
+            // accumulators: lanes l and l ^ 32 hold the two halves of each
+            // 32-column block of row l % 32, and one v_permlane32_swap per register
+            // pair (blocks 0 and 2, blocks 1 and 3) gives the lower half-wave all
+            // of blocks 0 and 1 and the upper all of blocks 2 and 3: in both, the
+            // first result of register r is element 8 (r / 4) + r % 4 of the block
+            // and the second element 8 (r / 4) + 4 + r % 4. Each lane then owns
+            // one (row, 64-column group) per row block, with no LDS staging.
+            const int hi = lane >> 5;
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int t = 0; t < NST; ++t)
-            if (t < nk) dma_tile(t);
-        wait_tiles(min(NST, nk) - 1);
+            for (int i = 0; i < 4; ++i) {
+                // keep the row blocks not yet converted in the accumulator
+                // registers: without this the allocator copies them all into
+                // VGPRs at the loop exit and spills
+#pragma unroll
+                for (int i2 = i; i2 < 4; ++i2)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i2][j]));
+                const int m = mbase + 32 * i + (lane & 31);
+                const int n = nbase + 64 * hi;
+                const bool in = m < t_rows && n < nlim;
+                const int slot = t_row0 + m;
+                const int col = t_nt * BN + n;  // multiple of 64
+                uint4* codes = reinterpret_cast<uint4*>(p.q_codes + ((int64_t)(col / 64) * p.q_srows + slot) * 96);
+                uint32_t sc = 0;
+#pragma unroll
+                for (int b = 0; b < 2; ++b) {  // one 32-column block at a time
+                    float x[32];
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int e = 8 * (r >> 2) + (r & 3);
+                        const u32x2_t sw = __builtin_amdgcn_permlane32_swap(
+                            __float_as_uint(acc[i][b][r]), __float_as_uint(acc[i][b + 2][r]), false, false);
+                        x[e] = silu_fast(__uint_as_float(sw[0]));
+                        x[e + 4] = silu_fast(__uint_as_float(sw[1]));
+                    }
+                    u32x6 t0, t1;
+                    uint32_t s0, s1;
+                    quant_block2(x, t0, t1, s0, s1);
+                    sc |= (s0 | (s1 << 8)) << (16 * b);
+                    if (in) {  // the block's 48 code bytes: t0 then t1
+                        codes[3 * b + 0] = make_uint4(t0[0], t0[1], t0[2], t0[3]);
+                        codes[3 * b + 1] = make_uint4(t0[4], t0[5], t1[0], t1[1]);
+                        codes[3 * b + 2] = make_uint4(t1[2], t1[3], t1[4], t1[5]);
+                    }
+                }
+                if (in) *reinterpret_cast<uint32_t*>(p.q_scales + ((int64_t)(col / 64) * p.q_srows + slot) * 4) = sc;
+                after_block(i);
+                __builtin_amdgcn_sched_barrier(0);  // one row block's values live at a time
+            }
+        } else {
+            // bf16 C: staged per wave as fp32 rows [EPR][WTN] (16-byte chunks
+            // swizzled by row), two passes.
+            constexpr int CH = WTN / 4;
+            float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (EPR * WTN);
+#pragma unroll
+            for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+                for (int ii = 0; ii < 2; ++ii) {
+                    const int i = pass * 2 + ii;
+                    const int lr = ii * 32 + (lane & 31);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int ch = j * 8 + 2 * q + (lane >> 5);
+                            *reinterpret_cast<f32x4*>(stage_f + lr * WTN + ((ch ^ (lr & (CH - 1))) * 4)) =
+                                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                        }
+                }
+                __syncthreads();
+                {
+                    constexpr int LPR = WTN / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
+                    uint16_t* C = p.c;
+                    const int cl = lane % LPR;
+                    const int n = nbase + cl * 8;
+#pragma unroll
+                    for (int k = 0; k < EPR / RPI; ++k) {
+                        const int rr = lane / LPR + RPI * k;
+                        const int m = mbase + pass * EPR + rr;
+                        if (m >= t_rows || n >= nlim) continue;
+                        const float* src = stage_f + rr * WTN;
+                        const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + (((2 * cl) ^ (rr & (CH - 1))) * 4));
+                        const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + (((2 * cl + 1) ^ (rr & (CH - 1))) * 4));
+                        const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                        st16_nt(C + (int64_t)(t_row0 + m) * p.ldc + t_nt * BN + n, pack8(v));
+                    }
+                }
+                __syncthreads();
+            }
+        }
+    };
+
+    set_tile(nt, e, row0);
+    bool prefetched = false;
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        // ---- main loop, unrolled by the ring depth so that every stage index
+        // is a compile-time constant ------------------------------------------
+        if (!prefetched) {
+#pragma unroll
+            for (int t = 0; t < NST; ++t)
+                if (t < nk) dma_tile(t);
+            wait_tiles(min(NST, nk) - 1);
+        } else {
+            wait_vm<0>();  // the K steps requested before the last epilogue (and its stores)
+        }
         __syncthreads();
         MX_LOAD_B(0, 0);
         MX_LOAD_A(0, 0);
@@ -383,110 +523,33 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p) {
             MX_STEP(2, 0);
             MX_STEP(3, 1);
         }
+        __syncthreads();  // every wave has read its last fragments: the ring is free
+
+        // the workgroup's next tile: its first NST K steps load during the
+        // epilogue, two before it and one after each of its first two row
+        // blocks (a burst of all four slowed the epilogue's own stores)
+        int vb2 = vb + (int)gridDim.x, nt2 = 0, e2 = -1, row02 = 0, rows2 = 0;
+        const bool more = QUANT_OUT && find_tile(vb2, nt2, e2, row02, rows2);
+        if (more) {
+            set_tile(nt2, e2, row02);
+            dma_tile(0);
+            if (1 < nk) dma_tile(1);
+        }
+        epilogue(row0, rows, nt, [&](int i) {
+            if (more && i < 2 && i + 2 < nk) dma_tile(i + 2);
+        });
+        if (!more) break;
+        vb = vb2;
+        nt = nt2;
+        e = e2;
+        row0 = row02;
+        rows = rows2;
+        prefetched = true;
     }
 #undef MX_STEP
 #undef MX_MMA_ROW
 #undef MX_LOAD_A
 #undef MX_LOAD_B
-    wait_vm<0>();
-    __syncthreads();
-
-    // ---- epilogue -----------------------------------------------------------
-    // acc[i][j][r] = C[m][n] with m = wm*128 + 32i + (lane&31) and
-    // n = wn*128 + 32j + 8(r>>2) + 4(lane>>5) + (r&3).
-    const int mbase = wm * 128, nbase = wn * 128;
-    if constexpr (QUANT_OUT) {
-        // SiLU and the two-term MX6 quantisation straight from the
-        // accumulators: lanes l and l ^ 32 hold the two halves of each
-        // 32-column block of row l % 32, and one v_permlane32_swap per register
-        // pair (blocks 0 and 2, blocks 1 and 3) gives the lower half-wave all
-        // of blocks 0 and 1 and the upper all of blocks 2 and 3: in both, the
-        // first result of register r is element 8 (r / 4) + r % 4 of the block
-        // and the second element 8 (r / 4) + 4 + r % 4. Each lane then owns
-        // one (row, 64-column group) per row block, with no LDS staging.
-        const int hi = lane >> 5;
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            // keep the row blocks not yet converted in the accumulator
-            // registers: without this the allocator copies them all into
-            // VGPRs at the loop exit and spills
-#pragma unroll
-            for (int i2 = i; i2 < 4; ++i2)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i2][j]));
-            const int m = mbase + 32 * i + (lane & 31);
-            const int n = nbase + 64 * hi;
-            const bool in = m < mlim && n < nlim;
-            const int slot = row0 + m;
-            const int col = nt * BN + n;  // multiple of 64
-            uint4* codes = reinterpret_cast<uint4*>(p.q_codes + ((int64_t)(col / 64) * p.q_srows + slot) * 96);
-            uint32_t sc = 0;
-#pragma unroll
-            for (int b = 0; b < 2; ++b) {  // one 32-column block at a time
-                float x[32];
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int e = 8 * (r >> 2) + (r & 3);
-                    const u32x2_t sw = __builtin_amdgcn_permlane32_swap(
-                        __float_as_uint(acc[i][b][r]), __float_as_uint(acc[i][b + 2][r]), false, false);
-                    x[e] = silu_fast(__uint_as_float(sw[0]));
-                    x[e + 4] = silu_fast(__uint_as_float(sw[1]));
-                }
-                u32x6 t0, t1;
-                uint32_t s0, s1;
-                quant_block2(x, t0, t1, s0, s1);
-                sc |= (s0 | (s1 << 8)) << (16 * b);
-                if (in) {  // the block's 48 code bytes: t0 then t1
-                    codes[3 * b + 0] = make_uint4(t0[0], t0[1], t0[2], t0[3]);
-                    codes[3 * b + 1] = make_uint4(t0[4], t0[5], t1[0], t1[1]);
-                    codes[3 * b + 2] = make_uint4(t1[2], t1[3], t1[4], t1[5]);
-                }
-            }
-            if (in) *reinterpret_cast<uint32_t*>(p.q_scales + ((int64_t)(col / 64) * p.q_srows + slot) * 4) = sc;
-            __builtin_amdgcn_sched_barrier(0);  // one row block's values live at a time
-        }
-        return;
-    }
-    // bf16 C: staged per wave as fp32 rows [EPR][WTN] (16-byte chunks
-    // swizzled by row), two passes.
-    constexpr int CH = WTN / 4;
-    float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (EPR * WTN);
-#pragma unroll
-    for (int pass = 0; pass < 2; ++pass) {
-#pragma unroll
-        for (int ii = 0; ii < 2; ++ii) {
-            const int i = pass * 2 + ii;
-            const int lr = ii * 32 + (lane & 31);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const int ch = j * 8 + 2 * q + (lane >> 5);
-                    *reinterpret_cast<f32x4*>(stage_f + lr * WTN + ((ch ^ (lr & (CH - 1))) * 4)) =
-                        f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                }
-        }
-        __syncthreads();
-        {
-            constexpr int LPR = WTN / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
-            uint16_t* C = p.c;
-            const int cl = lane % LPR;
-            const int n = nbase + cl * 8;
-#pragma unroll
-            for (int k = 0; k < EPR / RPI; ++k) {
-                const int rr = lane / LPR + RPI * k;
-                const int m = mbase + pass * EPR + rr;
-                if (m >= mlim || n >= nlim) continue;
-                const float* src = stage_f + rr * WTN;
-                const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + (((2 * cl) ^ (rr & (CH - 1))) * 4));
-                const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + (((2 * cl + 1) ^ (rr & (CH - 1))) * 4));
-                const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                st16_nt(C + (int64_t)(row0 + m) * p.ldc + nt * BN + n, pack8(v));
-            }
-        }
-        __syncthreads();
-    }
 }
 
 }  // namespace
@@ -501,7 +564,7 @@ hipError_t launch_mx_quant_rows(const MxQuantParams& p, hipStream_t s) {
 
 hipError_t launch_mx_gemm(bool quant_out, const MxGemmParams& p, hipStream_t s) {
     if (p.slots <= 0) return hipSuccess;
-    if (p.K % 64 != 0 || p.N % 64 != 0 || p.N <= 0) return hipErrorInvalidValue;
+    if (p.K % 64 != 0 || p.K <= 0 || p.N % 64 != 0 || p.N <= 0) return hipErrorInvalidValue;
     // lane offsets into one activation plane and into the weights are 32-bit
     if (p.a_srows * 96 > 0x7fffffffLL || (int64_t)p.N * (p.K / 2) > 0x7fffffffLL) return hipErrorInvalidValue;
     const int64_t ntn = (p.N + BN - 1) / BN;
@@ -511,8 +574,15 @@ hipError_t launch_mx_gemm(bool quant_out, const MxGemmParams& p, hipStream_t s) 
     const int64_t groups = ((mtiles + gm - 1) / gm) * ngn;
     const int64_t grid = (groups * 32 + 255) / 256 * 256;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
-    if (quant_out) mx_gemm_kernel<true><<<(unsigned)grid, 256, 0, s>>>(p);
-    else mx_gemm_kernel<false><<<(unsigned)grid, 256, 0, s>>>(p);
+    // The up GEMM runs persistent, one workgroup per CU (a multiple of 8, so
+    // each keeps its XCD); the down GEMM one workgroup per virtual block.
+    if (quant_out) {
+        const int64_t cus = cu_count() / 8 * 8;
+        const int64_t g = cus >= 8 && cus < grid ? cus : grid;
+        mx_gemm_kernel<true><<<(unsigned)g, 256, 0, s>>>(p, (int)grid);
+    } else {
+        mx_gemm_kernel<false><<<(unsigned)grid, 256, 0, s>>>(p, (int)grid);
+    }
     return hipGetLastError();
 }
 
