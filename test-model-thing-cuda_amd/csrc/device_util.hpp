@@ -25,6 +25,48 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
+// The M tiles (TBM slots each) of the experts' slot segments, one expert per
+// lane (E <= 64): lane e holds expert e's first tile and first slot, so a
+// tile's expert is one ballot rather than a walk over the offsets. Built
+// once per workgroup (one vector load of the offsets and a wave prefix sum);
+// two VGPRs stay live.
+struct ExpertTiles {
+    int first, beg;   // per lane: first tile and first slot of expert `lane` (lanes >= E: total, end)
+    int total, end;   // wave-uniform: tiles of all experts, offsets[E]
+};
+template <int TBM>
+__device__ __forceinline__ ExpertTiles expert_tiles(const int32_t* offsets, int E, int lane) {
+    ExpertTiles m;
+    m.end = __builtin_amdgcn_readfirstlane(offsets[E]);
+    m.beg = lane < E ? offsets[lane] : m.end;
+    const int nxt = __shfl_down(m.beg, 1);
+    const int tiles = lane < E ? ((lane + 1 < E ? nxt : m.end) - m.beg + TBM - 1) / TBM : 0;
+    int incl = tiles;  // inclusive prefix over the lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+    }
+    m.first = incl - tiles;
+    m.total = __builtin_amdgcn_readlane(incl, 63);
+    return m;
+}
+// Expert segment of M tile mt (wave-uniform): expert, first slot, rows;
+// false when mt is past the last tile.
+template <int TBM>
+__device__ __forceinline__ bool expert_tile(const ExpertTiles& m, int mt, int& e, int& row0, int& rows) {
+    const int lane = __lane_id();
+    const int dn = __shfl_down(m.first, 1);
+    const int next = lane == 63 ? m.total : dn;  // first tile of the next expert
+    const uint64_t hit = __ballot(m.first <= mt && mt < next);
+    if (hit == 0) return false;
+    e = __builtin_ctzll(hit);
+    row0 = __builtin_amdgcn_readlane(m.beg, e) + (mt - __builtin_amdgcn_readlane(m.first, e)) * TBM;
+    const int end = e < 63 ? __builtin_amdgcn_readlane(m.beg, e + 1) : m.end;
+    rows = min(TBM, end - row0);
+    return true;
+}
+
 // Unpack 8 bf16 held in a uint4 into fp32.
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
     f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);

@@ -259,9 +259,10 @@ constexpr bool persistent_tiles() {
 }
 
 // One output tile (or split-K part) of the grouped GEMM: launch-order block
-// index vb; returns without touching memory when vb maps to no tile.
+// index vb; returns without touching memory when vb maps to no tile. et: the
+// experts' activation tiles (unused by the weight-gradient kinds).
 template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2, int BM_ = 256>
-__device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int vb) {
+__device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int vb, const ExpertTiles& et) {
     using Tr = Traits<KIND>;
     using Gm = Geo<BK_, NST, BN_, NWM_, BM_>;
     constexpr int BM = Gm::BM;
@@ -317,7 +318,7 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
         kend = p.K;
         SplitPlan sp;
         if constexpr (kSplitK) {
-            if (p.part != nullptr) sp = split_plan<BK>(p, ntn, act_mtiles<BM>(p));
+            if (p.part != nullptr) sp = split_plan<BK>(p, ntn, et.total);
         }
         if (p.xcd_runs) {
             // Launches whose tiles all run at once: the tiles in (mt, nt)
@@ -325,7 +326,7 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
             // on XCD vb % 8 and takes tile vb / 8 of that XCD's run. Every
             // XCD gets the same number of tiles, and a run covers whole rows
             // of tiles of one or two experts, whose weights its L2 keeps.
-            const int R = act_mtiles<BM>(p) * ntn;
+            const int R = et.total * ntn;
             const int per = (R + 7) / 8;
             const int j = (vb & 7) * per + (vb >> 3);
             if ((vb >> 3) >= per || j >= R) return;
@@ -346,8 +347,7 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
             nt = (G % ngn) * gn + gi / gm;
             if (nt >= ntn) return;
         }
-        act_tile<BM>(p, mt, e, row0, rows);
-        if (e < 0) return;  // beyond the last tile of the last expert
+        if (!expert_tile<BM>(et, mt, e, row0, rows)) return;  // beyond the last tile of the last expert
         mlim = rows;
     } else {
         // A group's work is proportional to its expert's count, and groups
@@ -883,11 +883,15 @@ __device__ __forceinline__ void grouped_gemm_tile(const GemmParams& p, const int
 
 template <int KIND, bool DUAL, int BK_, int NST, int BN_, int NWM_ = 2, int BM_ = 256>
 __global__ __launch_bounds__(128 * NWM_, (BN_ == 256 && BM_ == 256 ? 1 : 2)) void grouped_gemm_kernel(GemmParams p) {
+    // the experts' tiles, once per workgroup (before any tile's stores, so
+    // the vector load of the offsets waits on nothing else)
+    ExpertTiles et{};
+    if constexpr (!Traits<KIND>::group_k) et = expert_tiles<Geo<BK_, NST, BN_, NWM_, BM_>::BM>(p.offsets, p.E, threadIdx.x & 63);
     if constexpr (persistent_tiles<KIND, BK_, BN_, NWM_, BM_>()) {
         for (int vb = blockIdx.x; vb < p.vblocks; vb += gridDim.x)
-            grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_, BM_>(p, vb);
+            grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_, BM_>(p, vb, et);
     } else {
-        grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_, BM_>(p, blockIdx.x);
+        grouped_gemm_tile<KIND, DUAL, BK_, NST, BN_, NWM_, BM_>(p, blockIdx.x, et);
     }
 }
 

@@ -180,40 +180,6 @@ __global__ __launch_bounds__(kThreads) void mx_quant_rows_kernel(MxQuantParams p
     store_group(p.codes + ((int64_t)c * p.srows + r) * 96, p.scales + ((int64_t)c * p.srows + r) * 4, t, s);
 }
 
-// The activation M tiles of the experts, one expert per lane (E <= 64):
-// lane e holds expert e's first tile, tile count and slot range, so finding
-// a tile's expert is one ballot rather than a walk over the offsets.
-struct TileMap {
-    int first, tiles, beg, end;
-};
-__device__ __forceinline__ TileMap tile_map(const MxGemmParams& p, int lane) {
-    TileMap m{0, 0, 0, 0};
-    if (lane < p.E) {
-        m.beg = p.offsets[lane];
-        m.end = p.offsets[lane + 1];
-        m.tiles = (m.end - m.beg + BM - 1) / BM;
-    }
-    int incl = m.tiles;  // inclusive prefix over the lanes
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int v = __shfl_up(incl, o);
-        if (lane >= o) incl += v;
-    }
-    m.first = incl - m.tiles;
-    return m;
-}
-// Expert segment of activation M tile mt (wave-uniform): expert, first slot,
-// rows; false when mt is past the last tile.
-__device__ __forceinline__ bool act_tile(const TileMap& m, int mt, int& e, int& row0, int& rows) {
-    const uint64_t hit = __ballot(m.tiles > 0 && m.first <= mt && mt < m.first + m.tiles);
-    if (hit == 0) return false;
-    e = __builtin_ctzll(hit);
-    const int first = __builtin_amdgcn_readlane(m.first, e);
-    row0 = __builtin_amdgcn_readlane(m.beg, e) + (mt - first) * BM;
-    rows = min(BM, __builtin_amdgcn_readlane(m.end, e) - row0);
-    return true;
-}
-
 // QUANT_OUT: the output is SiLU(C) in MX6x2 (the next GEMM's activation);
 // otherwise C in bf16. nvb virtual blocks map to tiles; a workgroup takes
 // vb = blockIdx.x, blockIdx.x + gridDim.x, ... (one each when the grid holds
@@ -235,7 +201,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
     // stays on the XCD of its groups. Blocks that hold no tile are skipped.
     const int gn = min(ntn, 8), gm = 32 / gn;
     const int ngn = (ntn + gn - 1) / gn;
-    const TileMap tmap = tile_map(p, lane);
+    const ExpertTiles tmap = expert_tiles<BM>(p.offsets, p.E, lane);
     auto find_tile = [&](int& vb, int& nt, int& e, int& row0, int& rows) {
         for (; vb < nvb; vb += (int)gridDim.x) {
             const int lid = (((vb >> 8) << 3) + (vb & 7)) * 32 + ((vb >> 3) & 31);
@@ -244,7 +210,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
             const int mt = (G / ngn) * gm + gi % gm;
             nt = (G % ngn) * gn + gi / gm;
             if (nt >= ntn) continue;
-            if (act_tile(tmap, mt, e, row0, rows)) return true;
+            if (expert_tile<BM>(tmap, mt, e, row0, rows)) return true;
         }
         return false;
     };
