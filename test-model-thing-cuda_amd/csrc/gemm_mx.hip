@@ -157,16 +157,16 @@ __device__ __forceinline__ void store_group(uint8_t* codes, uint8_t* scales, con
     *reinterpret_cast<uint32_t*>(scales) = s[0] | (s[1] << 8) | (s[2] << 16) | (s[3] << 24);
 }
 
-// bf16 rows (gathered through perm when given) to MX6x2: one thread per
-// (row, 64-column plane), rows fastest so that a wave writes 64 consecutive
-// rows of one plane.
+// bf16 rows to MX6x2, each row rounded once and written to every slot it
+// is routed to (slot_of): one thread per (row, 64-column plane), rows fastest
+// so that a wave reads 64 rows of one plane and writes runs of consecutive
+// slots (an expert's slots hold its tokens in token order).
 __global__ __launch_bounds__(kThreads) void mx_quant_rows_kernel(MxQuantParams p) {
     const int groups = p.K / 64;
     const int64_t idx = (int64_t)blockIdx.x * kThreads + threadIdx.x;
     if (idx >= (int64_t)p.rows * groups) return;
     const int c = (int)(idx / p.rows), r = (int)(idx % p.rows);
-    const int src = p.perm ? p.perm[r] : r;
-    const uint4* x = reinterpret_cast<const uint4*>(p.X + (int64_t)src * p.ldx + c * 64);
+    const uint4* x = reinterpret_cast<const uint4*>(p.X + (int64_t)r * p.ldx + c * 64);
     uint4 v[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = x[i];
@@ -177,7 +177,10 @@ __global__ __launch_bounds__(kThreads) void mx_quant_rows_kernel(MxQuantParams p
     uint32_t s[4];
     quant_block2(f, t[0], t[1], s[0], s[1]);
     quant_block2(f + 32, t[2], t[3], s[2], s[3]);
-    store_group(p.codes + ((int64_t)c * p.srows + r) * 96, p.scales + ((int64_t)c * p.srows + r) * 4, t, s);
+    for (int j = 0; j < p.copies; ++j) {
+        const int slot = p.slot_of ? p.slot_of[(int64_t)r * p.copies + j] : r;
+        store_group(p.codes + ((int64_t)c * p.srows + slot) * 96, p.scales + ((int64_t)c * p.srows + slot) * 4, t, s);
+    }
 }
 
 // QUANT_OUT: the output is SiLU(C) in MX6x2 (the next GEMM's activation);
@@ -522,7 +525,8 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
 
 hipError_t launch_mx_quant_rows(const MxQuantParams& p, hipStream_t s) {
     if (p.rows <= 0) return hipSuccess;
-    if (p.K % 64 != 0 || p.srows < p.rows) return hipErrorInvalidValue;
+    if (p.K % 64 != 0 || p.copies < 1 || (!p.slot_of && p.copies != 1) || p.srows < (int64_t)p.rows * p.copies)
+        return hipErrorInvalidValue;
     const int64_t items = (int64_t)p.rows * (p.K / 64);
     mx_quant_rows_kernel<<<(unsigned)((items + kThreads - 1) / kThreads), kThreads, 0, s>>>(p);
     return hipGetLastError();

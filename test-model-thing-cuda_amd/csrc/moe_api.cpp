@@ -1044,10 +1044,11 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
     if (T > 0 && ds.weight_format == TMT_MOE_WEIGHTS_MXFP4_MX) {
         const int TK = T * K;
         const int64_t srows = (int64_t)ds.max_tokens * K + kMxScalePadRows;
-        // X is rounded per slot, in slot order (each token's row K times), so
+        // X is rounded once per token and written to the token's K slots, so
         // that every up-GEMM tile reads one contiguous block per K step.
         MxQuantParams qp{};
-        qp.X = X; qp.ldx = d; qp.perm = E > 1 ? m->perm : nullptr; qp.rows = TK; qp.K = d;
+        qp.X = X; qp.ldx = d; qp.rows = T; qp.K = d;
+        qp.slot_of = E > 1 ? m->slot_of : nullptr; qp.copies = E > 1 ? K : 1;
         qp.codes = m->xq; qp.scales = m->xq_scales; qp.srows = srows;
         LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_quant_rows(qp, s));
         MxGemmParams up{};

@@ -226,9 +226,10 @@ inline size_t mx_scales_bytes(int64_t rows, int64_t K) {
     return (size_t)(K / 64) * (size_t)(rows + kMxScalePadRows) * 4;
 }
 struct MxQuantParams {
-    const uint16_t* X;       // bf16 rows
+    const uint16_t* X;       // bf16 rows (tokens)
     int64_t ldx;
-    const int32_t* perm;     // row r reads X row perm[r] (nullptr: row r)
+    const int32_t* slot_of;  // [rows][copies]: the slots row r is written to (nullptr: slot r)
+    int copies;              // slots per row (1 when slot_of is nullptr)
     int rows, K;
     uint8_t* codes;          // [K/64][srows][96]
     uint8_t* scales;         // [K/64][srows][4]
