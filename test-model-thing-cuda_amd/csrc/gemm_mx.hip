@@ -61,8 +61,11 @@ constexpr int A_LOADS = A_BYTES / 1024 / 4;  // 1 KiB wave loads per wave
 constexpr int B_LOADS = B_BYTES / 1024 / 4;
 constexpr int DMA_PER_TILE = A_LOADS + B_LOADS + 2;  // + the wave's activation-scale rows, the weight scales
 constexpr int EPR = 64, WTN = 128;  // epilogue: rows per wave and pass, wave tile width
-constexpr int EPI = 4 * EPR * WTN * 4;
-constexpr int LDS_BYTES = NST * STAGE > EPI ? NST * STAGE : EPI;
+// The bf16 epilogue stages each wave's EPR x WTN bf16 rows in ring slots 2
+// and 3, so slots 0 and 1 can take the next tile's first K steps meanwhile.
+constexpr int EPI_OFF = 2 * STAGE, EPI = 4 * EPR * WTN * 2;
+static_assert(EPI_OFF + EPI <= NST * STAGE, "bf16 staging must fit in ring slots 2 and 3");
+constexpr int LDS_BYTES = NST * STAGE;
 static_assert(LDS_BYTES <= 160 * 1024, "LDS ring too large");
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -419,23 +422,31 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
                 __builtin_amdgcn_sched_barrier(0);  // one row block's values live at a time
             }
         } else {
-            // bf16 C: staged per wave as fp32 rows [EPR][WTN] (16-byte chunks
-            // swizzled by row), two passes.
-            constexpr int CH = WTN / 4;
-            float* stage_f = reinterpret_cast<float*>(lds_raw) + wave * (EPR * WTN);
+            // bf16 C: rounded once and staged per wave as bf16 rows [EPR][WTN]
+            // (16-byte chunks swizzled by row) in ring slots 2 and 3, two
+            // passes; every row leaves as 16 lanes x 16 bytes.
+            constexpr int CH = WTN / 8;  // 16-byte chunks per staged row
+            uint8_t* stage_b = lds + EPI_OFF + wave * (EPR * WTN * 2);
 #pragma unroll
             for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
                 for (int ii = 0; ii < 2; ++ii) {
                     const int i = pass * 2 + ii;
                     const int lr = ii * 32 + (lane & 31);
+                    // the row blocks not yet staged stay in the accumulator registers
+#pragma unroll
+                    for (int i2 = i; i2 < 4; ++i2)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) asm volatile("" : "+a"(acc[i2][j]));
 #pragma unroll
                     for (int j = 0; j < 4; ++j)
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
-                            const int ch = j * 8 + 2 * q + (lane >> 5);
-                            *reinterpret_cast<f32x4*>(stage_f + lr * WTN + ((ch ^ (lr & (CH - 1))) * 4)) =
-                                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                            // columns 32j + 8q + 4(lane / 32) .. + 3: half (lane / 32) of chunk 4j + q
+                            const int ch = j * 4 + q;
+                            *reinterpret_cast<uint2*>(stage_b + lr * (WTN * 2) + ((ch ^ (lr & (CH - 1))) * 16) + (lane >> 5) * 8) =
+                                make_uint2(pack_bf2(acc[i][j][4 * q], acc[i][j][4 * q + 1]),
+                                           pack_bf2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]));
                         }
                 }
                 __syncthreads();
@@ -449,11 +460,8 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
                         const int rr = lane / LPR + RPI * k;
                         const int m = mbase + pass * EPR + rr;
                         if (m >= t_rows || n >= nlim) continue;
-                        const float* src = stage_f + rr * WTN;
-                        const f32x4 v0 = *reinterpret_cast<const f32x4*>(src + (((2 * cl) ^ (rr & (CH - 1))) * 4));
-                        const f32x4 v1 = *reinterpret_cast<const f32x4*>(src + (((2 * cl + 1) ^ (rr & (CH - 1))) * 4));
-                        const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                        st16_nt(C + (int64_t)(t_row0 + m) * p.ldc + t_nt * BN + n, pack8(v));
+                        const uint4 v = *reinterpret_cast<const uint4*>(stage_b + rr * (WTN * 2) + ((cl ^ (rr & (CH - 1))) * 16));
+                        st16_nt(C + (int64_t)(t_row0 + m) * p.ldc + t_nt * BN + n, v);
                     }
                 }
                 __syncthreads();
@@ -463,6 +471,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
 
     set_tile(nt, e, row0);
     bool prefetched = false;
+    int late = 0;
     for (;;) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -478,7 +487,9 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
                 if (t < nk) dma_tile(t);
             wait_tiles(min(NST, nk) - 1);
         } else {
-            wait_vm<0>();  // the K steps requested before the last epilogue (and its stores)
+            // the K steps requested before the last epilogue's stores (and
+            // those stores); `late` K steps went out after them
+            wait_tiles(late);
         }
         __syncthreads();
         MX_LOAD_B(0, 0);
@@ -494,19 +505,29 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
         }
         __syncthreads();  // every wave has read its last fragments: the ring is free
 
-        // the workgroup's next tile: its first NST K steps load during the
-        // epilogue, two before it and one after each of its first two row
-        // blocks (a burst of all four slowed the epilogue's own stores)
+        // the workgroup's next tile: its first NST K steps load around the
+        // epilogue. Two go out before it; with QUANT_OUT one after each of its
+        // first two row blocks (a burst of all four slowed the epilogue's own
+        // stores), in bf16 after it (it stages through slots 2 and 3).
         int vb2 = vb + (int)gridDim.x, nt2 = 0, e2 = -1, row02 = 0, rows2 = 0;
-        const bool more = QUANT_OUT && find_tile(vb2, nt2, e2, row02, rows2);
+        const bool more = find_tile(vb2, nt2, e2, row02, rows2);
         if (more) {
             set_tile(nt2, e2, row02);
             dma_tile(0);
             if (1 < nk) dma_tile(1);
         }
         epilogue(row0, rows, nt, [&](int i) {
-            if (more && i < 2 && i + 2 < nk) dma_tile(i + 2);
+            if (QUANT_OUT && more && i < 2 && i + 2 < nk) dma_tile(i + 2);
         });
+        late = 0;
+        if (!QUANT_OUT && more) {
+#pragma unroll
+            for (int t = 2; t < NST; ++t)
+                if (t < nk) {
+                    dma_tile(t);
+                    ++late;
+                }
+        }
         if (!more) break;
         vb = vb2;
         nt = nt2;
@@ -544,15 +565,11 @@ hipError_t launch_mx_gemm(bool quant_out, const MxGemmParams& p, hipStream_t s) 
     const int64_t groups = ((mtiles + gm - 1) / gm) * ngn;
     const int64_t grid = (groups * 32 + 255) / 256 * 256;
     if (grid > 0x7fffffff) return hipErrorInvalidValue;
-    // The up GEMM runs persistent, one workgroup per CU (a multiple of 8, so
-    // each keeps its XCD); the down GEMM one workgroup per virtual block.
-    if (quant_out) {
-        const int64_t cus = cu_count() / 8 * 8;
-        const int64_t g = cus >= 8 && cus < grid ? cus : grid;
-        mx_gemm_kernel<true><<<(unsigned)g, 256, 0, s>>>(p, (int)grid);
-    } else {
-        mx_gemm_kernel<false><<<(unsigned)grid, 256, 0, s>>>(p, (int)grid);
-    }
+    // persistent: one workgroup per CU (a multiple of 8, so each keeps its XCD)
+    const int64_t cus = cu_count() / 8 * 8;
+    const int64_t g = cus >= 8 && cus < grid ? cus : grid;
+    if (quant_out) mx_gemm_kernel<true><<<(unsigned)g, 256, 0, s>>>(p, (int)grid);
+    else mx_gemm_kernel<false><<<(unsigned)g, 256, 0, s>>>(p, (int)grid);
     return hipGetLastError();
 }
 
