@@ -32,6 +32,8 @@
 // D[i][j] = sum_k src0[i][k] * src1[j][k] lands in lane j, register i as for
 // the bf16 32x32 MFMAs. Weights are src0 (rows = output columns n), the
 // activation terms src1 (lanes = token rows m), as in gemm.hip.
+#include <algorithm>
+
 #include "device_util.hpp"
 #include "moe_internal.hpp"
 
@@ -186,6 +188,43 @@ __global__ __launch_bounds__(kThreads) void mx_quant_rows_kernel(MxQuantParams p
     }
 }
 
+// Weight codes to K planes: blocks of RB rows x UB units of 32 bytes (one
+// unit = one row's codes of one K step; UB = min(32, K/64), RB * UB = 1024)
+// through LDS, read row by row and written unit by unit, so both sides move
+// runs of at least 512 bytes. Blocks of set 0 come first in the grid.
+__device__ __forceinline__ void planes_shape(int K, int& ub, int& rb) {
+    ub = min(32, K / 64);
+    rb = 1024 / ub;
+}
+__global__ __launch_bounds__(kThreads) void mx_weight_planes_kernel(MxPlanesParams p, int nb0) {
+    __shared__ uint4 t[2048 + 1024];  // RB rows of 2 UB uint4, one uint4 of padding per row (RB <= 1024)
+    const int w = (int)blockIdx.x < nb0 ? 0 : 1;
+    const int N = p.N[w], units = p.K[w] / 64;
+    int ub, rb;
+    planes_shape(p.K[w], ub, rb);
+    const int bx = (int)blockIdx.x - (w ? nb0 : 0);
+    const int ncu = (units + ub - 1) / ub, ncr = (N + rb - 1) / rb;
+    const int e = bx / (ncu * ncr), rem = bx % (ncu * ncr);
+    const int r0 = (rem / ncu) * rb, u0 = (rem % ncu) * ub;
+    const int64_t row_bytes = p.K[w] / 2;
+    const uint8_t* src = p.src[w][e];
+    uint8_t* dst = p.dst[w] + (int64_t)e * N * row_bytes;
+    const int nu = min(ub, units - u0), stride = 2 * ub + 1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q = threadIdx.x + kThreads * j, row = q / (2 * ub), hu = q % (2 * ub);
+        if ((hu >> 1) < nu && r0 + row < N)
+            t[row * stride + hu] = *reinterpret_cast<const uint4*>(src + (int64_t)(r0 + row) * row_bytes + u0 * 32 + hu * 16);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int q = threadIdx.x + kThreads * j, u = q / (2 * rb), row = (q % (2 * rb)) >> 1, half = q & 1;
+        if (u < nu && r0 + row < N)
+            *reinterpret_cast<uint4*>(dst + ((int64_t)(u0 + u) * N + r0 + row) * 32 + half * 16) = t[row * stride + u * 2 + half];
+    }
+}
+
 // QUANT_OUT: the output is SiLU(C) in MX6x2 (the next GEMM's activation);
 // otherwise C in bf16. nvb virtual blocks map to tiles; a workgroup takes
 // vb = blockIdx.x, blockIdx.x + gridDim.x, ... (one each when the grid holds
@@ -245,12 +284,12 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
     const uint32_t as_off = (uint32_t)(64 * wave + lane) * 4u;
     const uint32_t as_lds = A_BYTES + B_BYTES + 256u * (uint32_t)wave;
     constexpr uint32_t ws_lds = A_BYTES + B_BYTES + AS_BYTES;
-    // Per tile: the bases, and the weight offsets. Weight codes: lane pair
-    // (2m, 2m+1) loads the 32 contiguous bytes (both 32-blocks) of row m, so a
-    // wave load covers 32 rows x 32 bytes rather than 64 rows x 16 bytes. In
-    // LDS the row's two 16-byte halves are swapped when bit 3 of the row is
-    // set, which keeps the fragment reads (16 rows at a 32-byte stride) free
-    // of bank conflicts. Rows past N are clamped to N - 1.
+    // Per tile: the bases, and the weight offsets. Weight codes are in K
+    // planes ([K/64][N][32]), so a tile's K step is one contiguous 8 KiB
+    // block: lane pair (2m, 2m+1) loads the 32 bytes (both 32-blocks) of row
+    // m. In LDS the row's two 16-byte halves are swapped when bit 3 of the
+    // row is set, which keeps the fragment reads (16 rows at a 32-byte stride)
+    // free of bank conflicts. Rows past N are clamped to N - 1.
     const uint8_t *a_base = nullptr, *as_base = nullptr, *wq = nullptr, *wsc = nullptr;
     uint32_t b_off[B_LOADS], ws_off = 0;
     auto set_tile = [&](int t_nt, int t_e, int t_row0) {
@@ -262,7 +301,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
         for (int i = 0; i < B_LOADS; ++i) {
             const int s = (wave * B_LOADS + i) * 64 + lane;  // 16-byte slot of the B region: row s/2, half s%2
             const int n = s >> 1, kb = (s & 1) ^ ((n >> 3) & 1);
-            b_off[i] = (uint32_t)(min(t_nt * BN + n, p.N - 1) * (int64_t)(p.K / 2) + kb * 16);
+            b_off[i] = (uint32_t)(min(t_nt * BN + n, p.N - 1) * 32 + kb * 16);
         }
         ws_off = (uint32_t)(((lane >> 4) & 1) * p.N + min(t_nt * BN + (lane & 15) * 16, p.N - 16));
     };
@@ -271,7 +310,7 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
     auto dma_tile = [&](int t) {
         const uint32_t sb = lds0 + (uint32_t)((t % NST) * STAGE);
         const uint8_t* ab = a_base + (int64_t)t * a_plane;
-        const uint8_t* bb = wq + (int64_t)t * 32;
+        const uint8_t* bb = wq + (int64_t)t * p.N * 32;
 #pragma unroll
         for (int i = 0; i < A_LOADS; ++i) dma16(ab, a_off[i], sb + (uint32_t)(wave * A_LOADS + i) * 1024u);
 #pragma unroll
@@ -543,6 +582,20 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
 }
 
 }  // namespace
+
+hipError_t launch_mx_weight_planes(const MxPlanesParams& p, hipStream_t s) {
+    if (p.E <= 0) return hipSuccess;
+    if (p.E > kMaxExperts) return hipErrorInvalidValue;
+    int64_t nb[2];
+    for (int w = 0; w < 2; ++w) {
+        if (p.N[w] <= 0 || p.N[w] % 32 != 0 || p.K[w] <= 0 || p.K[w] % 64 != 0) return hipErrorInvalidValue;
+        const int ub = std::min(32, p.K[w] / 64), rb = 1024 / ub;
+        nb[w] = (int64_t)p.E * ((p.K[w] / 64 + ub - 1) / ub) * ((p.N[w] + rb - 1) / rb);
+    }
+    if (nb[0] + nb[1] > 0x7fffffff) return hipErrorInvalidValue;
+    mx_weight_planes_kernel<<<(unsigned)(nb[0] + nb[1]), kThreads, 0, s>>>(p, (int)nb[0]);
+    return hipGetLastError();
+}
 
 hipError_t launch_mx_quant_rows(const MxQuantParams& p, hipStream_t s) {
     if (p.rows <= 0) return hipSuccess;

@@ -127,6 +127,8 @@ struct tmt_moe {
     uint16_t* wt = nullptr;  // W_up transposed ([E][d][hn]) for the backward's GEMM_DX (nullptr: none)
     // MX handles: activations of the two expert GEMMs as two MXFP6 terms
     uint8_t *xq = nullptr, *xq_scales = nullptr, *aq = nullptr, *aq_scales = nullptr;
+    // and the call's weight codes in K planes: W_up [E][h][d/2], then W_down [E][d][h/2]
+    uint8_t* wplanes = nullptr;
     float *dlogits, *dwr_partial;
     // LayerNorm in front of the block (tmt_moe_forward_ln / tmt_moe_backward_ln)
     uint16_t *H, *dH;
@@ -275,6 +277,7 @@ Sizes plan(const tmt_moe_desc* user, tmt_moe* m) {
     size_t o_dpart = dsplit ? W.add((size_t)2 * std::min<int64_t>(T, kSkinnyMaxTokens) * K * D * 4) : 0;
     size_t o_xq = mx ? W.add(mx_codes_bytes(TK, D)) : 0, o_xqs = mx ? W.add(mx_scales_bytes(TK, D)) : 0;
     size_t o_aq = mx ? W.add(mx_codes_bytes(TK, h)) : 0, o_aqs = mx ? W.add(mx_scales_bytes(TK, h)) : 0;
+    size_t o_wpl = mx ? W.add((size_t)E * h * D) : 0;
     const int64_t ln_rows = std::max(scatter_blocks((int)T), ln_chunks((int)T));
     size_t o_lnp = bwd ? W.add((size_t)ln_rows * 2 * D * 4) : 0;
     size_t o_lnp2 = bwd ? W.add((size_t)colsum_groups((int)ln_rows) * 2 * D * 4) : 0;
@@ -326,6 +329,7 @@ Sizes plan(const tmt_moe_desc* user, tmt_moe* m) {
         m->xq_scales = mx ? (uint8_t*)(w + o_xqs) : nullptr;
         m->aq = mx ? (uint8_t*)(w + o_aq) : nullptr;
         m->aq_scales = mx ? (uint8_t*)(w + o_aqs) : nullptr;
+        m->wplanes = mx ? (uint8_t*)(w + o_wpl) : nullptr;
         m->O = h > 0 ? (uint16_t*)(a + o_O) : nullptr;
         m->dO = bwd ? (uint16_t*)(w + o_dO) : nullptr;
         m->dU = bwd ? (h > 0 ? (uint16_t*)(w + o_dU) : m->dO) : nullptr;  // h == 0: combine_bwd writes dU
@@ -1051,16 +1055,24 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
         qp.slot_of = E > 1 ? m->slot_of : nullptr; qp.copies = E > 1 ? K : 1;
         qp.codes = m->xq; qp.scales = m->xq_scales; qp.srows = srows;
         LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_quant_rows(qp, s));
+        // the weight codes of both GEMMs in K planes, so that a tile's K step
+        // is one contiguous block (one launch, counted in the up phase)
+        MxPlanesParams wp{};
+        for (int e = 0; e < E; ++e) { wp.src[0][e] = W_up[e]; wp.src[1][e] = W_down[e]; }
+        wp.dst[0] = m->wplanes;
+        wp.dst[1] = m->wplanes + (size_t)E * h * d / 2;
+        wp.N[0] = h; wp.K[0] = d; wp.N[1] = d; wp.K[1] = h; wp.E = E;
+        LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_weight_planes(wp, s));
         MxGemmParams up{};
         up.offsets = m->offsets; up.E = E; up.N = h; up.K = d; up.slots = TK;
         up.a_codes = m->xq; up.a_scales = m->xq_scales; up.a_srows = srows;
-        for (int e = 0; e < E; ++e) { up.wq[e] = W_up[e]; up.wsc[e] = W_up_scale[e]; }
+        for (int e = 0; e < E; ++e) { up.wq[e] = wp.dst[0] + (size_t)e * h * d / 2; up.wsc[e] = W_up_scale[e]; }
         up.q_codes = m->aq; up.q_scales = m->aq_scales; up.q_srows = srows;
         LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_gemm(true, up, s));
         MxGemmParams dn{};
         dn.offsets = m->offsets; dn.E = E; dn.N = d; dn.K = h; dn.slots = TK;
         dn.a_codes = m->aq; dn.a_scales = m->aq_scales; dn.a_srows = srows;
-        for (int e = 0; e < E; ++e) { dn.wq[e] = W_down[e]; dn.wsc[e] = W_down_scale[e]; }
+        for (int e = 0; e < E; ++e) { dn.wq[e] = wp.dst[1] + (size_t)e * d * h / 2; dn.wsc[e] = W_down_scale[e]; }
         dn.c = m->O; dn.ldc = d;
         LAUNCH(TMT_MOE_PH_GEMM_DOWN, launch_mx_gemm(false, dn, s));
         CombineParams cp{};

@@ -236,6 +236,15 @@ struct MxQuantParams {
     int64_t srows;
 };
 hipError_t launch_mx_quant_rows(const MxQuantParams& p, hipStream_t s);
+// MXFP4 weight codes [N][K/2] (the caller's layout) to K planes of 64:
+// [K/64][N][32] bytes per expert, for two matrix sets (w = 0, 1) at once.
+struct MxPlanesParams {
+    const uint8_t* src[2][kMaxExperts];
+    uint8_t* dst[2];  // expert e at dst[w] + e * N[w] * K[w] / 2
+    int N[2], K[2];
+    int E;
+};
+hipError_t launch_mx_weight_planes(const MxPlanesParams& p, hipStream_t s);
 struct MxGemmParams {
     const int32_t* offsets;  // [E+1] expert segments (slot space)
     int E;
@@ -243,7 +252,7 @@ struct MxGemmParams {
     const uint8_t* a_codes;  // activations, MX6x2 planes in slot order (srows = a_srows)
     const uint8_t* a_scales;
     int64_t a_srows;
-    const uint8_t* wq[kMaxExperts];   // e2m1 codes [N][K/2] per expert
+    const uint8_t* wq[kMaxExperts];   // e2m1 codes in K planes [K/64][N][32] per expert
     const uint8_t* wsc[kMaxExperts];  // e8m0 scales [K/32][N] per expert
     uint16_t* c;             // bf16 output [slots][ldc] (quant_out == false)
     int64_t ldc;
