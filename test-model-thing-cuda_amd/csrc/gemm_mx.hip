@@ -17,8 +17,8 @@
 //
 // Activation tensors ("MX6x2"), rows R, length K (K % 64 == 0), in planes of
 // 64 columns so that the 256 rows of a tile's K step are one contiguous
-// 24 KiB block (rows R apart at a large stride put a K step's loads on a few
-// L2 channels: at c5 the down GEMM ran 1.64 ms that way, 1.33 ms in planes):
+// 24 KiB block (with rows R apart at a large stride, the loads bound the
+// K loop: at c5 the down GEMM ran 1.64 ms that way, 1.33 ms in planes):
 //   codes  [K/64][srows][96] bytes: per row, block 2c then block 2c+1 of
 //          plane c, each term 0 (24 bytes, element i at bits 6i..6i+5,
 //          little-endian) then term 1;
