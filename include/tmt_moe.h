@@ -64,8 +64,16 @@ enum {
  *   MXFP4_MX  MXFP4 weights on the scaled MFMA, activations rounded to the
  *             sum of two MXFP6 (e2m3) terms per 32-element block (relative
  *             L2 error of the block output about 1e-3), about twice the MFMA
- *             rate of the bf16 products (forward only). */
-enum { TMT_MOE_WEIGHTS_BF16 = 0, TMT_MOE_WEIGHTS_MXFP4 = 1, TMT_MOE_WEIGHTS_MXFP4_MX = 2 };
+ *             rate of the bf16 products (forward only);
+ *   MXFP4_MX_PLANES  the same arithmetic with the weight codes already in the
+ *             kernels' K-plane layout (tmt_moe_mxfp4_planes), which spares
+ *             each forward the copy into it. */
+enum {
+    TMT_MOE_WEIGHTS_BF16 = 0,
+    TMT_MOE_WEIGHTS_MXFP4 = 1,
+    TMT_MOE_WEIGHTS_MXFP4_MX = 2,
+    TMT_MOE_WEIGHTS_MXFP4_MX_PLANES = 3
+};
 
 typedef struct tmt_moe_desc {
     int32_t max_tokens;     /* T_max: largest T a call may pass */
@@ -129,8 +137,8 @@ int tmt_moe_forward(tmt_moe* moe, void* stream, int32_t T, const uint16_t* X,
                     uint16_t* Y, float beta);
 
 /*
- * MXFP4 variant of tmt_moe_forward for weight_format TMT_MOE_WEIGHTS_MXFP4 or
- * TMT_MOE_WEIGHTS_MXFP4_MX
+ * MXFP4 variant of tmt_moe_forward for weight_format TMT_MOE_WEIGHTS_MXFP4,
+ * TMT_MOE_WEIGHTS_MXFP4_MX or TMT_MOE_WEIGHTS_MXFP4_MX_PLANES
  * (no reference counterpart: the reference has no FP4 path). OCP MX format:
  * e2m1 values in blocks of 32 along the reduction dimension sharing one e8m0
  * scale 2^(s-127). Per expert e:
@@ -143,6 +151,8 @@ int tmt_moe_forward(tmt_moe* moe, void* stream, int32_t T, const uint16_t* X,
  * dequantised weights. With MXFP4_MX, the block input and the SiLU output
  * are rounded to two MXFP6 terms and both expert GEMMs run on the scaled
  * FP6 x FP4 MFMA. Forward only: backward needs bf16 master weights.
+ * With MXFP4_MX_PLANES, W_up[e] and W_down[e] hold the codes in K planes as
+ * tmt_moe_mxfp4_planes writes them; the scales keep the layout above.
  */
 int tmt_moe_forward_mxfp4(tmt_moe* moe, void* stream, int32_t T,
                           const uint16_t* X, const uint16_t* Wr,
@@ -150,6 +160,19 @@ int tmt_moe_forward_mxfp4(tmt_moe* moe, void* stream, int32_t T,
                           const uint8_t* const* W_up, const uint8_t* const* W_up_scale,
                           const uint8_t* const* W_down, const uint8_t* const* W_down_scale,
                           uint16_t* Y, float beta);
+
+/*
+ * MXFP4 weight codes [N][K/2] (the layout above: N output rows, K reduction
+ * columns, low nibble = even column) to K planes of 64 columns,
+ * [K/64][N][32] bytes: plane p holds the 32 code bytes of columns 64p ..
+ * 64p + 63 of every row, rows in order. No counterpart in the reference (it
+ * has no FP4 path); for callers of TMT_MOE_WEIGHTS_MXFP4_MX_PLANES, who pack
+ * each expert matrix once (W_up[e]: N = h, K = d; W_down[e]: N = d, K = h)
+ * instead of every forward doing it. N and K multiples of 64; codes and
+ * planes 16-byte aligned device buffers of N * K / 2 bytes; enqueued on
+ * `stream` on the current device.
+ */
+int tmt_moe_mxfp4_planes(void* stream, const uint8_t* codes, int32_t N, int32_t K, uint8_t* planes);
 
 /*
  * Replaces moe_backward (moe.cu:479-545) for the loss

@@ -586,13 +586,15 @@ __global__ __launch_bounds__(256, 1) void mx_gemm_kernel(MxGemmParams p, int nvb
 hipError_t launch_mx_weight_planes(const MxPlanesParams& p, hipStream_t s) {
     if (p.E <= 0) return hipSuccess;
     if (p.E > kMaxExperts) return hipErrorInvalidValue;
-    int64_t nb[2];
+    int64_t nb[2] = {0, 0};
     for (int w = 0; w < 2; ++w) {
-        if (p.N[w] <= 0 || p.N[w] % 32 != 0 || p.K[w] <= 0 || p.K[w] % 64 != 0) return hipErrorInvalidValue;
+        if (p.N[w] == 0) continue;  // an empty set
+        if (p.N[w] < 0 || p.N[w] % 32 != 0 || p.K[w] <= 0 || p.K[w] % 64 != 0) return hipErrorInvalidValue;
         const int ub = std::min(32, p.K[w] / 64), rb = 1024 / ub;
         nb[w] = (int64_t)p.E * ((p.K[w] / 64 + ub - 1) / ub) * ((p.N[w] + rb - 1) / rb);
     }
     if (nb[0] + nb[1] > 0x7fffffff) return hipErrorInvalidValue;
+    if (nb[0] + nb[1] == 0) return hipSuccess;
     mx_weight_planes_kernel<<<(unsigned)(nb[0] + nb[1]), kThreads, 0, s>>>(p, (int)nb[0]);
     return hipGetLastError();
 }

@@ -163,6 +163,9 @@ bool is_padded(const tmt_moe_desc& u) {
     return d.d != u.d || d.hidden != u.hidden;
 }
 
+// The weight formats on the scaled FP6 x FP4 MFMA.
+bool is_mx(int fmt) { return fmt == TMT_MOE_WEIGHTS_MXFP4_MX || fmt == TMT_MOE_WEIGHTS_MXFP4_MX_PLANES; }
+
 int validate_desc(const tmt_moe_desc* d) {
     if (!d) return fail(TMT_MOE_EINVAL, "descriptor is NULL");
     if (d->max_tokens < 1) return fail(TMT_MOE_EINVAL, "max_tokens must be >= 1");
@@ -177,9 +180,9 @@ int validate_desc(const tmt_moe_desc* d) {
     if ((int64_t)d->max_tokens * d->topk >= (1ll << 31))
         return fail(TMT_MOE_EINVAL, "max_tokens*topk must fit in int32");
     if (d->weight_format != TMT_MOE_WEIGHTS_BF16 && d->weight_format != TMT_MOE_WEIGHTS_MXFP4 &&
-        d->weight_format != TMT_MOE_WEIGHTS_MXFP4_MX)
+        !is_mx(d->weight_format))
         return fail(TMT_MOE_EINVAL, "unknown weight_format %d", d->weight_format);
-    if (d->weight_format == TMT_MOE_WEIGHTS_MXFP4_MX) {
+    if (is_mx(d->weight_format)) {
         // the scaled-MFMA GEMMs address operands with 32-bit byte offsets
         const int64_t TK = (int64_t)d->max_tokens * d->topk;
         const int64_t widest = std::max<int64_t>(d->d, d->hidden);
@@ -243,7 +246,7 @@ Sizes plan(const tmt_moe_desc* user, tmt_moe* m) {
     size_t o_ticket = L.add(4);
     size_t o_perm = L.add(TK * 4), o_slot = L.add(TK * 4);
     // MX handles (scaled-MFMA FP4 forward) keep activations in MX6x2 form instead of U / SiLU(U)
-    const bool mx = d->weight_format == TMT_MOE_WEIGHTS_MXFP4_MX;
+    const bool mx = is_mx(d->weight_format);
     // U: the single linear's output (hidden = 0), else silu'(U) for the
     // backward; MXFP4 handles are forward-only and keep neither
     const bool fp4 = d->weight_format != TMT_MOE_WEIGHTS_BF16;
@@ -277,7 +280,7 @@ Sizes plan(const tmt_moe_desc* user, tmt_moe* m) {
     size_t o_dpart = dsplit ? W.add((size_t)2 * std::min<int64_t>(T, kSkinnyMaxTokens) * K * D * 4) : 0;
     size_t o_xq = mx ? W.add(mx_codes_bytes(TK, D)) : 0, o_xqs = mx ? W.add(mx_scales_bytes(TK, D)) : 0;
     size_t o_aq = mx ? W.add(mx_codes_bytes(TK, h)) : 0, o_aqs = mx ? W.add(mx_scales_bytes(TK, h)) : 0;
-    size_t o_wpl = mx ? W.add((size_t)E * h * D) : 0;
+    size_t o_wpl = d->weight_format == TMT_MOE_WEIGHTS_MXFP4_MX ? W.add((size_t)E * h * D) : 0;
     const int64_t ln_rows = std::max(scatter_blocks((int)T), ln_chunks((int)T));
     size_t o_lnp = bwd ? W.add((size_t)ln_rows * 2 * D * 4) : 0;
     size_t o_lnp2 = bwd ? W.add((size_t)colsum_groups((int)ln_rows) * 2 * D * 4) : 0;
@@ -329,7 +332,7 @@ Sizes plan(const tmt_moe_desc* user, tmt_moe* m) {
         m->xq_scales = mx ? (uint8_t*)(w + o_xqs) : nullptr;
         m->aq = mx ? (uint8_t*)(w + o_aq) : nullptr;
         m->aq_scales = mx ? (uint8_t*)(w + o_aqs) : nullptr;
-        m->wplanes = mx ? (uint8_t*)(w + o_wpl) : nullptr;
+        m->wplanes = d->weight_format == TMT_MOE_WEIGHTS_MXFP4_MX ? (uint8_t*)(w + o_wpl) : nullptr;
         m->O = h > 0 ? (uint16_t*)(a + o_O) : nullptr;
         m->dO = bwd ? (uint16_t*)(w + o_dO) : nullptr;
         m->dU = bwd ? (h > 0 ? (uint16_t*)(w + o_dU) : m->dO) : nullptr;  // h == 0: combine_bwd writes dU
@@ -1028,7 +1031,7 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
                           uint16_t* Y, float beta) {
     if (!m) return fail(TMT_MOE_EINVAL, "handle is NULL");
     const tmt_moe_desc& ds = m->desc;
-    if (ds.weight_format != TMT_MOE_WEIGHTS_MXFP4 && ds.weight_format != TMT_MOE_WEIGHTS_MXFP4_MX)
+    if (ds.weight_format != TMT_MOE_WEIGHTS_MXFP4 && !is_mx(ds.weight_format))
         return fail(TMT_MOE_EINVAL, "handle expects bf16 weights: use tmt_moe_forward");
     if (T < 0 || T > ds.max_tokens) return fail(TMT_MOE_EINVAL, "T=%d outside [0, %d]", T, ds.max_tokens);
     const int E = ds.experts, K = ds.topk, d = ds.d, h = ds.hidden;
@@ -1045,7 +1048,7 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
     m->last_T = -1;
     m->last_ln = false;
     if ((rc = route(m, s, T, X, Wr, logit_bias))) return rc;
-    if (T > 0 && ds.weight_format == TMT_MOE_WEIGHTS_MXFP4_MX) {
+    if (T > 0 && is_mx(ds.weight_format)) {
         const int TK = T * K;
         const int64_t srows = (int64_t)ds.max_tokens * K + kMxScalePadRows;
         // X is rounded once per token and written to the token's K slots, so
@@ -1056,23 +1059,34 @@ int tmt_moe_forward_mxfp4(tmt_moe* m, void* stream, int32_t T, const uint16_t* X
         qp.codes = m->xq; qp.scales = m->xq_scales; qp.srows = srows;
         LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_quant_rows(qp, s));
         // the weight codes of both GEMMs in K planes, so that a tile's K step
-        // is one contiguous block (one launch, counted in the up phase)
-        MxPlanesParams wp{};
-        for (int e = 0; e < E; ++e) { wp.src[0][e] = W_up[e]; wp.src[1][e] = W_down[e]; }
-        wp.dst[0] = m->wplanes;
-        wp.dst[1] = m->wplanes + (size_t)E * h * d / 2;
-        wp.N[0] = h; wp.K[0] = d; wp.N[1] = d; wp.K[1] = h; wp.E = E;
-        LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_weight_planes(wp, s));
+        // is one contiguous block: given so (MX_PLANES), or copied here (one
+        // launch, counted in the up phase)
+        const uint8_t* wup_pl[kMaxExperts];
+        const uint8_t* wdn_pl[kMaxExperts];
+        if (ds.weight_format == TMT_MOE_WEIGHTS_MXFP4_MX_PLANES) {
+            for (int e = 0; e < E; ++e) { wup_pl[e] = W_up[e]; wdn_pl[e] = W_down[e]; }
+        } else {
+            MxPlanesParams wp{};
+            for (int e = 0; e < E; ++e) { wp.src[0][e] = W_up[e]; wp.src[1][e] = W_down[e]; }
+            wp.dst[0] = m->wplanes;
+            wp.dst[1] = m->wplanes + (size_t)E * h * d / 2;
+            wp.N[0] = h; wp.K[0] = d; wp.N[1] = d; wp.K[1] = h; wp.E = E;
+            LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_weight_planes(wp, s));
+            for (int e = 0; e < E; ++e) {
+                wup_pl[e] = wp.dst[0] + (size_t)e * h * d / 2;
+                wdn_pl[e] = wp.dst[1] + (size_t)e * d * h / 2;
+            }
+        }
         MxGemmParams up{};
         up.offsets = m->offsets; up.E = E; up.N = h; up.K = d; up.slots = TK;
         up.a_codes = m->xq; up.a_scales = m->xq_scales; up.a_srows = srows;
-        for (int e = 0; e < E; ++e) { up.wq[e] = wp.dst[0] + (size_t)e * h * d / 2; up.wsc[e] = W_up_scale[e]; }
+        for (int e = 0; e < E; ++e) { up.wq[e] = wup_pl[e]; up.wsc[e] = W_up_scale[e]; }
         up.q_codes = m->aq; up.q_scales = m->aq_scales; up.q_srows = srows;
         LAUNCH(TMT_MOE_PH_GEMM_UP, launch_mx_gemm(true, up, s));
         MxGemmParams dn{};
         dn.offsets = m->offsets; dn.E = E; dn.N = d; dn.K = h; dn.slots = TK;
         dn.a_codes = m->aq; dn.a_scales = m->aq_scales; dn.a_srows = srows;
-        for (int e = 0; e < E; ++e) { dn.wq[e] = wp.dst[1] + (size_t)e * d * h / 2; dn.wsc[e] = W_down_scale[e]; }
+        for (int e = 0; e < E; ++e) { dn.wq[e] = wdn_pl[e]; dn.wsc[e] = W_down_scale[e]; }
         dn.c = m->O; dn.ldc = d;
         LAUNCH(TMT_MOE_PH_GEMM_DOWN, launch_mx_gemm(false, dn, s));
         CombineParams cp{};
@@ -1295,6 +1309,23 @@ int tmt_moe_f32_to_bf16(void* stream, const float* in, uint16_t* out, int64_t n)
     if (n < 0) return fail(TMT_MOE_EINVAL, "n=%lld < 0", (long long)n);
     if (n > 0 && (!in || !out)) return fail(TMT_MOE_EINVAL, "in and out must be non-NULL");
     HIP_TRY(launch_f32_to_bf16(in, out, n, (hipStream_t)stream));
+    return TMT_MOE_OK;
+}
+
+int tmt_moe_mxfp4_planes(void* stream, const uint8_t* codes, int32_t N, int32_t K, uint8_t* planes) {
+    if (N <= 0 || K <= 0 || N % 64 != 0 || K % 64 != 0)
+        return fail(TMT_MOE_EINVAL, "N=%d and K=%d must be positive multiples of 64", N, K);
+    if ((int64_t)N * (K / 2) >= (int64_t(1) << 31)) return fail(TMT_MOE_EINVAL, "N*K/2 must fit in int32");
+    if (!codes || !planes) return fail(TMT_MOE_EINVAL, "codes and planes must be non-NULL");
+    if (!aligned16(codes) || !aligned16(planes)) return fail(TMT_MOE_EINVAL, "codes and planes must be 16-byte aligned");
+    if (codes == planes) return fail(TMT_MOE_EINVAL, "codes and planes must not be the same buffer");
+    MxPlanesParams p{};
+    p.src[0][0] = codes;
+    p.dst[0] = planes;
+    p.N[0] = N;
+    p.K[0] = K;
+    p.E = 1;  // set 1 empty (N = 0)
+    HIP_TRY(launch_mx_weight_planes(p, (hipStream_t)stream));
     return TMT_MOE_OK;
 }
 

@@ -241,7 +241,7 @@ hipError_t launch_mx_quant_rows(const MxQuantParams& p, hipStream_t s);
 struct MxPlanesParams {
     const uint8_t* src[2][kMaxExperts];
     uint8_t* dst[2];  // expert e at dst[w] + e * N[w] * K[w] / 2
-    int N[2], K[2];
+    int N[2], K[2];   // N[w] == 0: set w is empty
     int E;
 };
 hipError_t launch_mx_weight_planes(const MxPlanesParams& p, hipStream_t s);

@@ -24,6 +24,7 @@ LIB_PATH = os.path.join(_HERE, "libtmt_moe.so")
 WEIGHTS_BF16 = 0
 WEIGHTS_MXFP4 = 1
 WEIGHTS_MXFP4_MX = 2
+WEIGHTS_MXFP4_MX_PLANES = 3
 
 EXPORTED = (
     "tmt_moe_create",
@@ -51,6 +52,7 @@ EXPORTED = (
     "tmt_moe_adamw_zero_grads",
     "tmt_moe_adamw_chunks",
     "tmt_moe_f32_to_bf16",
+    "tmt_moe_mxfp4_planes",
     "tmt_moe_set_profiling",
     "tmt_moe_read_profile",
     "tmt_moe_phase_name",
@@ -111,6 +113,7 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.tmt_moe_adamw_zero_grads.argtypes = [vp, vp]
     lib.tmt_moe_adamw_chunks.argtypes = [vp, ctypes.POINTER(i32)]
     lib.tmt_moe_f32_to_bf16.argtypes = [vp, vp, vp, ctypes.c_int64]
+    lib.tmt_moe_mxfp4_planes.argtypes = [vp, vp, i32, i32, vp]
     lib.tmt_moe_read_stats.argtypes = [vp, vp, vp, vp, vp]
     lib.tmt_moe_stats_device_ptr.argtypes = [vp, pp]
     lib.tmt_moe_read_routing.argtypes = [vp, vp, vp, vp, vp, vp, vp, vp, vp]
@@ -220,6 +223,14 @@ def layernorm_backward_noalloc(S, dH, gamma, mean, rstd, dS, dGamma, dBeta, stre
     _check(load_library().tmt_moe_layernorm_backward_noalloc(
         _stream(stream), T, d, _ptr(S), _ptr(dH), _ptr(gamma), _ptr(mean), _ptr(rstd), _ptr(dS),
         _ptr(dGamma), _ptr(dBeta)))
+
+
+def mxfp4_planes(codes, planes, stream=None) -> None:
+    """MXFP4 weight codes [N, K/2] (uint8, the tmt_moe_forward_mxfp4 layout)
+    to the K-plane layout [K/64, N, 32] that WEIGHTS_MXFP4_MX_PLANES handles
+    take: one expert matrix, device tensors, enqueued on `stream`."""
+    N, half = int(codes.shape[0]), int(codes.shape[1])
+    _check(load_library().tmt_moe_mxfp4_planes(_stream(stream), _ptr(codes), N, 2 * half, _ptr(planes)))
 
 
 class MoE:

@@ -71,6 +71,8 @@ def test_shared_workspace_split():
     # the MXFP4 formats keep whole 64-wide K steps (blocks of 32 along d and h)
     ((16, 100, 4, 2, 256, tmt_moe.WEIGHTS_MXFP4), "multiples of 64"),
     ((16, 256, 4, 2, 100, tmt_moe.WEIGHTS_MXFP4_MX), "multiples of 64"),
+    ((16, 256, 4, 2, 100, tmt_moe.WEIGHTS_MXFP4_MX_PLANES), "multiples of 64"),
+    ((16, 256, 4, 2, 256, 4), "weight_format"),
 ])
 def test_invalid_descriptors_are_rejected(desc, msg):
     with pytest.raises(tmt_moe.MoeError) as ei:
@@ -220,3 +222,17 @@ def test_product_path_never_touches_the_oracle():
                 line = next(n.lineno for n in ast.walk(tree)
                             if isinstance(n, (ast.Import, ast.ImportFrom)) and node in n.names)
             assert any(a <= line <= b for a, b in allowed), f"bench.py:{line} uses the oracle"
+
+
+@pytest.mark.parametrize("N,K,null,msg", [
+    (100, 256, False, "multiples of 64"),
+    (256, 96, False, "multiples of 64"),
+    (0, 256, False, "multiples of 64"),
+    (256, 256, True, "non-NULL"),
+])
+def test_mxfp4_planes_rejects_bad_arguments(N, K, null, msg):
+    """The K-plane packer checks its arguments before any device work."""
+    lib = tmt_moe.load_library()
+    p = None if null else 4096
+    rc = lib.tmt_moe_mxfp4_planes(None, p, N, K, p and 8192)
+    assert rc != 0 and msg in tmt_moe.last_error()

@@ -42,7 +42,16 @@ def rel_l2(a, b):
     return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-30))
 
 
-FORMATS = [tmt_moe.WEIGHTS_MXFP4, tmt_moe.WEIGHTS_MXFP4_MX]
+FORMATS = [tmt_moe.WEIGHTS_MXFP4, tmt_moe.WEIGHTS_MXFP4_MX, tmt_moe.WEIGHTS_MXFP4_MX_PLANES]
+
+
+def planes(codes):
+    """Per-expert K-plane copies of stacked codes [E, N, K/2] (the layout
+    WEIGHTS_MXFP4_MX_PLANES handles take)."""
+    out = torch.empty_like(codes)
+    for e in range(codes.shape[0]):
+        tmt_moe.mxfp4_planes(codes[e], out[e])
+    return out
 
 
 def run_fp4(case, K, h, beta=0.0, Y0=None, fmt=tmt_moe.WEIGHTS_MXFP4, max_tokens=None):
@@ -52,8 +61,11 @@ def run_fp4(case, K, h, beta=0.0, Y0=None, fmt=tmt_moe.WEIGHTS_MXFP4, max_tokens
     m = tmt_moe.MoE(max_tokens or max(T, 1), d, E, K, h, weight_format=fmt)
     Y = dev16(Y0) if Y0 is not None else torch.zeros(T, d, dtype=torch.bfloat16, device="cuda")
     bias = torch.from_numpy(case["bias"]).cuda() if case.get("bias") is not None else None
-    m.forward_mxfp4(dev16(case["X"]), dev16(case["Wr"]), dev8(qu["codes"]), dev8(qu["scales"]),
-                    dev8(qd["codes"]), dev8(qd["scales"]), Y, beta=beta, bias=bias)
+    cu, cd = dev8(qu["codes"]), dev8(qd["codes"])
+    if fmt == tmt_moe.WEIGHTS_MXFP4_MX_PLANES:
+        cu, cd = planes(cu), planes(cd)
+    m.forward_mxfp4(dev16(case["X"]), dev16(case["Wr"]), cu, dev8(qu["scales"]),
+                    cd, dev8(qd["scales"]), Y, beta=beta, bias=bias)
     out = {"Y": bf16_to_f32(Y.view(torch.int16).cpu().numpy().view(np.uint16))}
     out.update(m.routing())
     m.close()
@@ -108,6 +120,30 @@ def test_mxfp4_c5_full_size(orc, fmt):
     err = rel_l2(g["Y"], ref["Y"].cpu().numpy())
     say(f"  Y rel-L2 {err:.2e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("N,K", [(256, 1024), (1024, 4096), (192, 64), (64, 2112)])
+def test_mxfp4_planes_layout(N, K):
+    """tmt_moe_mxfp4_planes: plane p, row n holds bytes 32p .. 32p + 31 of
+    code row n (columns 64p .. 64p + 63), against a numpy restatement."""
+    say(f"mxfp4 planes layout N={N} K={K}")
+    codes = np.random.default_rng(N + K).integers(0, 256, size=(N, K // 2), dtype=np.uint8)
+    out = torch.zeros(N * K // 2, dtype=torch.uint8, device="cuda")
+    tmt_moe.mxfp4_planes(dev8(codes), out)
+    torch.cuda.synchronize()
+    want = codes.reshape(N, K // 64, 32).transpose(1, 0, 2)
+    assert np.array_equal(out.cpu().numpy().reshape(K // 64, N, 32), want)
+
+
+@pytest.mark.parametrize("T,d,E,K,h", [(300, 256, 8, 2, 512), (5, 512, 4, 2, 192), (2048, 1024, 32, 4, 256)])
+def test_mx_planes_format_equals_mx(T, d, E, K, h):
+    """Pre-packed weights run the same arithmetic as the MX format over the
+    caller's layout: the outputs are bit-identical."""
+    say(f"mx planes vs mx T={T} d={d} E={E} K={K} h={h}")
+    case = make_case(T, d, E, K, h, seed=91 + T)
+    a, _, _ = run_fp4(case, K, h, fmt=tmt_moe.WEIGHTS_MXFP4_MX)
+    b, _, _ = run_fp4(case, K, h, fmt=tmt_moe.WEIGHTS_MXFP4_MX_PLANES)
+    assert np.array_equal(a["Y"].view(np.uint32), b["Y"].view(np.uint32))
 
 
 def test_mxfp4_handle_rejects_backward_and_bf16_forward():
