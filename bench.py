@@ -700,22 +700,24 @@ def main():
     for ph, (tot_ms, n) in prof.items():
         if n == 0:
             continue
-        avg = tot_ms / n
+        # the phase's work is done once per step, by all of its launches
+        # (e.g. gemm_dx: the W_up transpose and the GEMM over it)
+        per_step = tot_ms / prof_steps
         kind, work = kernel_work(ph, T, d, E, K, h)
-        k = {"avg_ms": round(avg, 4), "launches_per_step": n / prof_steps,
-             "share": round(tot_ms / prof_steps / ms_step, 4)}
+        k = {"avg_ms": round(tot_ms / n, 4), "launches_per_step": n / prof_steps, "ms_per_step": round(per_step, 4),
+             "share": round(per_step / ms_step, 4)}
         if kind == "mfma":
-            k["tflops"] = round(work / avg / 1e9, 1)
-            k["mfma_frac"] = round(work / avg / 1e9 / PEAK_BF16_TFLOPS, 4)
+            k["tflops"] = round(work / per_step / 1e9, 1)
+            k["mfma_frac"] = round(work / per_step / 1e9 / PEAK_BF16_TFLOPS, 4)
         elif work:
-            k["gbs"] = round(work / avg / 1e6, 1)
-            k["hbm_frac"] = round(work / avg / 1e6 / PEAK_HBM_GBS, 4)
+            k["gbs"] = round(work / per_step / 1e6, 1)
+            k["hbm_frac"] = round(work / per_step / 1e6 / PEAK_HBM_GBS, 4)
         kernels[ph] = k
     roofline = None
     if kernels:
-        dom = max(kernels, key=lambda p: kernels[p]["avg_ms"] * kernels[p]["launches_per_step"])
+        dom = max(kernels, key=lambda p: kernels[p]["ms_per_step"])
         kind, work = kernel_work(dom, T, d, E, K, h)
-        avg = kernels[dom]["avg_ms"]
+        avg = kernels[dom]["ms_per_step"]
         if kind == "mfma":
             ach = work / avg / 1e9
             roofline = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 1),
