@@ -77,6 +77,7 @@ def run_fp4(case, K, h, beta=0.0, Y0=None, fmt=tmt_moe.WEIGHTS_MXFP4, max_tokens
     (512, 1024, 32, 4, 256),   # the c5 router with a narrow expert
     (300, 256, 8, 2, 512),     # ragged T: partial row tiles in every expert segment
     (5, 512, 4, 2, 192),       # decode-sized batch, h not a multiple of the 256-column tile
+    (100, 256, 1, 1, 128),     # one expert: no router, slot = token
 ])
 def test_mxfp4_against_oracle(orc, fmt, T, d, E, K, h):
     say(f"mxfp4 format {fmt} T={T} d={d} E={E} K={K} h={h}")
