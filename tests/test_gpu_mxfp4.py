@@ -78,6 +78,7 @@ def run_fp4(case, K, h, beta=0.0, Y0=None, fmt=tmt_moe.WEIGHTS_MXFP4, max_tokens
     (300, 256, 8, 2, 512),     # ragged T: partial row tiles in every expert segment
     (5, 512, 4, 2, 192),       # decode-sized batch, h not a multiple of the 256-column tile
     (100, 256, 1, 1, 128),     # one expert: no router, slot = token
+    (1024, 256, 8, 2, 1024),   # a longer down GEMM (16 K steps) with partial row tiles
 ])
 def test_mxfp4_against_oracle(orc, fmt, T, d, E, K, h):
     say(f"mxfp4 format {fmt} T={T} d={d} E={E} K={K} h={h}")
