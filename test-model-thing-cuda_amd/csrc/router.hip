@@ -331,6 +331,7 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     __shared__ float s_stat[4][kMaxExperts + 1];
     __shared__ float s_fl[4][kMaxExperts + 1];
     __shared__ uint32_t s_flag[4];
+    __shared__ float s_bias[kMaxExperts];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int E = p.E, d = p.d, K = p.K;
@@ -341,37 +342,7 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     // touches spread over the banks
     uint16_t* sx = sw + 32 * wpitch + wave * 2 * 32 * 128;
     if (tid < kMaxExperts) s_cnt[tid] = 0;
-    {
-        // Wr's E rows (rows E .. 31 zero: their columns are unused). Each
-        // block starts at its own offset into the rows, so that the blocks,
-        // which all read the same few KiB at kernel start, do not all ask
-        // the same L2 lines for them at once.
-        const int vpr = d / 8;  // 16-byte vectors per row
-        const int nv = E * vpr;
-        const int rot = (int)((blockIdx.x * 97u) % (unsigned)nv);
-        for (int i0 = tid; i0 < nv; i0 += 8 * 256) {
-            uint4 v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                int i = min(i0 + u * 256, nv - 1) + rot;
-                i = i >= nv ? i - nv : i;
-                v[u] = *reinterpret_cast<const uint4*>(p.Wr + (int64_t)i * 8);  // row i / vpr, vector i % vpr
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                if (i0 + u * 256 < nv) {
-                    int i = i0 + u * 256 + rot;
-                    i = i >= nv ? i - nv : i;
-                    const int n = i / vpr, c = i - n * vpr;
-                    *reinterpret_cast<uint4*>(sw + n * wpitch + 8 * c) = v[u];
-                }
-            }
-        }
-        for (int i = tid; i < (32 - E) * vpr; i += 256) {
-            const int n = E + i / vpr, c = i % vpr;
-            *reinterpret_cast<uint4*>(sw + n * wpitch + 8 * c) = make_uint4(0, 0, 0, 0);
-        }
-    }
+    if (tid < E) s_bias[tid] = p.bias != nullptr ? p.bias[tid] : 0.0f;
     const int row_begin = blockIdx.x * kMfmaRouterRows;
     const int row_end = min(p.T, row_begin + kMfmaRouterRows);
     const int rl = lane & 31, hi = lane >> 5;
@@ -394,6 +365,43 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) dma16_lds(xsrc[i] + k0, sx0 + (uint32_t)(buf * 32 * 128 * 2 + i * 1024));
     };
+    // chunks 0 and 1 go out before Wr is read, so that the two memory round
+    // trips overlap (the vector-memory counter completes in order: the wait
+    // for the Wr loads below also covers these)
+    dma_chunk(0, 0);
+    dma_chunk(1, 1);
+    {
+        // Wr's E rows (rows E .. 31 zero: their columns are unused). Each
+        // block starts at its own offset into the rows, so that the blocks,
+        // which all read the same few KiB at kernel start, do not all ask
+        // the same L2 lines for them at once.
+        const int vpr = d / 8;  // 16-byte vectors per row
+        const int nv = E * vpr;
+        const int rot = (int)((blockIdx.x * 97u) % (unsigned)nv);
+        // 16 loads per thread in flight: one round trip up to E * d = 32 * 1024
+        for (int i0 = tid; i0 < nv; i0 += 16 * 256) {
+            uint4 v[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                int i = min(i0 + u * 256, nv - 1) + rot;
+                i = i >= nv ? i - nv : i;
+                v[u] = *reinterpret_cast<const uint4*>(p.Wr + (int64_t)i * 8);  // row i / vpr, vector i % vpr
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                if (i0 + u * 256 < nv) {
+                    int i = i0 + u * 256 + rot;
+                    i = i >= nv ? i - nv : i;
+                    const int n = i / vpr, c = i - n * vpr;
+                    *reinterpret_cast<uint4*>(sw + n * wpitch + 8 * c) = v[u];
+                }
+            }
+        }
+        for (int i = tid; i < (32 - E) * vpr; i += 256) {
+            const int n = E + i / vpr, c = i % vpr;
+            *reinterpret_cast<uint4*>(sw + n * wpitch + 8 * c) = make_uint4(0, 0, 0, 0);
+        }
+    }
     f32x16 acc, aab;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = aab[r] = 0.0f;
@@ -403,9 +411,7 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     // buffer its predecessor's predecessor used, once the wave's reads of
     // that buffer are done (8 loads per chunk: waiting for all but the last
     // 8 leaves the current chunk in LDS)
-    dma_chunk(0, 0);
-    dma_chunk(1, 1);
-    __syncthreads();  // Wr staged
+    __syncthreads();  // Wr and the bias staged
     for (int c = 0; c < nch; ++c) {
         wait_vmcnt<8>();
         const uint16_t* xb_ = sx + (c & 1) * 32 * 128;
@@ -435,14 +441,13 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     for (int r = 0; r < 16; ++r) {
         const int n = expert_of(r);
         const bool ev = n < E;
-        const float bias = (p.bias != nullptr && ev) ? p.bias[n] : 0.0f;
+        // selects, not branches: an expert >= E leaves every maximum as it is
+        const float bias = (p.bias != nullptr && ev) ? s_bias[n & (kMaxExperts - 1)] : 0.0f;
         v[r] = p.bias != nullptr ? acc[r] + bias : acc[r];
-        if (ev) {
-            vmax = fmaxf(vmax, v[r]);
-            vabs = fmaxf(vabs, fabsf(v[r]));
-            amax = fmaxf(amax, aab[r]);
-            babs = fmaxf(babs, fabsf(bias));
-        }
+        vmax = fmaxf(vmax, ev ? v[r] : -INFINITY);
+        vabs = fmaxf(vabs, ev ? fabsf(v[r]) : 0.0f);
+        amax = fmaxf(amax, ev ? aab[r] : 0.0f);
+        babs = fmaxf(babs, fabsf(bias));
     }
     vmax = fmaxf(vmax, xor_lane<32>(vmax));
     vabs = fmaxf(vabs, xor_lane<32>(vabs));
@@ -457,26 +462,42 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     }
     se += xor_lane<32>(se);  // own + partner: both lanes of the row get the same bits
     const float lse = vmax + __logf(se);
+    // Top K + 1 by rounds of arg-max over (logit desc, expert asc): per lane
+    // the largest candidate (a max tree), then the lowest expert holding it
+    // (a min tree over the matching experts; -0 and +0 compare equal, as in a
+    // scan with '>' and ties to the lower index), then the partner lane's
+    // pick. Experts >= E and picked ones compete as -inf. That equals the
+    // exclusion of those experts wherever the row can be clean (every logit
+    // of a clean row is finite: an infinite one makes vabs infinite, a NaN
+    // makes se NaN, and a round always has a finite candidate); a row that
+    // is not clean takes the canonical path below whatever its picks here.
     const int rounds = min(K + 1, E);
     float topv[kMaxTopK + 1];
     int tope[kMaxTopK + 1];
-    uint32_t selm = 0u;
+    float cand[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) cand[r] = expert_of(r) < E ? v[r] : -INFINITY;
 #pragma unroll
     for (int j = 0; j <= kMaxTopK; ++j) {
         topv[j] = -INFINITY;
         tope[j] = 0;
         if (j < rounds) {
-            float bv = -INFINITY;
-            int be = 1 << 20;
+            float tv[8];
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int n = expert_of(r);
-                const bool in = n < E && !((selm >> r) & 1u);
-                if (in && (v[r] > bv || (v[r] == bv && n < be))) {
-                    bv = v[r];
-                    be = n;
-                }
-            }
+            for (int q = 0; q < 8; ++q) tv[q] = fmaxf(cand[2 * q], cand[2 * q + 1]);
+#pragma unroll
+            for (int w = 4; w >= 1; w >>= 1)
+#pragma unroll
+                for (int q = 0; q < w; ++q) tv[q] = fmaxf(tv[2 * q], tv[2 * q + 1]);
+            float bv = tv[0];
+            int tn[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) tn[r] = cand[r] == bv ? expert_of(r) : (1 << 20);
+#pragma unroll
+            for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+                for (int q = 0; q < w; ++q) tn[q] = min(tn[q], tn[q + w]);
+            int be = tn[0];
             const float ov = xor_lane<32>(bv);
             const int oe = xor_lane<32>(be);
             if (ov > bv || (ov == bv && oe < be)) {
@@ -487,7 +508,7 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
             tope[j] = be;
 #pragma unroll
             for (int r = 0; r < 16; ++r)
-                if (expert_of(r) == be) selm |= 1u << r;
+                if (expert_of(r) == be) cand[r] = -INFINITY;
         }
     }
     const float u = 5.9604644775390625e-08f;  // 2^-24
@@ -549,17 +570,36 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     }
     const uint64_t fm = __ballot(rvalid && flag && hi == 0);
     if (lane == 0) s_flag[wave] = (uint32_t)fm;
-    // per-wave statistics over the wave's rows, in a fixed order
+    // per-wave statistics over the wave's rows, in a fixed order: the xor
+    // butterfly (16 .. 1) over the 32 lanes of each half for every register,
+    // as a reduce-scatter (each addition pairs the same partial trees as the
+    // full butterfly, so the bits are the same): at offset OFF the lane keeps
+    // the half of its entries selected by its lane bit OFF; after offset 2
+    // lane rl holds register 8 b4 + 4 b3 + 2 b2 + b1 (b_i: bit i of rl), and
+    // offset 1 is a plain butterfly step
+    {
+        auto level = [&](auto off_c, int n) {
+            constexpr int OFF = decltype(off_c)::value;
+            const bool upper = (lane & OFF) != 0;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        float t = psum[r];
-        t += xor_lane<16>(t);
-        t += xor_lane<8>(t);
-        t += xor_lane<4>(t);
-        t += xor_lane<2>(t);
+            for (int t = 0; t < 8; ++t) {
+                if (t < n) {
+                    const float lo = psum[t], hi_ = psum[t + n];
+                    const float send = upper ? lo : hi_;
+                    const float keep = upper ? hi_ : lo;
+                    psum[t] = keep + xor_lane<OFF>(send);
+                }
+            }
+        };
+        level(std::integral_constant<int, 16>{}, 8);
+        level(std::integral_constant<int, 8>{}, 4);
+        level(std::integral_constant<int, 4>{}, 2);
+        level(std::integral_constant<int, 2>{}, 1);
+        float t = psum[0];
         t += xor_lane<1>(t);
+        const int r = ((rl >> 4) & 1) * 8 + ((rl >> 3) & 1) * 4 + ((rl >> 2) & 1) * 2 + ((rl >> 1) & 1);
         const int n = expert_of(r);
-        if (rl == 0 && n < E) s_stat[wave][n] = t;
+        if ((rl & 1) == 0 && n < E) s_stat[wave][n] = t;
     }
     lsum += xor_lane<16>(lsum);
     lsum += xor_lane<8>(lsum);
@@ -569,75 +609,120 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     if (lane == 0) s_stat[wave][kMaxExperts] = lsum;
     __syncthreads();
 
-    // ---- flagged rows in the canonical order: the block's i-th flagged row
-    // (ascending) goes to wave i % 4 -------------------------------------
-    float fps = 0.0f, fls = 0.0f;  // lane e: expert e's probability sum; lane 0: lse^2 sum
-    int fi = 0;
-    for (int w = 0; w < 4; ++w) {
-        uint32_t m = s_flag[w];
-        while (m != 0u) {
-            const int bit = __builtin_ctz(m);
-            m &= m - 1u;
-            if ((fi++ & 3) != wave) continue;
-            const int frow = row_begin + w * 32 + bit;
-            // lane partials over the lane's elements c * 512 + 8 lane + t,
-            // fmaf in ascending k, then the full xor butterfly
-            float pa[EP];
+    // ---- flagged rows in the canonical order ---------------------------------
+    // Logits first: for every flagged row (ascending), wave w computes
+    // experts w, w + 4, ... as canonical lane partials over the elements
+    // c * 512 + 8 lane + t (fmaf in ascending k) and the full xor butterfly,
+    // which adds the same partial trees as router_kernel's reduce-scatter;
+    // rows go in batches of 4 with all their X loads in flight together. The
+    // logits go to LDS (the X ring, free once every wave has passed the
+    // barrier above), then softmax / top-k take R = 64 / EP rows per wave
+    // pass, lane l holding row l / EP, expert l % EP.
+    constexpr int R = 64 / EP;
+    constexpr int NCHM = 3;  // 512-element chunks per row: d <= 1536 (router_mfma_fits)
+    const uint32_t f0 = s_flag[0], f1 = s_flag[1], f2 = s_flag[2], f3 = s_flag[3];
+    const int c0 = __builtin_popcount(f0), c1 = c0 + __builtin_popcount(f1);
+    const int c2 = c1 + __builtin_popcount(f2), nflag = c2 + __builtin_popcount(f3);
+    float fps = 0.0f, fls = 0.0f;  // per lane: its (row slot, expert)'s sums, folded below
+    if (nflag > 0) {
+        float* s_logit = reinterpret_cast<float*>(sw + 32 * wpitch);  // [nflag][E]
+        int* s_frow = reinterpret_cast<int*>(s_logit + kMfmaRouterRows * 32);  // [nflag]
+        // the lane's two block-row slots, lane and 64 + lane: flagged, and rank
+        // among the block's flagged rows
+        const int sh = lane & 31;
+        const uint32_t mlo = lane < 32 ? f0 : f1, mhi = lane < 32 ? f2 : f3;
+        const uint32_t below = (1u << sh) - 1u;
+        const bool flo = (mlo >> sh) & 1u, fhi = (mhi >> sh) & 1u;
+        const int rlo = (lane < 32 ? 0 : c0) + __builtin_popcount(mlo & below);
+        const int rhi = (lane < 32 ? c1 : c2) + __builtin_popcount(mhi & below);
+        auto nth_flagged = [&](int i) -> int {  // block-row slot of flagged row i < nflag
+            const uint64_t bl = __ballot(flo && rlo == i);
+            if (bl != 0) return __builtin_ctzll(bl);
+            return 64 + __builtin_ctzll(__ballot(fhi && rhi == i));
+        };
+        const int nch = (d + 511) / 512;
+        for (int i0 = 0; i0 < nflag; i0 += 4) {
+            int frow[4];
 #pragma unroll
-            for (int e = 0; e < EP; ++e) pa[e] = 0.0f;
-            for (int c0 = 0; c0 < d; c0 += 512) {
-                const int k = c0 + 8 * lane;
-                if (k < d) {
-                    float xf[8];
-                    unpack8(*reinterpret_cast<const uint4*>(p.X + (int64_t)frow * d + k), xf);
+            for (int r = 0; r < 4; ++r) frow[r] = i0 + r < nflag ? row_begin + nth_flagged(i0 + r) : -1;
+            if (wave == 0 && lane < 4 && i0 + lane < nflag) {
+                int fr = frow[0];
 #pragma unroll
-                    for (int e = 0; e < EP; ++e) {
-                        if (e < E) {
-                            float wf[8];
-                            unpack8(*reinterpret_cast<const uint4*>(sw + e * wpitch + k), wf);
-                            float a = pa[e];
+                for (int r = 1; r < 4; ++r)
+                    if (lane == r) fr = frow[r];
+                s_frow[i0 + lane] = fr;
+            }
+            uint4 xv[4][NCHM];
 #pragma unroll
-                            for (int t = 0; t < 8; ++t) a = __builtin_fmaf(xf[t], wf[t], a);
-                            pa[e] = a;
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int c = 0; c < NCHM; ++c) {
+                    const int k = c * 512 + 8 * lane;
+                    const bool ok = frow[r] >= 0 && c < nch && k < d;  // clamped: no load under a branch
+                    xv[r][c] = *reinterpret_cast<const uint4*>(p.X + (int64_t)(ok ? frow[r] : row_begin) * d +
+                                                               (ok ? k : 0));
+                }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                if (frow[r] < 0) break;
+                float xf[NCHM][8];
+#pragma unroll
+                for (int c = 0; c < NCHM; ++c) unpack8(xv[r][c], xf[c]);
+#pragma unroll
+                for (int u = 0; u < EP / 4; ++u) {
+                    const int e = wave + 4 * u;
+                    if (e < E) {
+                        float t = 0.0f;
+#pragma unroll
+                        for (int c = 0; c < NCHM; ++c) {
+                            if (c < nch) {
+                                const int k = c * 512 + 8 * lane;
+                                const bool ok = k < d;  // a lane past d keeps its partial
+                                float wf[8];
+                                unpack8(*reinterpret_cast<const uint4*>(sw + e * wpitch + (ok ? k : 0)), wf);
+                                float a = t;
+#pragma unroll
+                                for (int q = 0; q < 8; ++q) a = __builtin_fmaf(xf[c][q], wf[q], a);
+                                t = ok ? a : t;
+                            }
                         }
+                        t = wave_sum(t);
+                        if (lane == 0) s_logit[(i0 + r) * E + e] = p.bias != nullptr ? t + s_bias[e] : t;
                     }
                 }
             }
-            float logit = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EP; ++e) {
-                if (e < E) {
-                    float t = pa[e];
-                    t += xor_lane<32>(t);
-                    t += xor_lane<16>(t);
-                    t += xor_lane<8>(t);
-                    t += xor_lane<4>(t);
-                    t += xor_lane<2>(t);
-                    t += xor_lane<1>(t);
-                    if (lane % EP == e) logit = p.bias != nullptr ? t + p.bias[e] : t;
-                }
-            }
-            const int e_mine = lane % EP;
-            const bool e_valid = lane < EP && e_mine < E;
+        }
+        __syncthreads();
+        const int e_mine = lane % EP, r_mine = lane / EP;
+        const bool e_valid = e_mine < E;
+        for (int g0 = wave * R; g0 < nflag; g0 += 4 * R) {
+            const int i = g0 + r_mine;
+            const bool rv = i < nflag;
+            const float logit = rv && e_valid ? s_logit[i * E + e_mine] : 0.0f;
             const RowPick pk = softmax_topk<EP>(logit, e_valid, e_mine, K);
-            if (lane < EP) {
+            if (rv) {
+                const int frw = s_frow[i];
                 if (e_valid) {
-                    p.logits[(int64_t)frow * E + e_mine] = logit;
-                    p.probs[(int64_t)frow * E + e_mine] = pk.prob;
+                    p.logits[(int64_t)frw * E + e_mine] = logit;
+                    p.probs[(int64_t)frw * E + e_mine] = pk.prob;
                     fps += pk.prob;
                     if (pk.sel) atomicAdd(&s_cnt[e_mine], 1);
                 }
                 if (e_mine < K) {
-                    p.idx[(int64_t)frow * K + e_mine] = pk.idx;
-                    p.gate[(int64_t)frow * K + e_mine] = pk.gate;
+                    p.idx[(int64_t)frw * K + e_mine] = pk.idx;
+                    p.gate[(int64_t)frw * K + e_mine] = pk.gate;
                 }
                 if (e_mine == 0) {
-                    p.lse[frow] = pk.lse;
+                    p.lse[frw] = pk.lse;
                     fls += pk.lse * pk.lse;
                 }
             }
         }
     }
+    // fold the row slots: lane e < EP holds expert e's sum, lane 0 the lse^2 sum
+    if constexpr (EP <= 32) { fps += xor_lane<32>(fps); fls += xor_lane<32>(fls); }
+    if constexpr (EP <= 16) { fps += xor_lane<16>(fps); fls += xor_lane<16>(fls); }
+    if constexpr (EP <= 8) { fps += xor_lane<8>(fps); fls += xor_lane<8>(fls); }
     if (lane < E) s_fl[wave][lane] = fps;
     if (lane == 0) s_fl[wave][kMaxExperts] = fls;
     __syncthreads();
@@ -660,7 +745,7 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
 static size_t router_mfma_lds(int d) { return ((size_t)32 * (d + 8) + (size_t)4 * 2 * 32 * 128) * 2; }
 
 bool router_mfma_fits(int T, int E, int K, int d) {
-    return E >= 2 && E <= 32 && K <= E && K <= kMaxTopK && d % 128 == 0 && d >= 128 &&
+    return E >= 2 && E <= 32 && K <= E && K <= kMaxTopK && d % 128 == 0 && d >= 128 && d <= 3 * 512 &&
            router_mfma_lds(d) <= 140 * 1024 && (T + kMfmaRouterRows - 1) / kMfmaRouterRows >= cu_count();
 }
 
