@@ -318,14 +318,58 @@ __device__ __forceinline__ void dma16_lds(const void* g, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "m0", "memory");
 }
 #pragma clang diagnostic pop
+// Sums of N entries per lane over the wave's 64 lanes (xor butterfly,
+// offsets 32 .. 1) as a reduce-scatter: at offset OFF while n > 1 entries are
+// left, the lanes with bit OFF set keep the upper half of their entries,
+// adding their partner's copy, so lane l ends with entry
+// sum_j bit(5 - j, l) * N / 2^(j+1) (j < log2 N); then plain butterfly steps.
+// Every addition is own + partner of the same partial trees as the full
+// butterfly, so each sum has that butterfly's bits.
+template <int OFF, int N>
+__device__ __forceinline__ void rs_sum_level(float* a, int lane) {
+    if constexpr (N > 1) {
+        const bool upper = (lane & OFF) != 0;
+#pragma unroll
+        for (int t = 0; t < N / 2; ++t) {
+            const float lo = a[t], hi = a[t + N / 2];
+            const float send = upper ? lo : hi;
+            const float keep = upper ? hi : lo;
+            a[t] = keep + xor_lane<OFF>(send);
+        }
+        rs_sum_level<OFF / 2, N / 2>(a, lane);
+    } else if constexpr (OFF >= 1) {
+        a[0] = a[0] + xor_lane<OFF>(a[0]);
+        rs_sum_level<OFF / 2, 1>(a, lane);
+    }
+}
+template <int N>
+__device__ __forceinline__ int rs_sum_entry(int lane) {
+    int idx = 0;
+#pragma unroll
+    for (int off = 32, n = N; n > 1; off >>= 1, n >>= 1)
+        if (lane & off) idx += n / 2;
+    return idx;
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 __device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Persistent over 128-row groups: block b routes groups b, b + gridDim.x, ...
+// (one block per CU). Wr and the bias are staged once per block, and the X
+// stream runs on across groups: the loads that would refill the ring after a
+// group's last chunks fetch the next group's first chunks instead, so they
+// are in flight during the group's epilogue.
 template <int EP>
 __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
+    // Staged Wr rows (the MFMA's 32 output columns: rows at or past WROWS
+    // enter as zeros) and X buffers per wave. A third buffer (room for it
+    // with 16 Wr rows) measured slower at c3: the stream is bandwidth-bound
+    // with two 8 KiB chunks in flight per wave.
+    constexpr int WROWS = EP <= 16 ? 16 : 32;
+    constexpr int NBUF = 2;
     extern __shared__ uint4 smem_rm[];
     __shared__ int s_cnt[kMaxExperts];
     __shared__ float s_stat[4][kMaxExperts + 1];
@@ -336,45 +380,52 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int E = p.E, d = p.d, K = p.K;
     const int wpitch = d + 8;  // bf16 elements per staged Wr row
-    uint16_t* sw = reinterpret_cast<uint16_t*>(smem_rm);  // [32][wpitch]
-    // this wave's two X buffers, [32 rows][128] bf16 each: 16-byte chunk q of
-    // row r sits at chunk q ^ (r & 15), so the 32 rows that one fragment read
-    // touches spread over the banks
-    uint16_t* sx = sw + 32 * wpitch + wave * 2 * 32 * 128;
+    uint16_t* sw = reinterpret_cast<uint16_t*>(smem_rm);  // [WROWS][wpitch]
+    // this wave's NBUF X buffers, [32 rows][128] bf16 each: 16-byte chunk q
+    // of row r sits at chunk q ^ (r & 15), so the 32 rows that one fragment
+    // read touches spread over the banks
+    uint16_t* sx_all = sw + WROWS * wpitch;
+    uint16_t* sx = sx_all + wave * NBUF * 32 * 128;
+    // flagged rows' logits [kMfmaRouterRows][32] and block-row slots
+    float* s_logit = reinterpret_cast<float*>(sx_all + 4 * NBUF * 32 * 128);
+    int* s_frow = reinterpret_cast<int*>(s_logit + kMfmaRouterRows * 32);
     if (tid < kMaxExperts) s_cnt[tid] = 0;
     if (tid < E) s_bias[tid] = p.bias != nullptr ? p.bias[tid] : 0.0f;
-    const int row_begin = blockIdx.x * kMfmaRouterRows;
-    const int row_end = min(p.T, row_begin + kMfmaRouterRows);
+    const int nblk = (p.T + kMfmaRouterRows - 1) / kMfmaRouterRows;
     const int rl = lane & 31, hi = lane >> 5;
-    const int row = row_begin + wave * 32 + rl;
-    const bool rvalid = row < row_end;
+    const int nch = d / 128;  // d % 128 == 0 (launch check)
     // X loads: load i of a chunk fills rows 4i .. 4i + 3 of the wave's 32
     // (lane -> row 4i + lane / 16, physical chunk lane % 16, which holds the
     // row's logical chunk (lane % 16) ^ (row & 15)): 4 rows x 256 bytes per
-    // load instead of the MFMA layout's 32 rows x 32 bytes
-    const uint16_t* xsrc[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int r = 4 * i + (lane >> 4);
-        const int rr = row_begin + wave * 32 + r < row_end ? row_begin + wave * 32 + r : row_begin;  // clamped
-        xsrc[i] = p.X + (int64_t)rr * d + 8 * ((lane & 15) ^ (r & 15));
-    }
+    // load instead of the MFMA layout's 32 rows x 32 bytes. Rows past T
+    // reload the group's first row; a chunk past the end reloads the last.
     const uint32_t sx0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)sx;
-    auto dma_chunk = [&](int c, int buf) {
-        const int k0 = min(c, d / 128 - 1) * 128;  // clamped: a chunk past the end reloads the last
+    auto dma_chunk = [&](int g, int c, int buf) {
+        const int rb = g * kMfmaRouterRows + wave * 32;
+        const int k0 = min(c, nch - 1) * 128;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) dma16_lds(xsrc[i] + k0, sx0 + (uint32_t)(buf * 32 * 128 * 2 + i * 1024));
+        for (int i = 0; i < 8; ++i) {
+            const int r = 4 * i + (lane >> 4);
+            const int rr = rb + r < p.T ? rb + r : g * kMfmaRouterRows;
+            dma16_lds(p.X + (int64_t)rr * d + k0 + 8 * ((lane & 15) ^ (r & 15)),
+                      sx0 + (uint32_t)(buf * 32 * 128 * 2 + i * 1024));
+        }
     };
-    // chunks 0 and 1 go out before Wr is read, so that the two memory round
-    // trips overlap (the vector-memory counter completes in order: the wait
-    // for the Wr loads below also covers these)
-    dma_chunk(0, 0);
-    dma_chunk(1, 1);
+    // The stream carries across groups only when a group has at least NBUF
+    // chunks (its tail loads are then the next group's chunks 0 .. NBUF-1).
+    const bool chain = nch >= NBUF;
+    int grp = blockIdx.x;
+    int qb = 0;  // ring buffer of the group's chunk 0
+    // the first group's leading chunks go out before Wr is read, so that the
+    // two memory round trips overlap (the vector-memory counter completes in
+    // order: the wait for the Wr loads below also covers these)
+#pragma unroll
+    for (int j = 0; j < NBUF; ++j) dma_chunk(grp, j, j);
     {
-        // Wr's E rows (rows E .. 31 zero: their columns are unused). Each
-        // block starts at its own offset into the rows, so that the blocks,
-        // which all read the same few KiB at kernel start, do not all ask
-        // the same L2 lines for them at once.
+        // Wr's E rows (rows E .. WROWS-1 zero: their columns are unused).
+        // Each block starts at its own offset into the rows, so that the
+        // blocks, which all read the same few KiB at kernel start, do not
+        // all ask the same L2 lines for them at once.
         const int vpr = d / 8;  // 16-byte vectors per row
         const int nv = E * vpr;
         const int rot = (int)((blockIdx.x * 97u) % (unsigned)nv);
@@ -397,29 +448,42 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
                 }
             }
         }
-        for (int i = tid; i < (32 - E) * vpr; i += 256) {
+        for (int i = tid; i < (WROWS - E) * vpr; i += 256) {
             const int n = E + i / vpr, c = i % vpr;
             *reinterpret_cast<uint4*>(sw + n * wpitch + 8 * c) = make_uint4(0, 0, 0, 0);
         }
     }
+    __syncthreads();  // Wr and the bias staged
+    const uint4 absm = make_uint4(0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu);
+    bool leading = true;  // the group's chunks 0 .. NBUF-1 are in flight
+    for (; grp < nblk; grp += gridDim.x) {
+    const int nxt = grp + (int)gridDim.x;
+    if (!leading) {
+#pragma unroll
+        for (int j = 0; j < NBUF; ++j) dma_chunk(grp, j, j);
+        qb = 0;
+    }
+    const int row_begin = grp * kMfmaRouterRows;
+    const int row_end = min(p.T, row_begin + kMfmaRouterRows);
+    const int row = row_begin + wave * 32 + rl;
+    const bool rvalid = row < row_end;
     f32x16 acc, aab;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = aab[r] = 0.0f;
-    const uint4 absm = make_uint4(0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu);
-    const int nch = d / 128;  // d % 128 == 0 (launch check)
-    // chunks 0 and 1 in flight; every later chunk is requested into the
-    // buffer its predecessor's predecessor used, once the wave's reads of
-    // that buffer are done (8 loads per chunk: waiting for all but the last
-    // 8 leaves the current chunk in LDS)
-    __syncthreads();  // Wr and the bias staged
+    // NBUF chunks in flight; every later chunk is requested into the buffer
+    // the chunk NBUF before it used, once the wave's reads of that buffer are
+    // done (8 loads per chunk: waiting for all but the last (NBUF - 1) * 8
+    // leaves the current chunk in LDS)
     for (int c = 0; c < nch; ++c) {
-        wait_vmcnt<8>();
-        const uint16_t* xb_ = sx + (c & 1) * 32 * 128;
+        wait_vmcnt<(NBUF - 1) * 8>();
+        const int buf = (qb + c) % NBUF;
+        const uint16_t* xb_ = sx + buf * 32 * 128;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
             const int q = (2 * s + hi) ^ (rl & 15);
             const uint4 xa = *reinterpret_cast<const uint4*>(xb_ + rl * 128 + 8 * q);
-            const uint4 wa = *reinterpret_cast<const uint4*>(sw + rl * wpitch + c * 128 + 16 * s + 8 * hi);
+            uint4 wa = *reinterpret_cast<const uint4*>(sw + (rl & (WROWS - 1)) * wpitch + c * 128 + 16 * s + 8 * hi);
+            if (WROWS < 32 && rl >= WROWS) wa = make_uint4(0, 0, 0, 0);
             const uint4 xb = make_uint4(xa.x & absm.x, xa.y & absm.y, xa.z & absm.z, xa.w & absm.w);
             const uint4 wb = make_uint4(wa.x & absm.x, wa.y & absm.y, wa.z & absm.z, wa.w & absm.w);
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wa),
@@ -428,9 +492,14 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
                                                            __builtin_bit_cast(bf16x8, xb), aab, 0, 0, 0);
         }
         wait_lgkm0();  // this buffer's reads are done before the next load overwrites it
-        dma_chunk(c + 2, c & 1);
+        const int cn = c + NBUF;
+        if (cn < nch) dma_chunk(grp, cn, buf);
+        else if (chain && nxt < nblk) dma_chunk(nxt, cn - nch, buf);
+        else dma_chunk(grp, nch - 1, buf);  // clamped: keeps the per-chunk load count
     }
-    wait_vmcnt<0>();  // the clamped extra loads, before the buffers go away
+    leading = chain && nxt < nblk;
+    if (leading) qb = (qb + nch) % NBUF;
+    else wait_vmcnt<0>();  // the clamped extra loads, before the buffers are refilled
 
     // ---- softmax, top K + 1, the separation test (lanes l and l ^ 32 share a
     // row; register r holds expert 8 (r / 4) + 4 (l / 32) + r % 4) ---------
@@ -612,21 +681,20 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     // ---- flagged rows in the canonical order ---------------------------------
     // Logits first: for every flagged row (ascending), wave w computes
     // experts w, w + 4, ... as canonical lane partials over the elements
-    // c * 512 + 8 lane + t (fmaf in ascending k) and the full xor butterfly,
-    // which adds the same partial trees as router_kernel's reduce-scatter;
-    // rows go in batches of 4 with all their X loads in flight together. The
-    // logits go to LDS (the X ring, free once every wave has passed the
-    // barrier above), then softmax / top-k take R = 64 / EP rows per wave
-    // pass, lane l holding row l / EP, expert l % EP.
+    // c * 512 + 8 lane + t (fmaf in ascending k) summed by the full xor
+    // butterfly (here as one reduce-scatter over the wave's 4 rows x E/4
+    // experts), which adds the same partial trees as router_kernel's
+    // reduce-scatter. Rows go in batches of 4 with all their X loads in
+    // flight together. The logits go to LDS, then softmax / top-k take
+    // R = 64 / EP rows per wave pass, lane l holding row l / EP, expert l % EP.
     constexpr int R = 64 / EP;
     constexpr int NCHM = 3;  // 512-element chunks per row: d <= 1536 (router_mfma_fits)
+    constexpr int U = EP / 4, V = 4 * U;  // experts per wave, (row, expert) sums per batch
     const uint32_t f0 = s_flag[0], f1 = s_flag[1], f2 = s_flag[2], f3 = s_flag[3];
     const int c0 = __builtin_popcount(f0), c1 = c0 + __builtin_popcount(f1);
     const int c2 = c1 + __builtin_popcount(f2), nflag = c2 + __builtin_popcount(f3);
     float fps = 0.0f, fls = 0.0f;  // per lane: its (row slot, expert)'s sums, folded below
     if (nflag > 0) {
-        float* s_logit = reinterpret_cast<float*>(sw + 32 * wpitch);  // [nflag][E]
-        int* s_frow = reinterpret_cast<int*>(s_logit + kMfmaRouterRows * 32);  // [nflag]
         // the lane's two block-row slots, lane and 64 + lane: flagged, and rank
         // among the block's flagged rows
         const int sh = lane & 31;
@@ -641,6 +709,9 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
             return 64 + __builtin_ctzll(__ballot(fhi && rhi == i));
         };
         const int nch = (d + 511) / 512;
+        // the entry this lane's sum ends on, and whether it writes it
+        const int ent = rs_sum_entry<V>(lane);
+        const bool writer = (lane & (64 / V - 1)) == 0;
         for (int i0 = 0; i0 < nflag; i0 += 4) {
             int frow[4];
 #pragma unroll
@@ -662,35 +733,38 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
                     xv[r][c] = *reinterpret_cast<const uint4*>(p.X + (int64_t)(ok ? frow[r] : row_begin) * d +
                                                                (ok ? k : 0));
                 }
+            float a[V];  // entry r * U + u: row i0 + r, expert wave + 4u
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                if (frow[r] < 0) break;
-                float xf[NCHM][8];
+            for (int i = 0; i < V; ++i) a[i] = 0.0f;
 #pragma unroll
-                for (int c = 0; c < NCHM; ++c) unpack8(xv[r][c], xf[c]);
+            for (int c = 0; c < NCHM; ++c) {
+                if (c < nch) {
+                    const int k = c * 512 + 8 * lane;
+                    const bool ok = k < d;  // a lane past d keeps its partials
+                    float xf[4][8];
 #pragma unroll
-                for (int u = 0; u < EP / 4; ++u) {
-                    const int e = wave + 4 * u;
-                    if (e < E) {
-                        float t = 0.0f;
+                    for (int r = 0; r < 4; ++r) unpack8(xv[r][c], xf[r]);
 #pragma unroll
-                        for (int c = 0; c < NCHM; ++c) {
-                            if (c < nch) {
-                                const int k = c * 512 + 8 * lane;
-                                const bool ok = k < d;  // a lane past d keeps its partial
-                                float wf[8];
-                                unpack8(*reinterpret_cast<const uint4*>(sw + e * wpitch + (ok ? k : 0)), wf);
-                                float a = t;
+                    for (int u = 0; u < U; ++u) {
+                        const int e = wave + 4 * u;
+                        if (e < E) {
+                            float wf[8];
+                            unpack8(*reinterpret_cast<const uint4*>(sw + e * wpitch + (ok ? k : 0)), wf);
 #pragma unroll
-                                for (int q = 0; q < 8; ++q) a = __builtin_fmaf(xf[c][q], wf[q], a);
-                                t = ok ? a : t;
+                            for (int r = 0; r < 4; ++r) {
+                                float t = a[r * U + u];
+#pragma unroll
+                                for (int q = 0; q < 8; ++q) t = __builtin_fmaf(xf[r][q], wf[q], t);
+                                a[r * U + u] = ok ? t : a[r * U + u];
                             }
                         }
-                        t = wave_sum(t);
-                        if (lane == 0) s_logit[(i0 + r) * E + e] = p.bias != nullptr ? t + s_bias[e] : t;
                     }
                 }
             }
+            rs_sum_level<32, V>(a, lane);
+            const int rr = ent / U, e = wave + 4 * (ent % U);
+            if (writer && i0 + rr < nflag && e < E)
+                s_logit[(i0 + rr) * E + e] = p.bias != nullptr ? a[0] + s_bias[e] : a[0];
         }
         __syncthreads();
         const int e_mine = lane % EP, r_mine = lane / EP;
@@ -726,7 +800,7 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     if (lane < E) s_fl[wave][lane] = fps;
     if (lane == 0) s_fl[wave][kMaxExperts] = fls;
     __syncthreads();
-    const int blk = blockIdx.x;
+    const int blk = grp;
     if (tid <= E) {
         const int col = tid < E ? tid : kMaxExperts;
         float t = s_stat[0][col];
@@ -738,25 +812,40 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
         t += s_fl[2][col];
         t += s_fl[3][col];
         p.blkstat[(int64_t)blk * (E + 1) + tid] = t;
-        if (tid < E) p.blkcnt[(int64_t)blk * E + tid] = s_cnt[tid];
+        if (tid < E) {
+            p.blkcnt[(int64_t)blk * E + tid] = s_cnt[tid];
+            s_cnt[tid] = 0;  // for the next group (after the barrier below)
+        }
+    }
+    // the next group rewrites the statistics, flags and counts read above
+    __syncthreads();
     }
 }
 
-static size_t router_mfma_lds(int d) { return ((size_t)32 * (d + 8) + (size_t)4 * 2 * 32 * 128) * 2; }
+// Dynamic LDS of router_mfma_kernel: staged Wr rows, the X buffers, the
+// flagged rows' logits and slots.
+static size_t router_mfma_lds(int d, int E) {
+    const int ep = router_ep(E);
+    const size_t wrows = ep <= 16 ? 16 : 32, nbuf = 2;
+    return wrows * (d + 8) * 2 + 4 * nbuf * 32 * 128 * 2 + (size_t)kMfmaRouterRows * 32 * 4 + kMfmaRouterRows * 4;
+}
 
 bool router_mfma_fits(int T, int E, int K, int d) {
     return E >= 2 && E <= 32 && K <= E && K <= kMaxTopK && d % 128 == 0 && d >= 128 && d <= 3 * 512 &&
-           router_mfma_lds(d) <= 140 * 1024 && (T + kMfmaRouterRows - 1) / kMfmaRouterRows >= cu_count();
+           router_mfma_lds(d, E) + 4096 <= 160 * 1024 && (T + kMfmaRouterRows - 1) / kMfmaRouterRows >= cu_count();
 }
 
 hipError_t launch_router_mfma(const RouterParams& p, int nblk, hipStream_t s) {
-    if (p.rows_per_block != kMfmaRouterRows || p.ln_H != nullptr || !router_mfma_fits(nblk * kMfmaRouterRows, p.E, p.K, p.d))
+    if (p.rows_per_block != kMfmaRouterRows || p.ln_H != nullptr || !router_mfma_fits(nblk * kMfmaRouterRows, p.E, p.K, p.d) ||
+        nblk != (p.T + kMfmaRouterRows - 1) / kMfmaRouterRows)
         return hipErrorInvalidValue;
-    const size_t lds = router_mfma_lds(p.d);
+    const size_t lds = router_mfma_lds(p.d, p.E);
+    // one block per CU (its LDS), each walking the 128-row groups b, b + grid, ...
+    const int grid = min(nblk, cu_count());
     switch (router_ep(p.E)) {
-        case 8: router_mfma_kernel<8><<<nblk, 256, lds, s>>>(p); break;
-        case 16: router_mfma_kernel<16><<<nblk, 256, lds, s>>>(p); break;
-        case 32: router_mfma_kernel<32><<<nblk, 256, lds, s>>>(p); break;
+        case 8: router_mfma_kernel<8><<<grid, 256, lds, s>>>(p); break;
+        case 16: router_mfma_kernel<16><<<grid, 256, lds, s>>>(p); break;
+        case 32: router_mfma_kernel<32><<<grid, 256, lds, s>>>(p); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
