@@ -293,6 +293,29 @@ def test_router_near_ties_follow_canonical_order(orc, E, K):
     assert np.array_equal(g["logits"][certain].view(np.uint32), r["logits"][certain].view(np.uint32))
 
 
+@pytest.mark.parametrize("T,d,E,K", [
+    (40000, 1024, 16, 4),  # blocks walk two 128-row groups; the next group's chunks load during the epilogue
+    (36000, 384, 8, 2),    # an odd number of 128-column chunks per row: the ring position flips between groups
+    (33000, 1152, 32, 8),  # the widest rows whose Wr staging (32 rows) fits in LDS, 9 chunks per row
+])
+def test_matrix_core_router_group_walk(orc, T, d, E, K):
+    """Batches with more 128-row groups than CUs: each block of the
+    matrix-core router walks several groups, with Wr staged once and the
+    X stream running on from one group into the next. Routing, offsets and
+    the permutation bit-exact against the oracle router and dispatch at the
+    full size; aux and z from the block statistics within float tolerance."""
+    say(f"matrix-core router group walk T={T} d={d} E={E} K={K}")
+    case = make_case(T, d, E, K, 0, seed=70 + E, with_dy=False)
+    g = run_gpu(case, K, 0)
+    rr = orc.router(case["X"], case["Wr"], K, bias=case.get("bias"))
+    rd = orc.dispatch(rr["idx"], E)
+    rr.update(rd)
+    check_routing(g, rr, E)
+    aux, z = orc.aux_z(rr["probs"], rd["counts"], rr["lse"], K)
+    near(g["aux"], aux, 1e-6, 1e-4, "aux")
+    near(g["z"], z, 1e-6, 1e-4, "z")
+
+
 def test_runs_are_bitwise_deterministic():
     say("determinism: two identical fwd+bwd runs")
     T, d, E, K, h = 2000, 512, 8, 2, 512
