@@ -282,16 +282,16 @@ __global__ __launch_bounds__(64 * NW) void router_kernel(RouterParams p) {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // ---- router logits on the matrix cores -----------------------------------
-// Large routed batches without the LayerNorm (E <= 32): wave w of a 4-wave
-// block takes rows 32w .. 32w + 31 of the block's kMfmaRouterRows and
+// Large routed batches without the LayerNorm (E <= 32): one 4-wave block per
+// CU walks 128-row groups; wave w takes rows 32w .. 32w + 31 of a group and
 // computes their logits with v_mfma_f32_32x32x16_bf16 (X rows as the A
 // operand, Wr rows as B, fp32 accumulation), together with
 // A = sum_k |x_k w_k| from a second MFMA over the operands with their sign
 // bits cleared. Wr sits in LDS for the block (rows padded by 16 bytes); X
-// streams through a per-wave LDS buffer in 128-element chunks, loaded as
-// 4 rows x 256 bytes per instruction (the MFMA's own layout, 32 rows x 32
-// bytes per instruction, kept the CU's load path busy for 37 us per block
-// at c3) and one chunk ahead in registers.
+// streams through a per-wave double buffer in LDS in 128-element chunks,
+// loaded as 4 rows x 256 bytes per instruction (the MFMA's own layout, 32
+// rows x 32 bytes per instruction, kept the CU's load path busy for 37 us
+// per block at c3), and on from one group into the next.
 // The MFMA sums the same exact bf16 products as the canonical order does,
 // only in another order, so a logit differs from the canonical one by at
 // most
@@ -308,7 +308,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // pair, or with a non-finite value, is flagged and recomputed in the
 // canonical order (the lane partials and full butterfly of token_logits,
 // then softmax_topk): bit for bit what router_kernel writes. Flagged rows
-// go to the waves in ascending row order, so the block statistics are
+// are taken in ascending row order, so the block statistics are
 // deterministic.
 // One wave-wide 16-byte-per-lane load from global memory into LDS at
 // lds_base + 16 * lane (lds_base wave-uniform); M0 is declared clobbered.
