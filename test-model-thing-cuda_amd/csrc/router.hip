@@ -317,6 +317,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ void dma16_lds(const void* g, uint32_t lds_base) {
     asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "m0", "memory");
 }
+// The same with 4 bytes per lane (to lds_base + 4 * lane).
+__device__ __forceinline__ void dma4_lds(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base) : "m0", "memory");
+}
 #pragma clang diagnostic pop
 // Sums of N entries per lane over the wave's 64 lanes (xor butterfly,
 // offsets 32 .. 1) as a reduce-scatter: at offset OFF while n > 1 entries are
@@ -366,7 +370,7 @@ template <int EP>
 __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     // Staged Wr rows (the MFMA's 32 output columns: rows at or past WROWS
     // enter as zeros) and X buffers per wave. A third buffer (room for it
-    // with 16 Wr rows) measured slower at c3: the stream is bandwidth-bound
+    // with 16 Wr rows) measured no faster at c3: the stream is bandwidth-bound
     // with two 8 KiB chunks in flight per wave.
     constexpr int WROWS = EP <= 16 ? 16 : 32;
     constexpr int NBUF = 2;
@@ -390,7 +394,6 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     float* s_logit = reinterpret_cast<float*>(sx_all + 4 * NBUF * 32 * 128);
     int* s_frow = reinterpret_cast<int*>(s_logit + kMfmaRouterRows * 32);
     if (tid < kMaxExperts) s_cnt[tid] = 0;
-    if (tid < E) s_bias[tid] = p.bias != nullptr ? p.bias[tid] : 0.0f;
     const int nblk = (p.T + kMfmaRouterRows - 1) / kMfmaRouterRows;
     const int rl = lane & 31, hi = lane >> 5;
     const int nch = d / 128;  // d % 128 == 0 (launch check)
@@ -416,12 +419,30 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
     const bool chain = nch >= NBUF;
     int grp = blockIdx.x;
     int qb = 0;  // ring buffer of the group's chunk 0
-    // the first group's leading chunks go out before Wr is read, so that the
-    // two memory round trips overlap (the vector-memory counter completes in
-    // order: the wait for the Wr loads below also covers these)
+    // Prologue loads. Where d is a multiple of 512, Wr's rows (1 KiB per
+    // load; wave w takes rows w, w + 4, ...) and the bias go straight to LDS
+    // ahead of the first group's leading X chunks, so waiting for all but
+    // the chunks' loads (the vector-memory counter completes in order) leaves
+    // Wr and the bias staged while the chunks are still in flight. A load
+    // into registers here would be waited for with the counter at zero,
+    // after every chunk. Otherwise the chunks go first and Wr is read through
+    // registers, a second round trip overlapping theirs.
+    const bool wr_dma = d % 512 == 0;
+    const uint32_t sw0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)sw;
+    if (wr_dma) {
+        for (int n = wave; n < E; n += 4)
+            for (int sg = 0; sg < d / 512; ++sg)
+                dma16_lds(p.Wr + (int64_t)n * d + sg * 512 + 8 * lane, sw0 + (uint32_t)(n * wpitch * 2 + sg * 1024));
+        if (wave == 0 && p.bias != nullptr)  // lanes past E load the last entry (unused)
+            dma4_lds(p.bias + min(lane, E - 1),
+                     (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)s_bias);
+    }
 #pragma unroll
     for (int j = 0; j < NBUF; ++j) dma_chunk(grp, j, j);
-    {
+    if (wr_dma) {
+        wait_vmcnt<NBUF * 8>();
+    } else {
+        if (tid < E && p.bias != nullptr) s_bias[tid] = p.bias[tid];
         // Wr's E rows (rows E .. WROWS-1 zero: their columns are unused).
         // Each block starts at its own offset into the rows, so that the
         // blocks, which all read the same few KiB at kernel start, do not
@@ -448,10 +469,11 @@ __global__ __launch_bounds__(256, 1) void router_mfma_kernel(RouterParams p) {
                 }
             }
         }
-        for (int i = tid; i < (WROWS - E) * vpr; i += 256) {
-            const int n = E + i / vpr, c = i % vpr;
-            *reinterpret_cast<uint4*>(sw + n * wpitch + 8 * c) = make_uint4(0, 0, 0, 0);
-        }
+    }
+    if (tid < E && p.bias == nullptr) s_bias[tid] = 0.0f;
+    for (int i = tid; i < (WROWS - E) * (d / 8); i += 256) {
+        const int n = E + i / (d / 8), c = i % (d / 8);
+        *reinterpret_cast<uint4*>(sw + n * wpitch + 8 * c) = make_uint4(0, 0, 0, 0);
     }
     __syncthreads();  // Wr and the bias staged
     const uint4 absm = make_uint4(0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu);
