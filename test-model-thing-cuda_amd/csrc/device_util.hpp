@@ -25,6 +25,26 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
 }
 
+// One wave-wide 16-byte-per-lane load from global memory into LDS at
+// lds_base + 16 * lane (lds_base wave-uniform); M0 is declared clobbered.
+// These loads count on the vector-memory counter like any other, but the
+// compiler does not see them: a compiler-placed wait for a later load waits
+// for them too (the counter completes in order).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16_lds(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "m0", "memory");
+}
+// The same with 4 bytes per lane (to lds_base + 4 * lane).
+__device__ __forceinline__ void dma4_lds(const void* g, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base) : "m0", "memory");
+}
+#pragma clang diagnostic pop
+// LDS address of a pointer into shared memory.
+__device__ __forceinline__ uint32_t lds_u32(const void* p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+
 // The M tiles (TBM slots each) of the experts' slot segments, one expert per
 // lane (E <= 64): lane e holds expert e's first tile and first slot, so a
 // tile's expert is one ballot rather than a walk over the offsets. Built

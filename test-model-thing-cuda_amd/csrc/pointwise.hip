@@ -347,6 +347,123 @@ __global__ __launch_bounds__(kThreads) void router_dw_partial_kernel(RouterDwPar
     }
 }
 
+// Pass 1 on the matrix cores (d a multiple of 256, E a multiple of 4): the
+// same (chunk, 256-column block) grid with experts in blocks of 32, the
+// chunk's partial dWr[e][k] = sum_t dl[t][e] X[t][k] by
+// v_mfma_f32_32x32x16_bf16 with the dlogits as src0 (expert rows) and X^T as
+// src1 (column rows). The fp32 dlogits enter as two bf16 terms, hi =
+// bf16(dl) and lo = bf16(dl - hi): both products with the bf16 X are exact
+// in fp32, and hi + lo is within 2^-18 |dl| of dl, so the partial sums keep
+// fp32 accuracy. Rows arrive in groups of 32 by DMA into three LDS buffers
+// (X as [32][256] bf16 with the 16-byte chunks of odd rows at position
+// XOR 4, the dlogits as [32][32] fp32); k step s of a group pairs lane half
+// h with rows 16s + 2j + h (j = 0..7), so the two half-waves read rows of
+// opposite parity and different banks. Wave w computes columns 64w .. 64w+63
+// of the block (two 32-column tiles). Rows past the chunk enter as zeros.
+constexpr int kDwmExperts = 32, kDwmGroup = 32, kDwmBufs = 3;
+constexpr int kDwmXBytes = kDwmGroup * kDwCols * 2;         // 16 KiB
+constexpr int kDwmBuf = kDwmXBytes + kDwmGroup * kDwmExperts * 4;  // + 4 KiB of dlogits
+constexpr int kDwmLoads = 5;  // DMA loads per wave and group: 4 of X, 1 of dlogits
+typedef float dwm_f32x16 __attribute__((ext_vector_type(16)));
+template <int N>
+__device__ __forceinline__ void dwm_wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__global__ __launch_bounds__(kThreads, 2) void router_dw_mfma_kernel(RouterDwParams p) {
+    __shared__ uint4 s_buf[kDwmBufs * kDwmBuf / 16];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int chunk = blockIdx.x, c0 = blockIdx.y * kDwCols, e0 = blockIdx.z * kDwmExperts;
+    const int E = p.E, d = p.d;
+    const int rows_per = (p.T + p.nchunks - 1) / p.nchunks;  // <= kDwRows
+    const int r0 = chunk * rows_per, r1 = min(p.T, r0 + rows_per);
+    const int nr = max(0, r1 - r0);
+    const int ng = (nr + kDwmGroup - 1) / kDwmGroup;
+    const uint32_t sb = lds_u32(s_buf);
+    const int h = lane >> 5, li = lane & 31;
+    // Group g into buffer b: wave w loads X rows 8w .. 8w + 7 (two 512-byte
+    // rows per load) and the dlogits rows 8w .. 8w + 7 (experts e0 .. e0+31,
+    // 128 bytes per row). Rows past the chunk reload its last row, experts
+    // past E the last four (both masked when read).
+    auto dma_group = [&](int g, int b) {
+        const uint32_t base = sb + (uint32_t)(b * kDwmBuf);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int q = wave * 4 + i, row = 2 * q + (lane >> 5), pos = lane & 31;
+            const int rr = min(g * kDwmGroup + row, nr - 1);
+            dma16_lds(p.X + (int64_t)(r0 + rr) * d + c0 + 8 * (pos ^ ((row & 1) * 4)), base + (uint32_t)q * 1024u);
+        }
+        const int row = 8 * wave + (lane >> 3), e = min(e0 + 4 * (lane & 7), E - 4);
+        const int rr = min(g * kDwmGroup + row, nr - 1);
+        dma16_lds(p.dlogits + (int64_t)(r0 + rr) * E + e, base + (uint32_t)(kDwmXBytes + wave * 1024));
+    };
+    dwm_f32x16 acc[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[c][r] = 0.0f;
+#pragma unroll
+    for (int g = 0; g < kDwmBufs - 1; ++g)
+        if (g < ng) dma_group(g, g);
+    for (int g = 0; g < ng; ++g) {
+        // this wave's loads of group g are in once at most group g + 1's remain
+        if (g + 1 < ng) dwm_wait_vm<kDwmLoads>();
+        else dwm_wait_vm<0>();
+        __syncthreads();  // every wave's loads of group g are in, and group g - 1's buffer is free
+        if (g + kDwmBufs - 1 < ng) dma_group(g + kDwmBufs - 1, (g + kDwmBufs - 1) % kDwmBufs);
+        const uint8_t* xb = reinterpret_cast<const uint8_t*>(s_buf) + (g % kDwmBufs) * kDwmBuf;
+        const float* db = reinterpret_cast<const float*>(xb + kDwmXBytes);
+        const int gr = g * kDwmGroup;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            float dv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int row = 16 * st + 2 * j + h;
+                const float v = db[row * kDwmExperts + li];
+                dv[j] = (gr + row < nr && e0 + li < E) ? v : 0.0f;
+            }
+            uint32_t hw[4], lw[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                hw[q] = pack_bf2(dv[2 * q], dv[2 * q + 1]);
+                lw[q] = pack_bf2(dv[2 * q] - bf_lo(hw[q]), dv[2 * q + 1] - bf_hi(hw[q]));
+            }
+            const bf16x8 dh = __builtin_bit_cast(bf16x8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+            const bf16x8 dlo = __builtin_bit_cast(bf16x8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+#pragma unroll
+            for (int ct = 0; ct < 2; ++ct) {
+                const int col = 64 * wave + 32 * ct + li;
+                uint32_t xv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int row = 16 * st + 2 * j + h;
+                    const int pos = (col >> 3) ^ ((row & 1) * 4);
+                    const uint32_t v = *reinterpret_cast<const uint16_t*>(xb + row * (kDwCols * 2) + pos * 16 + (col & 7) * 2);
+                    xv[j] = gr + row < nr ? v : 0u;
+                }
+                const bf16x8 xf = __builtin_bit_cast(
+                    bf16x8, make_uint4(xv[0] | (xv[1] << 16), xv[2] | (xv[3] << 16), xv[4] | (xv[5] << 16),
+                                       xv[6] | (xv[7] << 16)));
+                acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(dh, xf, acc[ct], 0, 0, 0);
+                acc[ct] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(dlo, xf, acc[ct], 0, 0, 0);
+            }
+        }
+    }
+    // acc[ct][r]: expert e0 + 8 (r / 4) + 4 h + r % 4, column c0 + 64 w + 32 ct + li
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int e = e0 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const int col = c0 + 64 * wave + 32 * ct + li;
+            if (e < E && col < d) p.partial[((int64_t)chunk * E + e) * d + col] = acc[ct][r];
+        }
+}
+static bool router_dw_mfma_fits(const RouterDwParams& p) {
+    return p.d % kDwCols == 0 && p.E % 4 == 0 && p.E >= 4 && p.E <= kMaxExperts;
+}
+
 // Pass 2: dWr[e][k] = sum over chunks in ascending order; each thread owns
 // one output and keeps 16 chunk loads in flight. Block b of the pass covers
 // outputs [b * kThreads, (b + 1) * kThreads).
@@ -658,8 +775,13 @@ int router_dw_chunks_max(int max_tokens, int E, int d) {
 
 hipError_t launch_router_dw(const RouterDwParams& p, hipStream_t s, bool reduce) {
     if (p.nchunks < 1 || (int64_t)p.nchunks * kDwRows < p.T) return hipErrorInvalidValue;
-    dim3 grid1(p.nchunks, (p.d + kDwCols - 1) / kDwCols, (p.E + kDwExperts - 1) / kDwExperts);
-    router_dw_partial_kernel<<<grid1, kThreads, 0, s>>>(p);
+    if (router_dw_mfma_fits(p)) {
+        dim3 grid1(p.nchunks, p.d / kDwCols, (p.E + kDwmExperts - 1) / kDwmExperts);
+        router_dw_mfma_kernel<<<grid1, kThreads, 0, s>>>(p);
+    } else {
+        dim3 grid1(p.nchunks, (p.d + kDwCols - 1) / kDwCols, (p.E + kDwExperts - 1) / kDwExperts);
+        router_dw_partial_kernel<<<grid1, kThreads, 0, s>>>(p);
+    }
     if (reduce) router_dw_reduce_kernel<<<(unsigned)router_dw_reduce_blocks(p), kThreads, 0, s>>>(p);
     return hipGetLastError();
 }

@@ -310,18 +310,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // then softmax_topk): bit for bit what router_kernel writes. Flagged rows
 // are taken in ascending row order, so the block statistics are
 // deterministic.
-// One wave-wide 16-byte-per-lane load from global memory into LDS at
-// lds_base + 16 * lane (lds_base wave-uniform); M0 is declared clobbered.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16_lds(const void* g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_base) : "m0", "memory");
-}
-// The same with 4 bytes per lane (to lds_base + 4 * lane).
-__device__ __forceinline__ void dma4_lds(const void* g, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_base) : "m0", "memory");
-}
-#pragma clang diagnostic pop
 // Sums of N entries per lane over the wave's 64 lanes (xor butterfly,
 // offsets 32 .. 1) as a reduce-scatter: at offset OFF while n > 1 entries are
 // left, the lanes with bit OFF set keep the upper half of their entries,
