@@ -481,11 +481,14 @@ def bench_layernorm(m, X, Wr, Wu, Wd, dY, T, d, E, K, h, aux_c, z_c, steps, warm
     prof = m.profile(reset=True)
     m.set_profiling(False)
     out = {"ms_per_step": round(ms, 4), "tokens_s": round(T / (ms / 1e3), 1)}
-    # The router normalises its rows itself on routed batches ("router" then
-    # carries the LayerNorm forward, and no "norm" launch runs); "scatter"
-    # carries the LayerNorm backward rows; "norm_bwd" is the fixed-order
-    # dGamma/dBeta column sum of the per-workgroup partials.
-    for ph, key in (("router", "router_ln"), ("norm", "norm"), ("scatter", "scatter_ln"), ("norm_bwd", None)):
+    # The router normalises its rows itself on routed batches that the VALU
+    # router takes ("router" then carries the LayerNorm forward, and no
+    # "norm" launch runs); where the matrix-core router applies, the
+    # LayerNorm is its own "norm" launch and "router" is the plain router
+    # over H. "scatter" carries the LayerNorm backward rows; "norm_bwd" is
+    # the fixed-order dGamma/dBeta column sum of the per-workgroup partials.
+    router_key = "router" if prof["norm"][1] > 0 else "router_ln"
+    for ph, key in (("router", router_key), ("norm", "norm"), ("scatter", "scatter_ln"), ("norm_bwd", None)):
         tot, n = prof[ph]
         if n == 0:
             continue

@@ -1008,9 +1008,12 @@ int tmt_moe_forward_ln(tmt_moe* m, void* stream, int32_t T, const uint16_t* S,
     ln.H = m->H; ln.mean = m->ln_mean; ln.rstd = m->ln_rstd;
     // Routed batches: the router normalises its rows itself (one read of S
     // instead of a LayerNorm pass and a read of H); otherwise the LayerNorm
-    // runs first.
+    // runs first. Batches whose logits come from the matrix cores also take
+    // the separate pass: at c3 the LayerNorm pass plus the matrix-core router
+    // over H is faster than the VALU router normalising S itself.
     const LnFuse fuse{S, ln_gamma, ln_beta};
-    const bool fused = !m->padded && ln_in_router(T, m->desc.experts, m->desc.d);
+    const bool fused = !m->padded && ln_in_router(T, m->desc.experts, m->desc.d) &&
+                       !router_mfma_fits(T, m->desc.experts, m->desc.topk, m->desc.d);
     if (!fused) LAUNCH(TMT_MOE_PH_NORM, launch_ln_fwd(ln, s));
     if (m->padded) {
         if ((rc = pad_weights(m, s, Wr, W_up, W_down))) return rc;

@@ -99,6 +99,54 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(LayerNormParams p) {
     }
 }
 
+// Rows of at most NP * 512 elements (16-byte pieces): each lane loads its
+// pieces once into registers, so the normalisation does not read the row a
+// second time after the statistics (one memory round trip per row instead
+// of two). The sums run over the same pieces in the same order as
+// row_stats, so mean, 1/std and H are bit-identical to ln_fwd_kernel<true>.
+template <int NP>
+__global__ __launch_bounds__(kThreads) void ln_fwd_reg_kernel(LayerNormParams p) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= p.T) return;
+    const int d = p.d;
+    const uint16_t* x = p.S + (int64_t)r * p.lds;
+    uint16_t* hrow = p.H + (int64_t)r * p.ldh;
+    uint4 raw[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int k0 = lane * 8 + 512 * i;
+        raw[i] = k0 < d ? *reinterpret_cast<const uint4*>(x + k0) : make_uint4(0, 0, 0, 0);
+    }
+    float ls = 0.0f, lq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        if (lane * 8 + 512 * i < d) {
+            float v[8];
+            unpack8(raw[i], v);
+            ln_accumulate(v, ls, lq);
+        }
+    }
+    float mean, rstd;
+    ln_finish(ls, lq, d, mean, rstd);
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int k0 = lane * 8 + 512 * i;
+        if (k0 >= p.ldh) break;
+        uint4 hv = make_uint4(0, 0, 0, 0);  // columns [d, ldh): zeros
+        if (k0 < d) {
+            float v[8];
+            unpack8(raw[i], v);
+            hv = ln_apply8(v, mean, rstd, p.gamma, p.beta, k0);
+        }
+        *reinterpret_cast<uint4*>(hrow + k0) = hv;
+    }
+    if (lane == 0) {
+        p.mean[r] = mean;
+        p.rstd[r] = rstd;
+    }
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void ln_bwd_rows_kernel(LayerNormParams p) {
     const int lane = threadIdx.x & 63;
@@ -303,8 +351,18 @@ bool ln_vec(const LayerNormParams& p, bool fwd) {
 hipError_t launch_ln_fwd(const LayerNormParams& p, hipStream_t s) {
     if (p.T <= 0) return hipSuccess;
     if (p.d < 1 || p.lds < p.d || p.ldh < p.d) return hipErrorInvalidValue;
-    if (ln_vec(p, true)) ln_fwd_kernel<true><<<(p.T + 3) / 4, kThreads, 0, s>>>(p);
-    else ln_fwd_kernel<false><<<(p.T + 3) / 4, kThreads, 0, s>>>(p);
+    const unsigned grid = (unsigned)((p.T + 3) / 4);
+    if (!ln_vec(p, true)) {
+        ln_fwd_kernel<false><<<grid, kThreads, 0, s>>>(p);
+    } else {
+        switch ((p.ldh + 511) / 512) {  // 16-byte pieces per lane, H's padded columns included
+            case 1: ln_fwd_reg_kernel<1><<<grid, kThreads, 0, s>>>(p); break;
+            case 2: ln_fwd_reg_kernel<2><<<grid, kThreads, 0, s>>>(p); break;
+            case 3: ln_fwd_reg_kernel<3><<<grid, kThreads, 0, s>>>(p); break;
+            case 4: ln_fwd_reg_kernel<4><<<grid, kThreads, 0, s>>>(p); break;
+            default: ln_fwd_kernel<true><<<grid, kThreads, 0, s>>>(p); break;
+        }
+    }
     return hipGetLastError();
 }
 

@@ -281,10 +281,10 @@ def test_standalone_layernorm_against_oracle(orc, T, d):
 
 def test_c3_full_size_layernorm_block(orc):
     """At the c3 size: H bit-exact against the oracle LayerNorm, routing
-    bit-exact against the oracle router on H, and the fused block equal to
-    the plain block on H: the same picks (the fused router's canonical
-    logits against the plain block's matrix-core logits, which differ only
-    in rounding), Y and the weight gradients within 1e-3 relative L2, and the
+    bit-exact against the oracle router on H, and the LayerNorm-fronted block
+    equal to the plain block on H (at this batch size both route H on the
+    matrix cores, the LayerNorm running as its own launch first): the same
+    picks, Y and the weight gradients within 1e-3 relative L2, and the
     LayerNorm backward against the oracle's."""
     cfg = CONFIGS["c3"]
     T, d, E, K, h = (cfg[k] for k in ("T", "d", "E", "K", "h"))
@@ -352,6 +352,7 @@ def test_c3_full_size_layernorm_block(orc):
     (2100, 2048, 12, 0),  # the widest fused row (4 chunks of 512 per lane)
     (40, 256, 4, 1),      # decode-sized batch: separate LayerNorm launch
     (300, 2560, 4, 1),    # d > 2048: separate LayerNorm launch
+    (32768, 256, 4, 1),   # one 128-row group per CU: separate LayerNorm launch, matrix-core router over H
 ])
 def test_layernorm_forward_placement(T, d, E, norm_launches):
     """Which kernel runs the LayerNorm forward: the phase profile counts the
