@@ -167,3 +167,26 @@ def test_width_identical_experts_equal_dense(orc):
     # compares the gradient below the layer, where that term enters too)
     r2 = oracle_case(orc, moe, 2, 0, backward=True)
     assert rel_l2(g2["dX"], r2["dX"]) <= REL_L2
+
+
+def test_router_weight_gradient_paths_agree():
+    """The router weight gradient's two first passes on one problem: width
+    1024 runs the matrix-core pass (dlogits entering as hi + lo bf16 terms),
+    width 960 (the same problem without the 64 zero columns) the VALU pass.
+    Routing and dlogits match (the zero columns add exact zeros), and both
+    passes keep fp32 accuracy, so dWr agrees far inside the block's 1e-2
+    bar. A matrix-core pass without the lo term would leave a 2^-9 relative
+    error per dlogit, about 2e-3 relative L2 on dWr here."""
+    T, d, dp, E, K, h = 4096, 960, 1024, 16, 4, 256
+    say(f"router dW paths: T={T} d={d} (VALU pass) against {dp} (matrix-core pass), E={E} K={K} h={h}")
+    case = dict(make_case(T, d, E, K, h, seed=321), bias=None)
+    g = run_gpu(case, K, h, backward=True, aux=0.1, z=1e-3)
+    padded = {"X": _pad(case["X"], (T, dp)), "Wr": _pad(case["Wr"], (E, dp)),
+              "W_up": _pad(case["W_up"], (E, h, dp)), "W_down": _pad(case["W_down"], (E, dp, h)),
+              "dY": _pad(case["dY"], (T, dp)), "bias": None}
+    q = run_gpu(padded, K, h, backward=True, aux=0.1, z=1e-3)
+    assert np.array_equal(g["idx"], q["idx"]), "routing differs"
+    err = rel_l2(g["dWr"], q["dWr"][:, :d])
+    say(f"  dWr rel-L2 between the passes {err:.2e}")
+    assert err <= 1e-4
+    assert not np.any(q["dWr"][:, d:]), "zero columns of X gave nonzero dWr"
